@@ -1,0 +1,348 @@
+// Memory-bound small operations: elementwise, RMS and L2 norms, rotary
+// embeddings, the Q8 cache store, the causal convolution, argmax and the
+// synthetic-weight generators.  Each reads and writes its operands once.
+#include "device_util.h"
+#include "quant_math.h"
+#include "runtime.h"
+
+static inline unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
+
+// ---------------------------------------------------------------- elementwise
+
+__global__ void k_fill_zero(float *x, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = 0.0f;
+}
+
+// x += y (dwim gpu/cpu.rs:151-155)
+__global__ void k_add(float *__restrict__ x, const float *__restrict__ y, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] += y[i];
+}
+
+// g = g * sigmoid(g) * u (gpu/cpu.rs:238-242)
+__global__ void k_silu_mul(float *__restrict__ g, const float *__restrict__ u, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        float v = g[i];
+        g[i] = v * sigmoidf_(v) * u[i];
+    }
+}
+
+// x *= sigmoid(g) (gpu/cpu.rs:244-248)
+__global__ void k_sigmoid_mul(float *__restrict__ x, const float *__restrict__ g, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] *= sigmoidf_(g[i]);
+}
+
+hipError_t launch_fill_zero(hipStream_t s, float *x, size_t n) {
+    k_fill_zero<<<blocks_for(n, 256), 256, 0, s>>>(x, n);
+    return hipGetLastError();
+}
+hipError_t launch_add(hipStream_t s, float *x, const float *y, size_t n) {
+    k_add<<<blocks_for(n, 256), 256, 0, s>>>(x, y, n);
+    return hipGetLastError();
+}
+hipError_t launch_silu_mul(hipStream_t s, float *g, const float *u, size_t n) {
+    k_silu_mul<<<blocks_for(n, 256), 256, 0, s>>>(g, u, n);
+    return hipGetLastError();
+}
+hipError_t launch_sigmoid_mul(hipStream_t s, float *x, const float *g, size_t n) {
+    k_sigmoid_mul<<<blocks_for(n, 256), 256, 0, s>>>(x, g, n);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- norms
+
+// out[row] = x[row] * (1/sqrt(mean(x^2) + eps) * w), one block per row
+// (gpu/cpu.rs:157-166; out may be x).
+__global__ void __launch_bounds__(256) k_rmsnorm(float *out, const float *x, const float *__restrict__ w,
+                                                 size_t dim, float eps) {
+    __shared__ float red[4];
+    const float *xr = x + (size_t)blockIdx.x * dim;
+    float *orow = out + (size_t)blockIdx.x * dim;
+    float ss = 0.0f;
+    for (size_t i = threadIdx.x; i < dim; i += 256) ss += xr[i] * xr[i];
+    ss = block_sum<256>(ss, red);
+    float scale = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (size_t i = threadIdx.x; i < dim; i += 256) orow[i] = xr[i] * (scale * w[i]);
+}
+
+// Rows of up to 256: a wave per row.
+__global__ void __launch_bounds__(256) k_rmsnorm_small(float *out, const float *x, const float *__restrict__ w,
+                                                       size_t rows, size_t dim, float eps) {
+    size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + row * dim;
+    float *orow = out + row * dim;
+    float v[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        size_t i = lane + 64 * k;
+        v[k] = i < dim ? xr[i] : 0.0f;
+        ss += v[k] * v[k];
+    }
+    ss = group_sum<64>(ss);
+    float scale = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        size_t i = lane + 64 * k;
+        if (i < dim) orow[i] = v[k] * (scale * w[i]);
+    }
+}
+
+hipError_t launch_rmsnorm(hipStream_t s, float *out, const float *x, const float *w, size_t rows, size_t dim,
+                          float eps) {
+    if (dim <= 256)
+        k_rmsnorm_small<<<blocks_for(rows, 4), 256, 0, s>>>(out, x, w, rows, dim, eps);
+    else
+        k_rmsnorm<<<(unsigned)rows, 256, 0, s>>>(out, x, w, dim, eps);
+    return hipGetLastError();
+}
+
+// x[row] *= 1/sqrt(sum(x^2) + eps) (gpu/cpu.rs:168-175), a wave per row of up
+// to 256, a block per longer row.
+__global__ void __launch_bounds__(256) k_l2norm_small(float *x, size_t rows, size_t dim, float eps) {
+    size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    float *xr = x + row * dim;
+    float v[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        size_t i = lane + 64 * k;
+        v[k] = i < dim ? xr[i] : 0.0f;
+        ss += v[k] * v[k];
+    }
+    ss = group_sum<64>(ss);
+    float scale = 1.0f / sqrtf(ss + eps);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        size_t i = lane + 64 * k;
+        if (i < dim) xr[i] = v[k] * scale;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_l2norm(float *x, size_t dim, float eps) {
+    __shared__ float red[4];
+    float *xr = x + (size_t)blockIdx.x * dim;
+    float ss = 0.0f;
+    for (size_t i = threadIdx.x; i < dim; i += 256) ss += xr[i] * xr[i];
+    ss = block_sum<256>(ss, red);
+    float scale = 1.0f / sqrtf(ss + eps);
+    for (size_t i = threadIdx.x; i < dim; i += 256) xr[i] *= scale;
+}
+
+hipError_t launch_l2norm(hipStream_t s, float *x, size_t rows, size_t dim, float eps) {
+    if (dim <= 256)
+        k_l2norm_small<<<blocks_for(rows, 4), 256, 0, s>>>(x, rows, dim, eps);
+    else
+        k_l2norm<<<(unsigned)rows, 256, 0, s>>>(x, dim, eps);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- rope
+
+// One thread per rotated pair (gpu/cpu.rs:177-200).
+__global__ void k_rope(float *x, const float *__restrict__ table, size_t n, size_t pos, size_t n_heads,
+                       size_t head_dim, size_t rot_dim) {
+    size_t half = rot_dim / 2;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * n_heads * half) return;
+    size_t p = i % half, head = (i / half) % n_heads, t = i / (half * n_heads);
+    const float *ang = table + (pos + t) * rot_dim + 2 * p;
+    float c = ang[0], sn = ang[1];
+    float *h = x + (t * n_heads + head) * head_dim;
+    float a = h[p], b = h[p + half];
+    h[p] = a * c - b * sn;
+    h[p + half] = b * c + a * sn;
+}
+
+hipError_t launch_rope(hipStream_t s, float *x, const float *table, size_t n, size_t pos, size_t n_heads,
+                       size_t head_dim, size_t rot_dim) {
+    size_t pairs = n * n_heads * (rot_dim / 2);
+    k_rope<<<blocks_for(pairs, 256), 256, 0, s>>>(x, table, n, pos, n_heads, head_dim, rot_dim);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- cache store
+
+// Half a wave per block of 32: the block's largest magnitude by shuffles,
+// then each lane its own value (gpu/quant.rs:161-180, bit for bit).
+__global__ void __launch_bounds__(256) k_store(int8_t *__restrict__ cq, uint16_t *__restrict__ cs,
+                                               const float *__restrict__ src, size_t blocks) {
+    size_t b = ((size_t)blockIdx.x * 256 + threadIdx.x) >> 5;
+    int l = threadIdx.x & 31;
+    bool live = b < blocks;
+    float x = live ? src[b * 32 + l] : 0.0f;
+    float amax = fabsf(x);
+#pragma unroll
+    for (int m = 16; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    if (!live) return;
+    uint16_t bits = dq::block_scale(amax);
+    float d = dq::from_f16(bits);
+    cq[b * 32 + l] = d > 0.0f ? dq::quantize_one(x, d) : (int8_t)0;
+    if (l == 0) cs[b] = bits;
+}
+
+hipError_t launch_store(hipStream_t s, int8_t *cq, uint16_t *cs, const float *src, size_t blocks) {
+    k_store<<<blocks_for(blocks * 32, 256), 256, 0, s>>>(cq, cs, src, blocks);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- conv
+
+// One thread per channel, the 4-tap window carried in registers over the
+// batch's tokens (gpu/cpu.rs:250-296).
+__global__ void k_conv(float *__restrict__ q, float *__restrict__ k, float *__restrict__ v,
+                       float *__restrict__ state_out, const float *__restrict__ x,
+                       const float *__restrict__ state, const float *__restrict__ w, size_t n, size_t qd,
+                       size_t kd, size_t vd) {
+    size_t ch = qd + kd + vd;
+    size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= ch) return;
+    float w0 = w[c * 4], w1 = w[c * 4 + 1], w2 = w[c * 4 + 2], w3 = w[c * 4 + 3];
+    float s0 = state[c], s1 = state[ch + c], s2 = state[2 * ch + c];
+    float *dst;
+    size_t stride, col;
+    if (c < qd) { dst = q; stride = qd; col = c; }
+    else if (c < qd + kd) { dst = k; stride = kd; col = c - qd; }
+    else { dst = v; stride = vd; col = c - qd - kd; }
+    for (size_t t = 0; t < n; t++) {
+        float xin = x[t * ch + c];
+        float acc = 0.0f;
+        acc += w0 * s0;
+        acc += w1 * s1;
+        acc += w2 * s2;
+        acc += w3 * xin;
+        dst[t * stride + col] = acc * sigmoidf_(acc);
+        s0 = s1;
+        s1 = s2;
+        s2 = xin;
+    }
+    state_out[c] = s0;
+    state_out[ch + c] = s1;
+    state_out[2 * ch + c] = s2;
+}
+
+hipError_t launch_conv(hipStream_t s, float *q, float *k, float *v, float *state_out, const float *x,
+                       const float *state, const float *w, size_t n, size_t qd, size_t kd, size_t vd) {
+    size_t ch = qd + kd + vd;
+    k_conv<<<blocks_for(ch, 256), 256, 0, s>>>(q, k, v, state_out, x, state, w, n, qd, kd, vd);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- argmax
+
+// One block per row: each thread scans its stride in increasing order keeping
+// the first maximum, then the block keeps the smallest index of the largest
+// value (qwen35::argmax's strict `>`).
+__global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ logits, size_t cols,
+                                                 uint32_t *__restrict__ out) {
+    __shared__ float bv[16];
+    __shared__ uint32_t bi[16];
+    const float *row = logits + (size_t)blockIdx.x * cols;
+    float best = -INFINITY;
+    uint32_t idx = 0xffffffffu;
+    for (size_t i = threadIdx.x; i < cols; i += 1024) {
+        float v = row[i];
+        if (idx == 0xffffffffu || v > best) {
+            best = v;
+            idx = (uint32_t)i;
+        }
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+        float ov = __shfl_xor(best, m, 64);
+        uint32_t oi = __shfl_xor(idx, m, 64);
+        bool take = oi != 0xffffffffu && (idx == 0xffffffffu || ov > best || (ov == best && oi < idx));
+        if (take) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        bv[wave] = best;
+        bi[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        uint32_t id = bi[0];
+        for (int i = 1; i < 16; i++) {
+            if (bi[i] == 0xffffffffu) continue;
+            if (id == 0xffffffffu || bv[i] > b || (bv[i] == b && bi[i] < id)) {
+                b = bv[i];
+                id = bi[i];
+            }
+        }
+        out[blockIdx.x] = id == 0xffffffffu ? 0u : id;
+    }
+}
+
+hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols, uint32_t *out) {
+    k_argmax<<<(unsigned)rows, 1024, 0, s>>>(logits, cols, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- synthetic weights
+
+// One thread per block of 256 weights: the stream's values for the block,
+// quantized as the host quantizers do (quant_math.h).
+__global__ void k_synthetic_q4_k(uint8_t *__restrict__ qs, uint8_t *__restrict__ meta, size_t blocks,
+                                 uint64_t seed, float c) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    float x[256];
+    for (int i = 0; i < 256; i++) x[i] = dq::synthetic(seed, b * 256 + i, c);
+    uint8_t blk[144];
+    dq::quantize_q4_k_block(x, blk);
+    for (int i = 0; i < 16; i++) meta[b * 16 + i] = blk[i];
+    for (int i = 0; i < 128; i++) qs[b * 128 + i] = blk[16 + i];
+}
+
+__global__ void k_synthetic_q6_k(uint8_t *__restrict__ ql, uint8_t *__restrict__ qh, int8_t *__restrict__ sc,
+                                 uint16_t *__restrict__ d, size_t blocks, uint64_t seed, float c) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    float x[256];
+    for (int i = 0; i < 256; i++) x[i] = dq::synthetic(seed, b * 256 + i, c);
+    uint8_t blk[210];
+    dq::quantize_q6_k_block(x, blk);
+    for (int i = 0; i < 128; i++) ql[b * 128 + i] = blk[i];
+    for (int i = 0; i < 64; i++) qh[b * 64 + i] = blk[128 + i];
+    for (int i = 0; i < 16; i++) sc[b * 16 + i] = (int8_t)blk[192 + i];
+    d[b] = (uint16_t)(blk[208] | (blk[209] << 8));
+}
+
+// bf16 by rounding to nearest, ties to even (gpu/float.rs:32-36).
+__global__ void k_synthetic_bf16(uint16_t *__restrict__ q, size_t n, uint64_t seed, float c) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t b = dq::bits_of(dq::synthetic(seed, i, c));
+    q[i] = (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+hipError_t launch_synthetic_q4_k(hipStream_t s, uint8_t *qs, uint8_t *meta, size_t rows, size_t cols,
+                                 uint64_t seed, float c) {
+    size_t blocks = rows * (cols / 256);
+    k_synthetic_q4_k<<<blocks_for(blocks, 128), 128, 0, s>>>(qs, meta, blocks, seed, c);
+    return hipGetLastError();
+}
+
+hipError_t launch_synthetic_q6_k(hipStream_t s, uint8_t *ql, uint8_t *qh, int8_t *sc, uint16_t *d, size_t rows,
+                                 size_t cols, uint64_t seed, float c) {
+    size_t blocks = rows * (cols / 256);
+    k_synthetic_q6_k<<<blocks_for(blocks, 128), 128, 0, s>>>(ql, qh, sc, d, blocks, seed, c);
+    return hipGetLastError();
+}
+
+hipError_t launch_synthetic_bf16(hipStream_t s, uint16_t *q, size_t rows, size_t cols, uint64_t seed, float c) {
+    size_t n = rows * cols;
+    k_synthetic_bf16<<<blocks_for(n, 256), 256, 0, s>>>(q, n, seed, c);
+    return hipGetLastError();
+}

@@ -1,0 +1,319 @@
+// Dequantizing matrix-vector products for decode and small batches:
+// out[t][r] = w[r] · x[t] (dwim gpu/cpu.rs:110-149, Device::matmul), for every
+// weight format, with f32 activations and f32 accumulation (no MFMA: at a
+// few tokens the product is bound by HBM, not arithmetic).
+//
+// Work split (gfx950, wave64): a wave's 64 lanes form 64/LPR groups of LPR
+// lanes; each group owns R consecutive rows and walks their columns in
+// 16-byte chunks of weights, lane l of the group taking chunks l, l+LPR, ...
+// All lanes of a wave load consecutive 16-byte chunks of one row per
+// instruction (coalesced, 16 B per lane), and every activation chunk a lane
+// loads serves its R rows.  The group's partial sums meet by xor shuffles
+// and one lane writes each result.  LPR is picked per shape so that the
+// row's chunks divide evenly among the group's lanes.
+//
+// Chunk semantics per format (weights per 16-byte chunk of the row's main
+// stream):
+//   Q4_K  32 weights: bytes 16h..16h+15 of 32-byte group g of a block's qs =
+//         sub-block 2g (low nibbles) and 2g+1 (high nibbles) at positions
+//         16h..16h+15; out += d1·Σq·x − m1·Σx per sub-block, the min folded out.
+//   Q6_K  64 weights (one chunk = 16 B of ql for k = 0/2, 16 B for k = 1/3 and
+//         16 B of qh): positions l0..l0+15 of the four 32-weight runs of one
+//         half of a block; out += (d·sc)·Σq·x per run of 16.
+//   Q4_0  one block of 32: out += d·Σ(q−8)·x.
+//   Q8_0  half a block (16 weights): out += d·Σq·x.
+//   BF16  8 weights: out += Σw·x.
+#include "device_util.h"
+#include "quant_math.h"
+#include "runtime.h"
+
+namespace {
+
+constexpr int kThreads = 256;  // 4 waves per block
+
+DEV float lo_nib(uint32_t v, int byte) { return (float)((v >> (8 * byte)) & 0xfu); }
+DEV float hi_nib(uint32_t v, int byte) { return (float)((v >> (8 * byte + 4)) & 0xfu); }
+
+DEV void load16f(const float *p, float *dst) {
+    const float4 *p4 = (const float4 *)p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float4 v = p4[i];
+        dst[4 * i] = v.x;
+        dst[4 * i + 1] = v.y;
+        dst[4 * i + 2] = v.z;
+        dst[4 * i + 3] = v.w;
+    }
+}
+
+DEV uint32_t word_of(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+// byte k (0..11) of the 12 packed Q4_K scale bytes (meta words y, z, w)
+DEV int meta_byte(const uint4 &m, int k) {
+    uint32_t w = k < 4 ? m.y : (k < 8 ? m.z : m.w);
+    return (int)((w >> (8 * (k & 3))) & 0xffu);
+}
+
+DEV void q4k_sm(const uint4 &m, int j, int &sc, int &mn) {
+    if (j < 4) {
+        sc = meta_byte(m, j) & 63;
+        mn = meta_byte(m, j + 4) & 63;
+    } else {
+        sc = (meta_byte(m, j + 4) & 0xf) | ((meta_byte(m, j - 4) >> 6) << 4);
+        mn = (meta_byte(m, j + 4) >> 4) | ((meta_byte(m, j) >> 6) << 4);
+    }
+}
+
+struct Weights {
+    const void *q, *s, *s2, *s3;
+    size_t rows, cols;
+};
+
+// ---- per-format chunk counts and dot products ----
+
+template <int FMT>
+struct Fmt;
+
+template <>
+struct Fmt<DWIM_Q4_K> {
+    static constexpr int kPerChunk = 32;
+    __host__ __device__ static size_t chunks(size_t cols) { return cols / 256 * 8; }
+    // partial for row r, chunk c, activations x (one token)
+    DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
+        size_t nb = w.cols / 256;
+        size_t b = c >> 3;
+        int j8 = (int)(c & 7), g = j8 >> 1, h = j8 & 1;
+        const uint4 q = ((const uint4 *)w.q)[(r * nb + b) * 8 + j8];
+        const uint4 m = ((const uint4 *)w.s)[r * nb + b];
+        float xl[16], xh[16];
+        const float *xb = x + b * 256 + 64 * g + 16 * h;
+        load16f(xb, xl);
+        load16f(xb + 32, xh);
+        float sl = 0.0f, sh = 0.0f, xsl = 0.0f, xsh = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            uint32_t v = word_of(q, i >> 2);
+            sl += lo_nib(v, i & 3) * xl[i];
+            sh += hi_nib(v, i & 3) * xh[i];
+            xsl += xl[i];
+            xsh += xh[i];
+        }
+        float d = dq::from_f16((uint16_t)(m.x & 0xffffu)), dmin = dq::from_f16((uint16_t)(m.x >> 16));
+        int sc1, m1, sc2, m2;
+        q4k_sm(m, 2 * g, sc1, m1);
+        q4k_sm(m, 2 * g + 1, sc2, m2);
+        return (d * (float)sc1) * sl - (dmin * (float)m1) * xsl + (d * (float)sc2) * sh - (dmin * (float)m2) * xsh;
+    }
+};
+
+template <>
+struct Fmt<DWIM_Q6_K> {
+    static constexpr int kPerChunk = 64;
+    __host__ __device__ static size_t chunks(size_t cols) { return cols / 256 * 4; }
+    DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
+        size_t nb = w.cols / 256;
+        size_t b = c >> 2;
+        int hh = (int)((c >> 1) & 1), l0 = (int)(c & 1) * 16;
+        size_t blk = r * nb + b;
+        const uint8_t *ql = (const uint8_t *)w.q + blk * 128 + 64 * hh;
+        const uint4 a = *(const uint4 *)(ql + l0);       // k = 0 (low), k = 2 (high)
+        const uint4 bq = *(const uint4 *)(ql + 32 + l0); // k = 1 (low), k = 3 (high)
+        const uint4 hq = *(const uint4 *)((const uint8_t *)w.s + blk * 64 + 32 * hh + l0);
+        const int8_t *sc = (const int8_t *)w.s2 + blk * 16 + 8 * hh + (l0 >> 4);
+        float d = dq::from_f16(((const uint16_t *)w.s3)[blk]);
+        const float *xb = x + b * 256 + 128 * hh + l0;
+        float total = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float xv[16];
+            load16f(xb + 32 * k, xv);
+            const uint4 &lowsrc = (k & 1) ? bq : a;
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                uint32_t lw = word_of(lowsrc, i >> 2), hw = word_of(hq, i >> 2);
+                int low = (int)((lw >> (8 * (i & 3) + 4 * (k >> 1))) & 0xfu);
+                int high = (int)((hw >> (8 * (i & 3) + 2 * k)) & 3u);
+                s += (float)((low | (high << 4)) - 32) * xv[i];
+            }
+            total += (d * (float)sc[2 * k]) * s;
+        }
+        return total;
+    }
+};
+
+template <>
+struct Fmt<DWIM_Q4_0> {
+    static constexpr int kPerChunk = 32;
+    __host__ __device__ static size_t chunks(size_t cols) { return cols / 32; }
+    DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
+        size_t nb = w.cols / 32;
+        const uint4 q = ((const uint4 *)w.q)[r * nb + c];
+        float d = dq::from_f16(((const uint16_t *)w.s)[r * nb + c]);
+        float xl[16], xh[16];
+        load16f(x + c * 32, xl);
+        load16f(x + c * 32 + 16, xh);
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            uint32_t v = word_of(q, i >> 2);
+            s += (lo_nib(v, i & 3) - 8.0f) * xl[i] + (hi_nib(v, i & 3) - 8.0f) * xh[i];
+        }
+        return d * s;
+    }
+};
+
+template <>
+struct Fmt<DWIM_Q8_0> {
+    static constexpr int kPerChunk = 16;
+    __host__ __device__ static size_t chunks(size_t cols) { return cols / 16; }
+    DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
+        const uint4 q = ((const uint4 *)w.q)[r * (w.cols / 16) + c];
+        float d = dq::from_f16(((const uint16_t *)w.s)[r * (w.cols / 32) + (c >> 1)]);
+        float xv[16];
+        load16f(x + c * 16, xv);
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            int v = (int)(int8_t)((word_of(q, i >> 2) >> (8 * (i & 3))) & 0xffu);
+            s += (float)v * xv[i];
+        }
+        return d * s;
+    }
+};
+
+template <>
+struct Fmt<DWIM_BF16> {
+    static constexpr int kPerChunk = 8;
+    __host__ __device__ static size_t chunks(size_t cols) { return cols / 8; }
+    DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
+        const uint4 q = ((const uint4 *)w.q)[r * (w.cols / 8) + c];
+        const float4 x0 = ((const float4 *)(x + c * 8))[0];
+        const float4 x1 = ((const float4 *)(x + c * 8))[1];
+        float s = 0.0f;
+        s += dq::bf16_to_f32((uint16_t)(q.x & 0xffff)) * x0.x;
+        s += dq::bf16_to_f32((uint16_t)(q.x >> 16)) * x0.y;
+        s += dq::bf16_to_f32((uint16_t)(q.y & 0xffff)) * x0.z;
+        s += dq::bf16_to_f32((uint16_t)(q.y >> 16)) * x0.w;
+        s += dq::bf16_to_f32((uint16_t)(q.z & 0xffff)) * x1.x;
+        s += dq::bf16_to_f32((uint16_t)(q.z >> 16)) * x1.y;
+        s += dq::bf16_to_f32((uint16_t)(q.w & 0xffff)) * x1.z;
+        s += dq::bf16_to_f32((uint16_t)(q.w >> 16)) * x1.w;
+        return s;
+    }
+};
+
+// out[t][r] (+)= w[r]·x[t] for T tokens from `x`, rows in groups of R per LPR lanes.
+template <int FMT, int R, int T, int LPR>
+__global__ void __launch_bounds__(kThreads) k_matvec(Weights w, const float *__restrict__ x, float *out, size_t n_out_stride,
+                                                     int add) {
+    const int lane = threadIdx.x & 63;
+    const size_t group = ((size_t)blockIdx.x * kThreads + threadIdx.x) / LPR;
+    const int sl = lane & (LPR - 1);
+    const size_t row0 = group * R;
+    if (row0 >= w.rows) return;  // whole groups only: shuffles stay within a group
+    const size_t cpr = Fmt<FMT>::chunks(w.cols);
+    float acc[R][T];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int t = 0; t < T; t++) acc[r][t] = 0.0f;
+    for (size_t c = sl; c < cpr; c += LPR) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            size_t row = row0 + r < w.rows ? row0 + r : w.rows - 1;
+#pragma unroll
+            for (int t = 0; t < T; t++) acc[r][t] += Fmt<FMT>::dot(w, row, c, x + t * w.cols);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            float v = group_sum<LPR>(acc[r][t]);
+            if (sl == 0 && row0 + r < w.rows) {
+                float *o = out + t * n_out_stride + row0 + r;
+                *o = add ? *o + v : v;
+            }
+        }
+}
+
+template <int FMT, int R, int T>
+hipError_t launch_lpr(hipStream_t s, const Weights &w, const float *x, float *out, int add, int lpr) {
+    size_t groups = (w.rows + R - 1) / R;
+    unsigned blocks = (unsigned)((groups * lpr + kThreads - 1) / kThreads);
+    switch (lpr) {
+    case 64: k_matvec<FMT, R, T, 64><<<blocks, kThreads, 0, s>>>(w, x, out, w.rows, add); break;
+    case 32: k_matvec<FMT, R, T, 32><<<blocks, kThreads, 0, s>>>(w, x, out, w.rows, add); break;
+    case 16: k_matvec<FMT, R, T, 16><<<blocks, kThreads, 0, s>>>(w, x, out, w.rows, add); break;
+    case 8: k_matvec<FMT, R, T, 8><<<blocks, kThreads, 0, s>>>(w, x, out, w.rows, add); break;
+    default: k_matvec<FMT, R, T, 4><<<blocks, kThreads, 0, s>>>(w, x, out, w.rows, add); break;
+    }
+    return hipGetLastError();
+}
+
+// Lanes per row group: the largest of 64..4 that splits the row's chunks
+// evenly, else the one that wastes the fewest lane-iterations.
+int pick_lpr(size_t cpr) {
+    int best = 4;
+    double best_eff = 0.0;
+    for (int l = 64; l >= 4; l >>= 1) {
+        size_t iters = (cpr + l - 1) / l;
+        double eff = (double)cpr / (double)(iters * l);
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best = l;
+        }
+    }
+    return best;
+}
+
+template <int FMT>
+hipError_t launch_fmt(hipStream_t s, const Weights &w, const float *x, float *out, size_t n, int add) {
+    int lpr = pick_lpr(Fmt<FMT>::chunks(w.cols));
+    // Few rows: one row per group so that the launch still fills the GPU.
+    bool many_rows = w.rows * 64 / lpr >= 4096 * 4;
+    size_t t = 0;
+    hipError_t e = hipSuccess;
+    while (t < n && e == hipSuccess) {
+        size_t left = n - t;
+        const float *xt = x + t * w.cols;
+        float *ot = out + t * w.rows;
+        if (left >= 4) {
+            e = launch_lpr<FMT, 2, 4>(s, w, xt, ot, add, lpr);
+            t += 4;
+        } else if (left == 3) {
+            e = launch_lpr<FMT, 2, 3>(s, w, xt, ot, add, lpr);
+            t += 3;
+        } else if (left == 2) {
+            e = launch_lpr<FMT, 2, 2>(s, w, xt, ot, add, lpr);
+            t += 2;
+        } else {
+            e = many_rows ? launch_lpr<FMT, 4, 1>(s, w, xt, ot, add, lpr)
+                          : launch_lpr<FMT, 1, 1>(s, w, xt, ot, add, lpr);
+            t += 1;
+        }
+    }
+    return e;
+}
+
+}  // namespace
+
+hipError_t launch_matvec(hipStream_t s, const dwim_weight *wt, float *out, const float *x, size_t n, int add) {
+    Weights w{wt->q, wt->s, wt->s2, wt->s3, wt->rows, wt->cols};
+    switch (wt->fmt) {
+    case DWIM_Q4_K: return launch_fmt<DWIM_Q4_K>(s, w, x, out, n, add);
+    case DWIM_Q6_K: return launch_fmt<DWIM_Q6_K>(s, w, x, out, n, add);
+    case DWIM_Q4_0: return launch_fmt<DWIM_Q4_0>(s, w, x, out, n, add);
+    case DWIM_Q8_0: return launch_fmt<DWIM_Q8_0>(s, w, x, out, n, add);
+    default: return launch_fmt<DWIM_BF16>(s, w, x, out, n, add);
+    }
+}
+
+hipError_t launch_swiglu(hipStream_t s, const dwim_weight *gate, const dwim_weight *up, float *out, float *scratch,
+                         const float *x, size_t n) {
+    hipError_t e = launch_matvec(s, gate, out, x, n, 0);
+    if (e == hipSuccess) e = launch_matvec(s, up, scratch, x, n, 0);
+    if (e == hipSuccess) e = launch_silu_mul(s, out, scratch, n * gate->rows);
+    return e;
+}

@@ -1,0 +1,98 @@
+// Internal structures of the HIP backend and the kernel launchers the C ABI
+// calls.  Everything here is gfx950 (CDNA4): 64-lane wavefronts, 160 KB of LDS
+// per CU, 256 CUs in 8 XCDs.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "dwim_hip.h"
+
+struct dwim_dev {
+    int index = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+    int cus = 256;
+    // Device scratch the library owns: attention split-K partials, argmax
+    // results.  Grown on demand, freed with the device.
+    float *partials = nullptr;
+    size_t partials_cap = 0;  // floats
+    uint32_t *argmax_buf = nullptr;
+    size_t argmax_cap = 0;
+};
+
+struct dwim_buf {
+    dwim_dev *dev;
+    float *data;
+    size_t len, cap;
+};
+
+// Device layouts of a weight matrix (`upload` re-lays the host formats):
+//   BF16  q: u16 [rows][cols]
+//   Q4_0  q: u8 [rows][cols/2] (the reference's nibble order), s: u16 [rows][cols/32]
+//   Q8_0  q: i8 [rows][cols],                                    s: u16 [rows][cols/32]
+//   Q4_K  q: qs u8 [rows][nb][128], s: meta u8 [rows][nb][16] = d, dmin, scales[12]
+//   Q6_K  q: ql u8 [rows][nb][128], s: qh u8 [rows][nb][64], s2: i8 scales [rows][nb][16],
+//         s3: f16 d [rows][nb]
+// with nb = cols/256 blocks per row.  Splitting each K-quant block into
+// streams keeps every lane's 16-byte load aligned and each stream contiguous.
+struct dwim_weight {
+    dwim_dev *dev;
+    int fmt;
+    size_t rows, cols;
+    void *q = nullptr, *s = nullptr, *s2 = nullptr, *s3 = nullptr;
+};
+
+struct dwim_cache {
+    dwim_dev *dev;
+    int8_t *q;
+    uint16_t *s;
+    size_t len;
+};
+
+// ---- errors ----
+int dwim_fail(const std::string &msg);
+#define DWIM_HIP(call)                                                                        \
+    do {                                                                                      \
+        hipError_t e_ = (call);                                                               \
+        if (e_ != hipSuccess) return dwim_fail(std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+#define DWIM_CHECK(cond, msg)                      \
+    do {                                           \
+        if (!(cond)) return dwim_fail(msg);        \
+    } while (0)
+
+// ---- launchers (each returns hipGetLastError() of its launch) ----
+hipError_t launch_fill_zero(hipStream_t s, float *x, size_t n);
+hipError_t launch_add(hipStream_t s, float *x, const float *y, size_t n);
+hipError_t launch_silu_mul(hipStream_t s, float *g, const float *u, size_t n);
+hipError_t launch_sigmoid_mul(hipStream_t s, float *x, const float *g, size_t n);
+hipError_t launch_rmsnorm(hipStream_t s, float *out, const float *x, const float *w, size_t rows,
+                          size_t dim, float eps);
+hipError_t launch_l2norm(hipStream_t s, float *x, size_t rows, size_t dim, float eps);
+hipError_t launch_rope(hipStream_t s, float *x, const float *table, size_t n, size_t pos,
+                       size_t n_heads, size_t head_dim, size_t rot_dim);
+hipError_t launch_store(hipStream_t s, int8_t *cq, uint16_t *cs, const float *src, size_t blocks);
+hipError_t launch_matvec(hipStream_t s, const dwim_weight *w, float *out, const float *x, size_t n,
+                         int add);
+hipError_t launch_swiglu(hipStream_t s, const dwim_weight *gate, const dwim_weight *up, float *out,
+                         float *scratch, const float *x, size_t n);
+hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
+                            const dwim_cache *v, size_t n, size_t pos, size_t n_heads,
+                            size_t head_dim, size_t n_kv_heads);
+hipError_t launch_conv(hipStream_t s, float *q, float *k, float *v, float *state_out,
+                       const float *x, const float *state, const float *w, size_t n, size_t q_dim,
+                       size_t k_dim, size_t v_dim);
+hipError_t launch_delta_net(hipStream_t s, float *out, const float *q, const float *k,
+                            const float *v, const float *gates, const float *decay, float *state,
+                            size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim);
+hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols,
+                         uint32_t *out);
+hipError_t launch_synthetic_q4_k(hipStream_t s, uint8_t *qs, uint8_t *meta, size_t rows,
+                                 size_t cols, uint64_t seed, float c);
+hipError_t launch_synthetic_q6_k(hipStream_t s, uint8_t *ql, uint8_t *qh, int8_t *sc,
+                                 uint16_t *d, size_t rows, size_t cols, uint64_t seed, float c);
+hipError_t launch_synthetic_bf16(hipStream_t s, uint16_t *q, size_t rows, size_t cols,
+                                 uint64_t seed, float c);

@@ -1,0 +1,180 @@
+/*
+ * dwim_hip.h — the C ABI of the MI355X (gfx950) backend for dwim's inference
+ * engine.  It is the `gpu::Device` trait of the reference (dwim `gpu/mod.rs:
+ * 176-401`) as plain C: one function per trait method, opaque handles for the
+ * trait's three associated types (`Buffer`, `Weight`, `Cache`), plain pointers
+ * and sizes, no C++ or torch types.  A Rust `gpu/hip` module binds it with
+ * `extern "C"` declarations; this repository's own C++
+ * host (the qwen35 forward pass) and its Python tests call it directly.
+ *
+ * Conventions (those of the reference's `Device`):
+ *  - Every function that can fail returns 0 on success and a nonzero status
+ *    otherwise, with a message from dwim_last_error().  The reference's ops
+ *    panic on contract violations (`gpu/cpu.rs:51-56` "a buffer of {cap}
+ *    activations can't hold {len}") and on launch failures; a binding turns a
+ *    nonzero status into that panic.  Only dwim_open's failure is a plain
+ *    error (the reference's `open` returns `Result`, `gpu/cuda/mod.rs:210`).
+ *  - Lengths count f32 activations.  Operations over rows of activations take
+ *    a buffer's length as a whole number of rows.
+ *  - Operations are queued on the device's one stream, in order; dwim_read and
+ *    dwim_read_cache wait for everything queued before them
+ *    (`gpu/mod.rs:174-175`).  A device is used from one thread at a time.
+ *  - A buffer has a length and the capacity it was allocated with;
+ *    dwim_resize changes only the length (`gpu/mod.rs:216-219`).
+ */
+#ifndef DWIM_HIP_H
+#define DWIM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct dwim_dev dwim_dev;       /* the device: one GPU, one stream          */
+typedef struct dwim_buf dwim_buf;       /* Device::Buffer: f32 activations          */
+typedef struct dwim_weight dwim_weight; /* Device::Weight: a weight matrix          */
+typedef struct dwim_cache dwim_cache;   /* Device::Cache: Q8 key or value cache     */
+
+/* Weight formats (`Tensor`, gpu/mod.rs:46-61, plus the two K-quant formats the
+ * reference has no device form of). */
+enum dwim_format {
+    DWIM_BF16 = 0, /* quants: u16 bf16 bits [rows][cols]; scales: NULL                        */
+    DWIM_Q4_0 = 1, /* quants: u8 [rows][cols/2], element j low / j+16 high nibble of byte j;
+                      scales: f16 bits [rows][cols/32]  (gpu/quant.rs:1-12)                     */
+    DWIM_Q8_0 = 2, /* quants: i8 [rows][cols]; scales: f16 bits [rows][cols/32]                */
+    DWIM_Q4_K = 3, /* quants: ggml block_q4_K, 144 B per 256 weights, row-major; scales: NULL  */
+    DWIM_Q6_K = 4  /* quants: ggml block_q6_K, 210 B per 256 weights, row-major; scales: NULL
+                      (the file layout of inference/quants.rs:79-104)                          */
+};
+
+/* The message of the last failure on this thread ("" if none). */
+const char *dwim_last_error(void);
+
+/* ---- the device (gpu/cuda/mod.rs:210-306 `open`; gpu/mod.rs:188-204) ---- */
+
+/* Opens GPU `index` (a gfx950 device), with one in-order stream. */
+int dwim_open(int index, dwim_dev **out);
+void dwim_close(dwim_dev *dev);
+/* Device::name: the GPU's name, NUL-terminated, truncated to `cap` bytes. */
+int dwim_name(dwim_dev *dev, char *out, size_t cap);
+/* Device::memory: bytes of device memory free. */
+int dwim_memory(dwim_dev *dev, uint64_t *free_bytes);
+/* Device::batch: most tokens a forward pass should run through at once. */
+size_t dwim_batch(dwim_dev *dev);
+/* Waits for every operation queued on the device. */
+int dwim_sync(dwim_dev *dev);
+/* The device's stream (a hipStream_t), for timing with HIP events. */
+void *dwim_stream(dwim_dev *dev);
+
+/* ---- memory (gpu/mod.rs:206-249) ---- */
+
+/* Device::upload: copies a weight matrix to the device, which may lay it out
+ * anew.  `quants`/`scales` as enum dwim_format says; `cols` a whole number of
+ * the format's blocks (32, or 256 for the K formats; any multiple of 8 for bf16). */
+int dwim_upload(dwim_dev *dev, int format, size_t rows, size_t cols, const void *quants,
+                const uint16_t *scales, dwim_weight **out);
+void dwim_free_weight(dwim_weight *w);
+/* Device::alloc: a zeroed buffer of `len` activations. */
+int dwim_alloc(dwim_dev *dev, size_t len, dwim_buf **out);
+void dwim_free_buffer(dwim_buf *buf);
+/* Device::alloc_cache: a zeroed cache of `len` activations, whole blocks of 32. */
+int dwim_alloc_cache(dwim_dev *dev, size_t len, dwim_cache **out);
+void dwim_free_cache(dwim_cache *cache);
+/* Device::resize: sets the length, up to the capacity. */
+int dwim_resize(dwim_dev *dev, dwim_buf *buf, size_t len);
+size_t dwim_len(const dwim_buf *buf);
+/* Device::read: copies the buffer's `len` activations out; `len` must equal
+ * its length.  Waits for the operations before it. */
+int dwim_read(dwim_dev *dev, const dwim_buf *buf, float *out, size_t len);
+/* Device::write: copies `len` activations in; `len` must equal its length. */
+int dwim_write(dwim_dev *dev, dwim_buf *buf, const float *data, size_t len);
+/* Device::copy: dst[dst_offset..][..len] = src[src_offset..][..len]. */
+int dwim_copy(dwim_dev *dev, dwim_buf *dst, size_t dst_offset, const dwim_buf *src,
+              size_t src_offset, size_t len);
+/* Device::store: quantizes `src` into the cache from `offset` on, a block of
+ * 32 at a time as gpu/quant.rs:161-180 does; offset and length whole blocks. */
+int dwim_store(dwim_dev *dev, dwim_cache *cache, size_t offset, const dwim_buf *src);
+/* Device::read_cache: the first `len` activations as stored, `len` int8 then
+ * len/32 little-endian f16 scales: dwim_cache_bytes(len) bytes into `out`. */
+int dwim_read_cache(dwim_dev *dev, const dwim_cache *cache, size_t len, uint8_t *out);
+/* Device::write_cache: sets the first activations from bytes as read_cache gives them. */
+int dwim_write_cache(dwim_dev *dev, dwim_cache *cache, const uint8_t *data, size_t bytes);
+/* gpu/mod.rs:404-407 */
+size_t dwim_cache_bytes(size_t len);
+
+/* ---- operations (gpu/mod.rs:251-400) ---- */
+
+/* out[t] = w · x[t] for each token row of x. */
+int dwim_matmul(dwim_dev *dev, dwim_buf *out, const dwim_weight *w, const dwim_buf *x);
+/* x += w · input (scratch as long as x, left undefined). */
+int dwim_matmul_add(dwim_dev *dev, dwim_buf *x, const dwim_weight *w, const dwim_buf *input,
+                    dwim_buf *scratch);
+/* out = silu(gate · x) * (up · x) (scratch as long as out, left undefined). */
+int dwim_swiglu(dwim_dev *dev, dwim_buf *out, const dwim_weight *gate, const dwim_weight *up,
+                const dwim_buf *x, dwim_buf *scratch);
+/* x += y */
+int dwim_add(dwim_dev *dev, dwim_buf *x, const dwim_buf *y);
+/* out = rmsnorm(x[..len]) * weight, rows of weight's length. */
+int dwim_normalize(dwim_dev *dev, dwim_buf *out, const dwim_buf *x, const dwim_buf *weight,
+                   size_t len, float eps);
+/* each weight-long row of x normalized by its root mean square, times weight. */
+int dwim_rmsnorm(dwim_dev *dev, dwim_buf *x, const dwim_buf *weight, float eps);
+/* each dim-long row of x to unit length. */
+int dwim_l2norm(dwim_dev *dev, dwim_buf *x, size_t dim, float eps);
+/* rotary embeddings: pair (i, i + rot/2) of each head at position p rotated by
+ * table[(p*rot/2 + i)*2 ..][..2] = (cos, sin); the first token at `pos`. */
+int dwim_rope(dwim_dev *dev, dwim_buf *x, const dwim_buf *table, size_t pos, size_t n_heads,
+              size_t head_dim, size_t rot_dim);
+/* causal GQA over the caches, the first token at `pos`. */
+int dwim_attention(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_cache *k_cache,
+                   const dwim_cache *v_cache, size_t pos, size_t n_heads, size_t head_dim,
+                   size_t n_kv_heads);
+/* gate = silu(gate) * up */
+int dwim_silu_mul(dwim_dev *dev, dwim_buf *gate, const dwim_buf *up);
+/* x *= sigmoid(gate) */
+int dwim_sigmoid_mul(dwim_dev *dev, dwim_buf *x, const dwim_buf *gate);
+/* the causal 4-tap convolution of linear attention, SiLU, split into q|k|v. */
+int dwim_conv(dwim_dev *dev, dwim_buf *q, dwim_buf *k, dwim_buf *v, dwim_buf *state_out,
+              const dwim_buf *x, const dwim_buf *state, const dwim_buf *weight);
+/* the gated delta rule, token after token, state [n_v_heads][head_dim][head_dim]. */
+int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_buf *k,
+                   const dwim_buf *v, const dwim_buf *gates, const dwim_buf *decay,
+                   dwim_buf *state, size_t n_k_heads, size_t n_v_heads, size_t head_dim);
+
+/* ---- beyond the trait ---- */
+
+/* The greedy token of each of `rows` rows of logits: the first index of the
+ * largest value (qwen35::argmax, inference/qwen35/mod.rs:702-710), on the
+ * device, so that a token's 1 MB of logits need not be read back.  Writes
+ * `rows` indices to `out` (host memory) and waits. */
+int dwim_argmax(dwim_dev *dev, const dwim_buf *logits, size_t rows, uint32_t *out);
+
+/* Host-side quantizers, the product's own (gpu/quant.rs restated for the host
+ * loader, plus the K formats).  `x` holds `cols` weights. */
+void dwim_quantize_q4_0_row(const float *x, size_t cols, uint16_t *scales, uint8_t *quants);
+void dwim_quantize_q8_0_row(const float *x, size_t cols, uint16_t *scales, int8_t *quants);
+void dwim_quantize_q4_k_row(const float *x, size_t cols, uint8_t *blocks);
+void dwim_quantize_q6_k_row(const float *x, size_t cols, uint8_t *blocks);
+/* The cache quantizer for one block of 32 (gpu/quant.rs:161-180). */
+void dwim_quantize_block(const float *block, uint16_t *scale, int8_t *q);
+uint16_t dwim_to_f16(float x);
+float dwim_from_f16(uint16_t bits);
+
+/* Synthetic weights for a random-init model: value i of stream `seed` is an
+ * approximately normal N(0, sigma) draw (the centred sum of four 16-bit
+ * uniforms of a SplitMix64 hash of (seed, i), times sigma·sqrt(3)/65536), a
+ * computation with integer steps and one f32 multiply, so that host and device
+ * produce the same bits.  dwim_synthetic_values fills `n` values from index
+ * `first` on the host; dwim_upload_synthetic builds a rows×cols weight of the
+ * format directly on the device, row r's values being indices r*cols.. of the
+ * stream, quantized exactly as the host quantizers above do. */
+void dwim_synthetic_values(uint64_t seed, uint64_t first, size_t n, float sigma, float *out);
+int dwim_upload_synthetic(dwim_dev *dev, int format, size_t rows, size_t cols, uint64_t seed,
+                          float sigma, dwim_weight **out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
