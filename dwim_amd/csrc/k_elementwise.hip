@@ -2,6 +2,7 @@
 // embeddings, the Q8 cache store, the causal convolution, argmax and the
 // synthetic-weight generators.  Each reads and writes its operands once.
 #include "device_util.h"
+#include "layout.h"
 #include "quant_math.h"
 #include "runtime.h"
 
@@ -293,16 +294,14 @@ hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t
 
 // One thread per block of 256 weights: the stream's values for the block,
 // quantized as the host quantizers do (quant_math.h).
-__global__ void k_synthetic_q4_k(uint8_t *__restrict__ qs, uint8_t *__restrict__ meta, size_t blocks,
-                                 uint64_t seed, float c) {
+__global__ void k_synthetic_q4_k(uint8_t *__restrict__ tiled, size_t blocks, size_t nb, uint64_t seed, float c) {
     size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= blocks) return;
     float x[256];
     for (int i = 0; i < 256; i++) x[i] = dq::synthetic(seed, b * 256 + i, c);
     uint8_t blk[144];
     dq::quantize_q4_k_block(x, blk);
-    for (int i = 0; i < 16; i++) meta[b * 16 + i] = blk[i];
-    for (int i = 0; i < 128; i++) qs[b * 128 + i] = blk[16 + i];
+    q4kt::place(tiled, nb, b / nb, b % nb, blk);
 }
 
 __global__ void k_synthetic_q6_k(uint8_t *__restrict__ ql, uint8_t *__restrict__ qh, int8_t *__restrict__ sc,
@@ -327,10 +326,9 @@ __global__ void k_synthetic_bf16(uint16_t *__restrict__ q, size_t n, uint64_t se
     q[i] = (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
 }
 
-hipError_t launch_synthetic_q4_k(hipStream_t s, uint8_t *qs, uint8_t *meta, size_t rows, size_t cols,
-                                 uint64_t seed, float c) {
+hipError_t launch_synthetic_q4_k(hipStream_t s, uint8_t *tiled, size_t rows, size_t cols, uint64_t seed, float c) {
     size_t blocks = rows * (cols / 256);
-    k_synthetic_q4_k<<<blocks_for(blocks, 128), 128, 0, s>>>(qs, meta, blocks, seed, c);
+    k_synthetic_q4_k<<<blocks_for(blocks, 128), 128, 0, s>>>(tiled, blocks, cols / 256, seed, c);
     return hipGetLastError();
 }
 

@@ -12,20 +12,20 @@
 // and one lane writes each result.  LPR is picked per shape so that the
 // row's chunks divide evenly among the group's lanes.
 //
-// Chunk semantics per format (weights per 16-byte chunk of the row's main
-// stream):
-//   Q4_K  32 weights: bytes 16h..16h+15 of 32-byte group g of a block's qs =
-//         sub-block 2g (low nibbles) and 2g+1 (high nibbles) at positions
-//         16h..16h+15; out += d1·Σq·x − m1·Σx per sub-block, the min folded out.
+// Chunk semantics of the generic kernel per format (weights per 16-byte chunk
+// of the row's main stream):
 //   Q6_K  64 weights (one chunk = 16 B of ql for k = 0/2, 16 B for k = 1/3 and
 //         16 B of qh): positions l0..l0+15 of the four 32-weight runs of one
 //         half of a block; out += (d·sc)·Σq·x per run of 16.
 //   Q4_0  one block of 32: out += d·Σ(q−8)·x.
 //   Q8_0  half a block (16 weights): out += d·Σq·x.
 //   BF16  8 weights: out += Σw·x.
+// Q4_K, the format of the model's body, has a kernel of its own below.
 #include "device_util.h"
 #include "quant_math.h"
 #include "runtime.h"
+
+#include <stdlib.h>
 
 namespace {
 
@@ -48,22 +48,6 @@ DEV void load16f(const float *p, float *dst) {
 
 DEV uint32_t word_of(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
-// byte k (0..11) of the 12 packed Q4_K scale bytes (meta words y, z, w)
-DEV int meta_byte(const uint4 &m, int k) {
-    uint32_t w = k < 4 ? m.y : (k < 8 ? m.z : m.w);
-    return (int)((w >> (8 * (k & 3))) & 0xffu);
-}
-
-DEV void q4k_sm(const uint4 &m, int j, int &sc, int &mn) {
-    if (j < 4) {
-        sc = meta_byte(m, j) & 63;
-        mn = meta_byte(m, j + 4) & 63;
-    } else {
-        sc = (meta_byte(m, j + 4) & 0xf) | ((meta_byte(m, j - 4) >> 6) << 4);
-        mn = (meta_byte(m, j + 4) >> 4) | ((meta_byte(m, j) >> 6) << 4);
-    }
-}
-
 struct Weights {
     const void *q, *s, *s2, *s3;
     size_t rows, cols;
@@ -73,38 +57,6 @@ struct Weights {
 
 template <int FMT>
 struct Fmt;
-
-template <>
-struct Fmt<DWIM_Q4_K> {
-    static constexpr int kPerChunk = 32;
-    __host__ __device__ static size_t chunks(size_t cols) { return cols / 256 * 8; }
-    // partial for row r, chunk c, activations x (one token)
-    DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
-        size_t nb = w.cols / 256;
-        size_t b = c >> 3;
-        int j8 = (int)(c & 7), g = j8 >> 1, h = j8 & 1;
-        const uint4 q = ((const uint4 *)w.q)[(r * nb + b) * 8 + j8];
-        const uint4 m = ((const uint4 *)w.s)[r * nb + b];
-        float xl[16], xh[16];
-        const float *xb = x + b * 256 + 64 * g + 16 * h;
-        load16f(xb, xl);
-        load16f(xb + 32, xh);
-        float sl = 0.0f, sh = 0.0f, xsl = 0.0f, xsh = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            uint32_t v = word_of(q, i >> 2);
-            sl += lo_nib(v, i & 3) * xl[i];
-            sh += hi_nib(v, i & 3) * xh[i];
-            xsl += xl[i];
-            xsh += xh[i];
-        }
-        float d = dq::from_f16((uint16_t)(m.x & 0xffffu)), dmin = dq::from_f16((uint16_t)(m.x >> 16));
-        int sc1, m1, sc2, m2;
-        q4k_sm(m, 2 * g, sc1, m1);
-        q4k_sm(m, 2 * g + 1, sc2, m2);
-        return (d * (float)sc1) * sl - (dmin * (float)m1) * xsl + (d * (float)sc2) * sh - (dmin * (float)m2) * xsh;
-    }
-};
 
 template <>
 struct Fmt<DWIM_Q6_K> {
@@ -268,6 +220,11 @@ int pick_lpr(size_t cpr) {
     return best;
 }
 
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
 template <int FMT>
 hipError_t launch_fmt(hipStream_t s, const Weights &w, const float *x, float *out, size_t n, int add) {
     int lpr = pick_lpr(Fmt<FMT>::chunks(w.cols));
@@ -299,10 +256,11 @@ hipError_t launch_fmt(hipStream_t s, const Weights &w, const float *x, float *ou
 
 }  // namespace
 
-hipError_t launch_matvec(hipStream_t s, const dwim_weight *wt, float *out, const float *x, size_t n, int add) {
+hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const float *x, size_t n, int add) {
+    hipStream_t s = dev->stream;
     Weights w{wt->q, wt->s, wt->s2, wt->s3, wt->rows, wt->cols};
     switch (wt->fmt) {
-    case DWIM_Q4_K: return launch_fmt<DWIM_Q4_K>(s, w, x, out, n, add);
+    case DWIM_Q4_K: return launch_matvec_q4k(s, wt, out, x, n, add);
     case DWIM_Q6_K: return launch_fmt<DWIM_Q6_K>(s, w, x, out, n, add);
     case DWIM_Q4_0: return launch_fmt<DWIM_Q4_0>(s, w, x, out, n, add);
     case DWIM_Q8_0: return launch_fmt<DWIM_Q8_0>(s, w, x, out, n, add);
@@ -310,10 +268,10 @@ hipError_t launch_matvec(hipStream_t s, const dwim_weight *wt, float *out, const
     }
 }
 
-hipError_t launch_swiglu(hipStream_t s, const dwim_weight *gate, const dwim_weight *up, float *out, float *scratch,
+hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out, float *scratch,
                          const float *x, size_t n) {
-    hipError_t e = launch_matvec(s, gate, out, x, n, 0);
-    if (e == hipSuccess) e = launch_matvec(s, up, scratch, x, n, 0);
-    if (e == hipSuccess) e = launch_silu_mul(s, out, scratch, n * gate->rows);
+    hipError_t e = launch_matvec(dev, gate, out, x, n, 0);
+    if (e == hipSuccess) e = launch_matvec(dev, up, scratch, x, n, 0);
+    if (e == hipSuccess) e = launch_silu_mul(dev->stream, out, scratch, n * gate->rows);
     return e;
 }

@@ -21,7 +21,13 @@ struct dwim_dev {
     size_t partials_cap = 0;  // floats
     uint32_t *argmax_buf = nullptr;
     size_t argmax_cap = 0;
+    // The open handle and every live buffer, weight and cache hold a
+    // reference: the device (its stream) outlives whatever was made on it,
+    // whichever order a binding frees them in.
+    int refs = 1;
 };
+
+void dwim_dev_release(dwim_dev *dev);
 
 struct dwim_buf {
     dwim_dev *dev;
@@ -33,7 +39,7 @@ struct dwim_buf {
 //   BF16  q: u16 [rows][cols]
 //   Q4_0  q: u8 [rows][cols/2] (the reference's nibble order), s: u16 [rows][cols/32]
 //   Q8_0  q: i8 [rows][cols],                                    s: u16 [rows][cols/32]
-//   Q4_K  q: qs u8 [rows][nb][128], s: meta u8 [rows][nb][16] = d, dmin, scales[12]
+//   Q4_K  q: 64-row tiles of blocks as layout.h describes (rows padded to 64)
 //   Q6_K  q: ql u8 [rows][nb][128], s: qh u8 [rows][nb][64], s2: i8 scales [rows][nb][16],
 //         s3: f16 d [rows][nb]
 // with nb = cols/256 blocks per row.  Splitting each K-quant block into
@@ -75,9 +81,11 @@ hipError_t launch_l2norm(hipStream_t s, float *x, size_t rows, size_t dim, float
 hipError_t launch_rope(hipStream_t s, float *x, const float *table, size_t n, size_t pos,
                        size_t n_heads, size_t head_dim, size_t rot_dim);
 hipError_t launch_store(hipStream_t s, int8_t *cq, uint16_t *cs, const float *src, size_t blocks);
-hipError_t launch_matvec(hipStream_t s, const dwim_weight *w, float *out, const float *x, size_t n,
+hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n,
                          int add);
-hipError_t launch_swiglu(hipStream_t s, const dwim_weight *gate, const dwim_weight *up, float *out,
+hipError_t launch_matvec_q4k(hipStream_t s, const dwim_weight *w, float *out, const float *x, size_t n,
+                             int add);
+hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                             const dwim_cache *v, size_t n, size_t pos, size_t n_heads,
@@ -90,8 +98,8 @@ hipError_t launch_delta_net(hipStream_t s, float *out, const float *q, const flo
                             size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim);
 hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols,
                          uint32_t *out);
-hipError_t launch_synthetic_q4_k(hipStream_t s, uint8_t *qs, uint8_t *meta, size_t rows,
-                                 size_t cols, uint64_t seed, float c);
+hipError_t launch_synthetic_q4_k(hipStream_t s, uint8_t *tiled, size_t rows, size_t cols,
+                                 uint64_t seed, float c);
 hipError_t launch_synthetic_q6_k(hipStream_t s, uint8_t *ql, uint8_t *qh, int8_t *sc,
                                  uint16_t *d, size_t rows, size_t cols, uint64_t seed, float c);
 hipError_t launch_synthetic_bf16(hipStream_t s, uint16_t *q, size_t rows, size_t cols,

@@ -9,6 +9,7 @@
 #include <string>
 #include <vector>
 
+#include "layout.h"
 #include "quant_math.h"
 #include "runtime.h"
 
@@ -41,7 +42,7 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
     DWIM_HIP(hipSetDevice(index));
     dwim_dev *dev = new dwim_dev();
     dev->index = index;
-    dev->name = prop.name;
+    dev->name = prop.name[0] ? prop.name : (std::string("AMD ") + prop.gcnArchName);
     dev->cus = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking) != hipSuccess) {
         delete dev;
@@ -51,14 +52,20 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
     return 0;
 }
 
-extern "C" void dwim_close(dwim_dev *dev) {
-    if (!dev) return;
+void dwim_dev_release(dwim_dev *dev) {
+    if (--dev->refs > 0) return;
     hipSetDevice(dev->index);
     hipStreamSynchronize(dev->stream);
     if (dev->partials) hipFree(dev->partials);
     if (dev->argmax_buf) hipFree(dev->argmax_buf);
     hipStreamDestroy(dev->stream);
     delete dev;
+}
+
+extern "C" void dwim_close(dwim_dev *dev) {
+    if (!dev) return;
+    hipStreamSynchronize(dev->stream);
+    dwim_dev_release(dev);
 }
 
 extern "C" int dwim_name(dwim_dev *dev, char *out, size_t cap) {
@@ -97,15 +104,18 @@ extern "C" int dwim_alloc(dwim_dev *dev, size_t len, dwim_buf **out) {
         hipFree(p);
         return dwim_fail("zeroing a buffer failed");
     }
+    dev->refs++;
     *out = new dwim_buf{dev, p, len, len};
     return 0;
 }
 
 extern "C" void dwim_free_buffer(dwim_buf *buf) {
     if (!buf) return;
-    hipStreamSynchronize(buf->dev->stream);
+    dwim_dev *dev = buf->dev;
+    hipStreamSynchronize(dev->stream);
     hipFree(buf->data);
     delete buf;
+    dwim_dev_release(dev);
 }
 
 extern "C" int dwim_alloc_cache(dwim_dev *dev, size_t len, dwim_cache **out) {
@@ -120,16 +130,19 @@ extern "C" int dwim_alloc_cache(dwim_dev *dev, size_t len, dwim_cache **out) {
     }
     hipMemsetAsync(q, 0, std::max<size_t>(len, 32), dev->stream);
     hipMemsetAsync(s, 0, std::max<size_t>(len / 32, 1) * 2, dev->stream);
+    dev->refs++;
     *out = new dwim_cache{dev, q, s, len};
     return 0;
 }
 
 extern "C" void dwim_free_cache(dwim_cache *c) {
     if (!c) return;
-    hipStreamSynchronize(c->dev->stream);
+    dwim_dev *dev = c->dev;
+    hipStreamSynchronize(dev->stream);
     hipFree(c->q);
     hipFree(c->s);
     delete c;
+    dwim_dev_release(dev);
 }
 
 extern "C" int dwim_resize(dwim_dev *, dwim_buf *buf, size_t len) {
@@ -211,10 +224,12 @@ static int alloc_copy(dwim_dev *dev, void **dst, const void *src, size_t bytes) 
 
 extern "C" void dwim_free_weight(dwim_weight *w) {
     if (!w) return;
-    hipStreamSynchronize(w->dev->stream);
+    dwim_dev *dev = w->dev;
+    hipStreamSynchronize(dev->stream);
     for (void *p : {w->q, w->s, w->s2, w->s3})
         if (p) hipFree(p);
     delete w;
+    dwim_dev_release(dev);
 }
 
 static int check_shape(int fmt, size_t rows, size_t cols) {
@@ -224,6 +239,9 @@ static int check_shape(int fmt, size_t rows, size_t cols) {
     case DWIM_Q4_0:
     case DWIM_Q8_0: DWIM_CHECK(cols % 32 == 0, "rows must be a whole number of blocks"); break;
     case DWIM_Q4_K:
+        DWIM_CHECK(cols % 256 == 0, "K-quant rows are whole blocks of 256");
+        DWIM_CHECK(cols <= 80 * 256, "Q4_K rows of at most 20480 weights");
+        break;
     case DWIM_Q6_K: DWIM_CHECK(cols % 256 == 0, "K-quant rows are whole blocks of 256"); break;
     default: return dwim_fail("unknown weight format " + std::to_string(fmt));
     }
@@ -236,6 +254,7 @@ extern "C" int dwim_upload(dwim_dev *dev, int fmt, size_t rows, size_t cols, con
     if (check_shape(fmt, rows, cols)) return 1;
     DWIM_HIP(hipSetDevice(dev->index));
     dwim_weight *w = new dwim_weight{dev, fmt, rows, cols};
+    dev->refs++;
     int err = 0;
     size_t nb = cols / 256;
     switch (fmt) {
@@ -249,14 +268,12 @@ extern "C" int dwim_upload(dwim_dev *dev, int fmt, size_t rows, size_t cols, con
               alloc_copy(dev, &w->s, scales, rows * cols / 32 * 2);
         break;
     case DWIM_Q4_K: {
-        // 144-byte blocks -> qs stream and 16-byte meta stream
-        std::vector<uint8_t> qs(rows * nb * 128), meta(rows * nb * 16);
+        // 144-byte blocks -> 64-row tiles (layout.h), padding rows zero
+        std::vector<uint8_t> tiled(q4kt::bytes(rows, cols), 0);
         const uint8_t *src = (const uint8_t *)quants;
-        for (size_t b = 0; b < rows * nb; b++) {
-            memcpy(&meta[b * 16], src + b * 144, 16);
-            memcpy(&qs[b * 128], src + b * 144 + 16, 128);
-        }
-        err = alloc_copy(dev, &w->q, qs.data(), qs.size()) || alloc_copy(dev, &w->s, meta.data(), meta.size());
+        for (size_t r = 0; r < rows; r++)
+            for (size_t b = 0; b < nb; b++) q4kt::place(tiled.data(), nb, r, b, src + (r * nb + b) * 144);
+        err = alloc_copy(dev, &w->q, tiled.data(), tiled.size());
         if (!err) err = hipStreamSynchronize(dev->stream) != hipSuccess;
         break;
     }
@@ -294,13 +311,13 @@ extern "C" int dwim_upload_synthetic(dwim_dev *dev, int fmt, size_t rows, size_t
     DWIM_HIP(hipSetDevice(dev->index));
     float c = sigma * (1.7320508075688772f / 65536.0f);
     dwim_weight *w = new dwim_weight{dev, fmt, rows, cols};
+    dev->refs++;
     size_t nb = cols / 256;
     int err = 0;
     if (fmt == DWIM_Q4_K) {
-        err = alloc_copy(dev, &w->q, nullptr, rows * nb * 128) || alloc_copy(dev, &w->s, nullptr, rows * nb * 16);
-        if (!err)
-            err = launch_synthetic_q4_k(dev->stream, (uint8_t *)w->q, (uint8_t *)w->s, rows, cols, seed, c) !=
-                  hipSuccess;
+        err = alloc_copy(dev, &w->q, nullptr, q4kt::bytes(rows, cols));
+        if (!err) err = hipMemsetAsync(w->q, 0, q4kt::bytes(rows, cols), dev->stream) != hipSuccess;
+        if (!err) err = launch_synthetic_q4_k(dev->stream, (uint8_t *)w->q, rows, cols, seed, c) != hipSuccess;
     } else if (fmt == DWIM_Q6_K) {
         err = alloc_copy(dev, &w->q, nullptr, rows * nb * 128) || alloc_copy(dev, &w->s, nullptr, rows * nb * 64) ||
               alloc_copy(dev, &w->s2, nullptr, rows * nb * 16) || alloc_copy(dev, &w->s3, nullptr, rows * nb * 2);
@@ -333,7 +350,7 @@ extern "C" int dwim_matmul(dwim_dev *dev, dwim_buf *out, const dwim_weight *w, c
     size_t n;
     if (matmul_shapes(out, w, x, &n)) return 1;
     if (n == 0) return 0;
-    LAUNCH(launch_matvec(dev->stream, w, out->data, x->data, n, 0));
+    LAUNCH(launch_matvec(dev, w, out->data, x->data, n, 0));
     return 0;
 }
 
@@ -343,7 +360,7 @@ extern "C" int dwim_matmul_add(dwim_dev *dev, dwim_buf *x, const dwim_weight *w,
     if (matmul_shapes(x, w, input, &n)) return 1;
     DWIM_CHECK(scratch->cap >= x->len, "the scratch buffer is shorter than x");
     if (n == 0) return 0;
-    LAUNCH(launch_matvec(dev->stream, w, x->data, input->data, n, 1));
+    LAUNCH(launch_matvec(dev, w, x->data, input->data, n, 1));
     return 0;
 }
 
@@ -354,7 +371,7 @@ extern "C" int dwim_swiglu(dwim_dev *dev, dwim_buf *out, const dwim_weight *gate
     DWIM_CHECK(up->rows == gate->rows && up->cols == gate->cols, "gate and up differ in shape");
     DWIM_CHECK(scratch->cap >= out->len, "the scratch buffer is shorter than out");
     if (n == 0) return 0;
-    LAUNCH(launch_swiglu(dev->stream, gate, up, out->data, scratch->data, x->data, n));
+    LAUNCH(launch_swiglu(dev, gate, up, out->data, scratch->data, x->data, n));
     return 0;
 }
 

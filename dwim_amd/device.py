@@ -395,3 +395,13 @@ class Hip:
         out = np.empty(rows, np.uint32)
         _check(self.L.dwim_argmax(self.h, logits.h, rows, _ptr(out, _u32p)))
         return out
+
+
+def _hip_del(self):
+    try:
+        self.close()
+    except Exception:
+        pass
+
+
+Hip.__del__ = _hip_del
