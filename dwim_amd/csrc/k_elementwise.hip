@@ -290,6 +290,64 @@ hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- embedding rows
+
+// Weight (row, col) dequantized exactly as the host dequantizers do (the same
+// operations, unfused), for any device layout.
+__device__ float weight_at(const dwim_weight w, size_t row, size_t col) {
+#pragma clang fp contract(off)
+    switch (w.fmt) {
+    case DWIM_BF16: return dq::bf16_to_f32(((const uint16_t *)w.q)[row * w.cols + col]);
+    case DWIM_Q4_0: {
+        const uint8_t q = ((const uint8_t *)w.q)[row * w.cols / 2 + (col / 32) * 16 + (col % 16)];
+        const float d = dq::from_f16(((const uint16_t *)w.s)[row * (w.cols / 32) + col / 32]);
+        const int nib = (col % 32) < 16 ? (q & 0xf) : (q >> 4);
+        return ((float)nib - 8.0f) * d;
+    }
+    case DWIM_Q8_0: {
+        const int8_t q = ((const int8_t *)w.q)[row * w.cols + col];
+        return (float)q * dq::from_f16(((const uint16_t *)w.s)[row * (w.cols / 32) + col / 32]);
+    }
+    case DWIM_Q4_K: {
+        const size_t nb = w.cols / 256, b = col / 256, pos = col % 256;
+        const uint8_t *u = (const uint8_t *)w.q + q4kt::unit(row / q4kt::kTile, b, nb);
+        const size_t r = row % q4kt::kTile;
+        const int g = (int)(pos / 64), within = (int)(pos % 64), hi = within >= 32, l = within % 32;
+        const uint8_t byte = u[q4kt::qs_off(g, l / 16, r) + l % 16];
+        const int q = hi ? (byte >> 4) : (byte & 0xf);
+        const uint8_t *m = u + q4kt::meta_off(r);
+        int sc, mn;
+        dq::q4k_scale_min(2 * g + hi, m + 4, sc, mn);
+        const float d = dq::from_f16((uint16_t)(m[0] | m[1] << 8)), dmin = dq::from_f16((uint16_t)(m[2] | m[3] << 8));
+        const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+        return d1 * (float)q - m1;
+    }
+    default: {  // Q6_K
+        const size_t nb = w.cols / 256, blk = row * nb + col / 256;
+        const int i = (int)(col % 256), half = i / 128, rr = i % 128, k = rr / 32, l = rr % 32;
+        const uint8_t *ql = (const uint8_t *)w.q + blk * 128, *qh = (const uint8_t *)w.s + blk * 64;
+        const int low = (ql[64 * half + l + 32 * (k % 2)] >> (4 * (k / 2))) & 0xf;
+        const int high = (qh[32 * half + l] >> (2 * k)) & 3;
+        const int q = (low | high << 4) - 32;
+        const int8_t sc = ((const int8_t *)w.s2)[blk * 16 + 8 * half + 2 * k + l / 16];
+        const float d = dq::from_f16(((const uint16_t *)w.s3)[blk]);
+        return d * (float)sc * (float)q;
+    }
+    }
+}
+
+__global__ void k_embed(float *__restrict__ out, const dwim_weight w, const uint32_t *__restrict__ tokens, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * w.cols) return;
+    const size_t t = i / w.cols, c = i % w.cols;
+    out[i] = weight_at(w, tokens[t], c);
+}
+
+hipError_t launch_embed(hipStream_t s, float *out, const dwim_weight *w, const uint32_t *tokens, size_t n) {
+    k_embed<<<blocks_for(n * w->cols, 256), 256, 0, s>>>(out, *w, tokens, n);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- synthetic weights
 
 // One thread per block of 256 weights: the stream's values for the block,

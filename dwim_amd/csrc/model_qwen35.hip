@@ -1,0 +1,454 @@
+// The qwen35 hybrid model (dwim inference/qwen35/mod.rs) as a host program
+// over the C ABI of include/dwim_hip.h: the same buffers, the same operations
+// in the same order as `Model::forward_batch` / `Pass::layer` /
+// `Pass::drafter`, so that what the reference's token loop asks of its
+// `Device` is exactly what runs here.  It is the stand-in for the reference's
+// Rust caller (no Rust toolchain here) and the driver of the model benchmark.
+//
+// Weights are random (dwim_model_synthetic): every tensor is drawn from its own
+// stream, seeded from the model seed and the tensor's GGUF-style name, and the
+// matrices are generated and quantized on the device.
+#include <math.h>
+#include <string.h>
+
+#include <array>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "quant_math.h"
+#include "runtime.h"
+
+namespace {
+
+#define TRY(call)                   \
+    do {                            \
+        if ((call) != 0) return 1;  \
+    } while (0)
+
+constexpr size_t kConvKernel = 4;
+
+// FNV-1a of a tensor's name, the key of its value stream
+uint64_t fnv1a(const std::string &s) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+struct Layer {
+    bool attention = false;
+    dwim_buf *attn_norm = nullptr, *mlp_norm = nullptr;
+    dwim_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+    // full attention
+    dwim_weight *q = nullptr, *qgate = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    dwim_buf *q_norm = nullptr, *k_norm = nullptr;
+    size_t cache = 0;
+    // linear attention
+    dwim_weight *qkv = nullptr, *z = nullptr, *ab = nullptr, *out = nullptr;
+    dwim_buf *conv = nullptr, *decay = nullptr, *norm = nullptr;
+    size_t slot = 0;
+};
+
+struct Draft {
+    dwim_buf *embed_norm = nullptr, *hidden_norm = nullptr, *norm = nullptr;
+    dwim_weight *embed_proj = nullptr, *hidden_proj = nullptr;
+    Layer layer;
+};
+
+struct Sequence {
+    std::vector<dwim_cache *> k_cache, v_cache;
+    std::vector<std::array<dwim_buf *, 2>> conv_state;
+    bool parity = false;
+    std::vector<dwim_buf *> ssm_state;
+    size_t max_len = 0;
+    dwim_buf *hidden = nullptr;
+    bool carry = false;
+};
+
+}  // namespace
+
+struct dwim_model {
+    dwim_dev *dev = nullptr;
+    dwim_qwen35_config c{};
+    uint64_t seed = 0;
+    std::vector<Layer> layers;
+    dwim_buf *norm = nullptr;
+    dwim_weight *head = nullptr, *embd = nullptr;
+    bool has_draft = false;
+    Draft draft;
+    // State (qwen35/mod.rs:1298-1344): per-token buffers for `most` tokens
+    size_t most = 0;
+    std::array<size_t, 11> widths{};
+    dwim_buf *x = nullptr, *xb = nullptr, *xh = nullptr, *q = nullptr, *gate = nullptr, *k = nullptr,
+             *v = nullptr, *att = nullptr, *qkv = nullptr, *z = nullptr, *ab = nullptr;
+    dwim_buf *up = nullptr, *gate_ffn = nullptr, *logits = nullptr, *rope = nullptr, *drafted = nullptr;
+    Sequence seq;
+    size_t caches = 0, slots = 0;
+    // everything allocated, freed with the model
+    std::vector<dwim_buf *> bufs;
+    std::vector<dwim_weight *> weights;
+    std::vector<dwim_cache *> cache_list;
+
+    size_t q_dim() const { return c.heads * c.head_dim; }
+    size_t kv_dim() const { return c.kv_heads * c.head_dim; }
+    size_t k_dim() const { return c.k_heads * c.state_dim; }
+    size_t v_dim() const { return c.v_heads * c.state_dim; }
+    size_t conv_width() const { return (kConvKernel - 1) * (2 * k_dim() + v_dim()); }
+    size_t ssm_width() const { return c.v_heads * c.state_dim * c.state_dim; }
+    bool is_attention(size_t layer) const { return (layer + 1) % c.full_attention_interval == 0; }
+
+    // ---- allocation
+    int buf(size_t len, dwim_buf **out) {
+        TRY(dwim_alloc(dev, len, out));
+        bufs.push_back(*out);
+        return 0;
+    }
+    int vec(const std::string &name, size_t len, float sigma, float offset, dwim_buf **out) {
+        std::vector<float> v(len);
+        const uint64_t s = dq::splitmix(seed, fnv1a(name));
+        dwim_synthetic_values(s, 0, len, sigma, v.data());
+        for (auto &e : v) e = e + offset;
+        TRY(buf(len, out));
+        return dwim_write(dev, *out, v.data(), len);
+    }
+    // values u ∈ [0, 1) from the tensor's stream: (hash >> 40) / 2^24
+    int uniform_vec(const std::string &name, size_t len, float scale, float offset, dwim_buf **out) {
+#pragma clang fp contract(off)
+        std::vector<float> v(len);
+        const uint64_t s = dq::splitmix(seed, fnv1a(name));
+        for (size_t i = 0; i < len; i++) {
+            const float u = (float)(dq::splitmix(s, i) >> 40) * (1.0f / 16777216.0f);
+            v[i] = u * scale + offset;
+        }
+        TRY(buf(len, out));
+        return dwim_write(dev, *out, v.data(), len);
+    }
+    int mat(const std::string &name, int fmt, size_t rows, size_t cols, float sigma, dwim_weight **out) {
+        TRY(dwim_upload_synthetic(dev, fmt, rows, cols, dq::splitmix(seed, fnv1a(name)), sigma, out));
+        weights.push_back(*out);
+        return 0;
+    }
+
+    int load_layer(size_t i, bool attention, int fmt, Layer &l) {
+        const std::string p = "blk." + std::to_string(i) + ".";
+        const size_t H = c.hidden;
+        const float s = 0.02f;
+        l.attention = attention;
+        TRY(vec(p + "attn_norm", H, 0.1f, 1.0f, &l.attn_norm));
+        if (attention) {
+            TRY(mat(p + "attn_q", fmt, q_dim(), H, s, &l.q));
+            TRY(mat(p + "attn_q_gate", fmt, q_dim(), H, s, &l.qgate));
+            TRY(mat(p + "attn_k", fmt, kv_dim(), H, s, &l.k));
+            TRY(mat(p + "attn_v", fmt, kv_dim(), H, s, &l.v));
+            TRY(mat(p + "attn_output", fmt, H, q_dim(), s, &l.o));
+            TRY(vec(p + "attn_q_norm", c.head_dim, 0.1f, 1.0f, &l.q_norm));
+            TRY(vec(p + "attn_k_norm", c.head_dim, 0.1f, 1.0f, &l.k_norm));
+            l.cache = caches++;
+        } else {
+            TRY(mat(p + "attn_qkv", fmt, 2 * k_dim() + v_dim(), H, s, &l.qkv));
+            TRY(mat(p + "attn_gate", fmt, v_dim(), H, s, &l.z));
+            TRY(mat(p + "ssm_ab", DWIM_BF16, 2 * c.v_heads, H, s, &l.ab));
+            TRY(vec(p + "ssm_conv1d", (2 * k_dim() + v_dim()) * kConvKernel, 0.3f, 0.0f, &l.conv));
+            // decay: a ∈ [-1, -0.1) for every value head, then dt_bias ∈ [-4, 4)
+            dwim_buf *a = nullptr, *dt = nullptr;
+            TRY(uniform_vec(p + "ssm_a", c.v_heads, -0.9f, -0.1f, &a));
+            TRY(uniform_vec(p + "ssm_dt.bias", c.v_heads, 8.0f, -4.0f, &dt));
+            TRY(buf(2 * c.v_heads, &l.decay));
+            TRY(dwim_copy(dev, l.decay, 0, a, 0, c.v_heads));
+            TRY(dwim_copy(dev, l.decay, c.v_heads, dt, 0, c.v_heads));
+            TRY(vec(p + "ssm_norm", c.state_dim, 0.1f, 1.0f, &l.norm));
+            TRY(mat(p + "ssm_out", fmt, H, v_dim(), s, &l.out));
+            l.slot = slots++;
+        }
+        TRY(vec(p + "post_attention_norm", H, 0.1f, 1.0f, &l.mlp_norm));
+        TRY(mat(p + "ffn_gate", fmt, c.intermediate, H, s, &l.gate));
+        TRY(mat(p + "ffn_up", fmt, c.intermediate, H, s, &l.up));
+        TRY(mat(p + "ffn_down", fmt, H, c.intermediate, s, &l.down));
+        return 0;
+    }
+
+    int zeroed(size_t len, dwim_buf **out) { return buf(len, out); }  // dwim_alloc zeroes
+
+    int new_sequence(Sequence &s, size_t max_len) {
+        s.max_len = max_len;
+        for (size_t i = 0; i < caches; i++) {
+            dwim_cache *kc, *vc;
+            TRY(dwim_alloc_cache(dev, max_len * kv_dim(), &kc));
+            cache_list.push_back(kc);
+            TRY(dwim_alloc_cache(dev, max_len * kv_dim(), &vc));
+            cache_list.push_back(vc);
+            s.k_cache.push_back(kc);
+            s.v_cache.push_back(vc);
+        }
+        for (size_t i = 0; i < slots; i++) {
+            std::array<dwim_buf *, 2> pair{};
+            TRY(zeroed(conv_width(), &pair[0]));
+            TRY(zeroed(conv_width(), &pair[1]));
+            s.conv_state.push_back(pair);
+            dwim_buf *st;
+            TRY(zeroed(ssm_width(), &st));
+            s.ssm_state.push_back(st);
+        }
+        TRY(buf((most + 1) * c.hidden, &s.hidden));
+        return 0;
+    }
+
+    // State::batch (qwen35/mod.rs:1476-1497)
+    int batch(size_t n) {
+        if (n > most) return dwim_fail("a batch of " + std::to_string(n) + " tokens is more than " + std::to_string(most));
+        dwim_buf *b[11] = {x, xb, xh, q, gate, k, v, att, qkv, z, ab};
+        for (int i = 0; i < 11; i++) TRY(dwim_resize(dev, b[i], n * widths[i]));
+        TRY(dwim_resize(dev, up, n * c.intermediate));
+        TRY(dwim_resize(dev, gate_ffn, n * c.intermediate));
+        return 0;
+    }
+
+    int normalize(dwim_buf *out, dwim_buf *in, dwim_buf *weight, size_t rows) {
+        return dwim_normalize(dev, out, in, weight, rows * c.hidden, c.eps);
+    }
+
+    // Pass::layer (qwen35/mod.rs:541-655), the verify-free path
+    int layer(const Layer &l, size_t n, size_t pos) {
+        const float eps = c.eps;
+        TRY(normalize(xh, x, l.attn_norm, n));
+        if (l.attention) {
+            TRY(dwim_resize(dev, q, n * q_dim()));
+            TRY(dwim_resize(dev, gate, n * q_dim()));
+            TRY(dwim_resize(dev, k, n * kv_dim()));
+            TRY(dwim_resize(dev, v, n * kv_dim()));
+            TRY(dwim_resize(dev, att, n * q_dim()));
+            TRY(dwim_matmul(dev, q, l.q, xh));
+            TRY(dwim_matmul(dev, gate, l.qgate, xh));
+            TRY(dwim_matmul(dev, k, l.k, xh));
+            TRY(dwim_matmul(dev, v, l.v, xh));
+            TRY(dwim_rmsnorm(dev, q, l.q_norm, eps));
+            TRY(dwim_rmsnorm(dev, k, l.k_norm, eps));
+            TRY(dwim_rope(dev, q, rope, pos, c.heads, c.head_dim, c.rot_dim));
+            TRY(dwim_rope(dev, k, rope, pos, c.kv_heads, c.head_dim, c.rot_dim));
+            TRY(dwim_store(dev, seq.k_cache[l.cache], pos * kv_dim(), k));
+            TRY(dwim_store(dev, seq.v_cache[l.cache], pos * kv_dim(), v));
+            TRY(dwim_attention(dev, att, q, seq.k_cache[l.cache], seq.v_cache[l.cache], pos, c.heads, c.head_dim,
+                               c.kv_heads));
+            TRY(dwim_sigmoid_mul(dev, att, gate));
+            TRY(dwim_matmul_add(dev, x, l.o, att, xb));
+        } else {
+            TRY(dwim_resize(dev, q, n * k_dim()));
+            TRY(dwim_resize(dev, k, n * k_dim()));
+            TRY(dwim_resize(dev, v, n * v_dim()));
+            TRY(dwim_resize(dev, att, n * v_dim()));
+            TRY(dwim_matmul(dev, qkv, l.qkv, xh));
+            TRY(dwim_matmul(dev, z, l.z, xh));
+            TRY(dwim_matmul(dev, ab, l.ab, xh));
+            auto &pair = seq.conv_state[l.slot];
+            dwim_buf *state = seq.parity ? pair[0] : pair[1];
+            dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
+            TRY(dwim_conv(dev, q, k, v, state_out, qkv, state, l.conv));
+            TRY(dwim_l2norm(dev, q, c.state_dim, eps));
+            TRY(dwim_l2norm(dev, k, c.state_dim, eps));
+            TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, seq.ssm_state[l.slot], c.k_heads, c.v_heads,
+                               c.state_dim));
+            TRY(dwim_rmsnorm(dev, att, l.norm, eps));
+            TRY(dwim_silu_mul(dev, z, att));
+            TRY(dwim_matmul_add(dev, x, l.out, z, xb));
+        }
+        TRY(normalize(xh, x, l.mlp_norm, n));
+        TRY(dwim_swiglu(dev, up, l.gate, l.up, xh, gate_ffn));
+        TRY(dwim_matmul_add(dev, x, l.down, up, xb));
+        return 0;
+    }
+
+    // Pass::drafter (qwen35/mod.rs:663-698), fed rows of seq.hidden from `first`
+    int drafter(size_t rows, size_t pos, size_t first, bool chain, const uint32_t *tokens) {
+        if (rows == 0) return 0;
+        TRY(batch(rows));
+        TRY(dwim_embed(dev, xb, embd, tokens, rows));
+        TRY(dwim_rmsnorm(dev, xb, draft.embed_norm, c.eps));
+        if (chain)
+            TRY(dwim_copy(dev, xh, 0, drafted, 0, c.hidden));
+        else
+            TRY(dwim_copy(dev, xh, 0, seq.hidden, first * c.hidden, rows * c.hidden));
+        TRY(dwim_rmsnorm(dev, xh, draft.hidden_norm, c.eps));
+        TRY(dwim_matmul(dev, x, draft.embed_proj, xb));
+        TRY(dwim_matmul(dev, xb, draft.hidden_proj, xh));
+        TRY(dwim_add(dev, x, xb));
+        TRY(layer(draft.layer, rows, pos));
+        return normalize(xh, x, draft.norm, rows);
+    }
+
+    // State::carry_over (qwen35/mod.rs:1466-1473)
+    int carry_over(size_t n) {
+        const size_t h = c.hidden;
+        TRY(dwim_resize(dev, xb, h));
+        TRY(dwim_copy(dev, xb, 0, seq.hidden, n * h, h));
+        TRY(dwim_copy(dev, seq.hidden, 0, xb, 0, h));
+        seq.carry = true;
+        return 0;
+    }
+
+    int finish() {
+        float one;
+        TRY(dwim_resize(dev, xb, 1));
+        return dwim_read(dev, xb, &one, 1);
+    }
+
+    // forward_batch (qwen35/mod.rs:425-496) for verify = false.  With
+    // `logits_out` the logits after the last token are read back; with
+    // `greedy` the first index of their maximum is taken on the device.
+    int forward_batch(const uint32_t *tokens, size_t n, size_t pos, bool wanted, float *logits_out, uint32_t *greedy) {
+        TRY(batch(n));
+        TRY(dwim_embed(dev, x, embd, tokens, n));
+        for (const Layer &l : layers) TRY(layer(l, n, pos));
+        seq.parity = !seq.parity;
+        const size_t h = c.hidden;
+        if (!has_draft) {
+            if (!wanted) return finish();
+            TRY(dwim_resize(dev, xb, h));
+            TRY(dwim_resize(dev, xh, h));
+            TRY(dwim_copy(dev, xb, 0, x, (n - 1) * h, h));
+            TRY(normalize(xh, xb, norm, 1));
+            TRY(dwim_resize(dev, logits, c.vocab));
+            TRY(dwim_matmul(dev, logits, head, xh));
+            return read_logits(logits_out, greedy);
+        }
+        TRY(normalize(xh, x, norm, n));
+        TRY(dwim_copy(dev, seq.hidden, h, xh, 0, n * h));
+        if (wanted) {
+            TRY(dwim_resize(dev, xb, h));
+            TRY(dwim_copy(dev, xb, 0, xh, (n - 1) * h, h));
+            TRY(dwim_resize(dev, logits, c.vocab));
+            TRY(dwim_matmul(dev, logits, head, xb));
+        }
+        const size_t first = seq.carry ? 0 : 1;
+        TRY(drafter(n - first, pos + first - 1, first, false, tokens + first));
+        TRY(carry_over(n));
+        if (wanted) return read_logits(logits_out, greedy);
+        return finish();
+    }
+
+    int read_logits(float *logits_out, uint32_t *greedy) {
+        if (greedy) TRY(dwim_argmax(dev, logits, 1, greedy));
+        if (logits_out) TRY(dwim_read(dev, logits, logits_out, c.vocab));
+        if (!greedy && !logits_out) return finish();
+        return 0;
+    }
+
+    // LanguageModel::forward (qwen35/mod.rs:1021-1038)
+    int forward(const uint32_t *tokens, size_t n, size_t pos, float *logits_out, uint32_t *greedy) {
+        if (n == 0) return dwim_fail("no tokens to run");
+        if (pos + n > seq.max_len) return dwim_fail("tokens past the end of the cache");
+        const size_t batches = (n + most - 1) / most;
+        for (size_t i = 0; i < batches; i++) {
+            const size_t m = std::min(most, n - i * most);
+            const bool last = i + 1 == batches;
+            TRY(forward_batch(tokens + i * most, m, pos + i * most, last, last ? logits_out : nullptr,
+                              last ? greedy : nullptr));
+        }
+        return 0;
+    }
+
+    // LanguageModel::reset (qwen35/mod.rs:1230-1246)
+    int reset() {
+        std::vector<float> zeros(std::max(conv_width(), ssm_width()), 0.0f);
+        for (size_t s = 0; s < slots; s++) {
+            for (dwim_buf *b : seq.conv_state[s]) TRY(dwim_write(dev, b, zeros.data(), conv_width()));
+            TRY(dwim_write(dev, seq.ssm_state[s], zeros.data(), ssm_width()));
+        }
+        seq.parity = false;
+        seq.carry = false;
+        return 0;
+    }
+
+    ~dwim_model() {
+        for (auto *b : bufs) dwim_free_buffer(b);
+        for (auto *w : weights) dwim_free_weight(w);
+        for (auto *cc : cache_list) dwim_free_cache(cc);
+    }
+};
+
+// rope_table (qwen35/mod.rs:1504-1515): cos, sin of pos·theta^(-2i/rot)
+static void rope_table(std::vector<float> &t, size_t max_len, size_t rot, float theta) {
+    const size_t half = rot / 2;
+    t.resize(max_len * rot);
+    for (size_t pos = 0; pos < max_len; pos++)
+        for (size_t i = 0; i < half; i++) {
+            const float freq = 1.0f / powf(theta, (float)(2 * i) / (float)rot);
+            const float a = (float)pos * freq;
+            t[(pos * half + i) * 2] = cosf(a);
+            t[(pos * half + i) * 2 + 1] = sinf(a);
+        }
+}
+
+extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg, uint64_t seed, int body_format,
+                                    int head_format, size_t max_len, dwim_model **out) {
+    *out = nullptr;
+    const dwim_qwen35_config &c = *cfg;
+    if (c.full_attention_interval == 0 || c.k_heads == 0 || c.v_heads % c.k_heads != 0 || c.head_dim % 32 != 0 ||
+        max_len == 0)
+        return dwim_fail("model: an inconsistent configuration");
+    std::unique_ptr<dwim_model> m(new dwim_model());
+    m->dev = dev;
+    m->c = c;
+    m->seed = seed;
+    m->most = dwim_batch(dev);
+    for (size_t i = 0; i < c.layers; i++) {
+        m->layers.emplace_back();
+        if (m->load_layer(i, m->is_attention(i), body_format, m->layers.back())) return 1;
+    }
+    if (m->vec("output_norm", c.hidden, 0.1f, 1.0f, &m->norm)) return 1;
+    if (m->mat("output", head_format, c.vocab, c.hidden, 0.02f, &m->head)) return 1;
+    if (m->mat("token_embd", body_format, c.vocab, c.hidden, 1.0f, &m->embd)) return 1;
+    if (c.drafter) {
+        m->has_draft = true;
+        const std::string p = "blk." + std::to_string(c.layers) + ".";
+        if (m->vec(p + "enorm", c.hidden, 0.1f, 1.0f, &m->draft.embed_norm) ||
+            m->vec(p + "hnorm", c.hidden, 0.1f, 1.0f, &m->draft.hidden_norm) ||
+            m->mat(p + "eh_proj.embed", body_format, c.hidden, c.hidden, 0.02f, &m->draft.embed_proj) ||
+            m->mat(p + "eh_proj.hidden", body_format, c.hidden, c.hidden, 0.02f, &m->draft.hidden_proj) ||
+            m->load_layer(c.layers, true, body_format, m->draft.layer) ||
+            m->vec(p + "shared_head_norm", c.hidden, 0.1f, 1.0f, &m->draft.norm))
+            return 1;
+    }
+    // State::new (qwen35/mod.rs:1416-1460)
+    const size_t q_dim = m->q_dim(), kv_dim = m->kv_dim(), k_dim = m->k_dim(), v_dim = m->v_dim();
+    m->widths = {c.hidden,
+                 c.hidden,
+                 c.hidden,
+                 std::max(q_dim, k_dim),
+                 q_dim,
+                 std::max(kv_dim, k_dim),
+                 std::max(kv_dim, v_dim),
+                 std::max(q_dim, v_dim),
+                 2 * k_dim + v_dim,
+                 v_dim,
+                 2 * c.v_heads};
+    dwim_buf **b[11] = {&m->x, &m->xb, &m->xh, &m->q, &m->gate, &m->k, &m->v, &m->att, &m->qkv, &m->z, &m->ab};
+    for (int i = 0; i < 11; i++)
+        if (m->buf(m->most * m->widths[i], b[i])) return 1;
+    if (m->buf(m->most * c.intermediate, &m->up) || m->buf(m->most * c.intermediate, &m->gate_ffn) ||
+        m->buf((c.drafter ? 9 : 1) * c.vocab, &m->logits) || m->buf(c.hidden, &m->drafted))
+        return 1;
+    std::vector<float> table;
+    rope_table(table, max_len, c.rot_dim, c.rope_theta);
+    if (m->buf(table.size(), &m->rope) || dwim_write(dev, m->rope, table.data(), table.size())) return 1;
+    if (m->new_sequence(m->seq, max_len)) return 1;
+    if (dwim_sync(dev)) return 1;
+    *out = m.release();
+    return 0;
+}
+
+extern "C" void dwim_model_free(dwim_model *m) { delete m; }
+
+extern "C" size_t dwim_model_batch(const dwim_model *m) { return m->most; }
+
+extern "C" int dwim_model_forward(dwim_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits) {
+    return m->forward(tokens, n, pos, logits, nullptr);
+}
+
+extern "C" int dwim_model_forward_greedy(dwim_model *m, const uint32_t *tokens, size_t n, size_t pos, uint32_t *next) {
+    return m->forward(tokens, n, pos, nullptr, next);
+}
+
+extern "C" int dwim_model_reset(dwim_model *m) { return m->reset(); }

@@ -21,6 +21,8 @@ struct dwim_dev {
     size_t partials_cap = 0;  // floats
     uint32_t *argmax_buf = nullptr;
     size_t argmax_cap = 0;
+    uint32_t *tokens = nullptr;  // token ids for the embedding lookup
+    size_t tokens_cap = 0;
     // The open handle and every live buffer, weight and cache hold a
     // reference: the device (its stream) outlives whatever was made on it,
     // whichever order a binding frees them in.
@@ -96,6 +98,8 @@ hipError_t launch_conv(hipStream_t s, float *q, float *k, float *v, float *state
 hipError_t launch_delta_net(hipStream_t s, float *out, const float *q, const float *k,
                             const float *v, const float *gates, const float *decay, float *state,
                             size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim);
+hipError_t launch_embed(hipStream_t s, float *out, const dwim_weight *w, const uint32_t *tokens,
+                        size_t n);
 hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols,
                          uint32_t *out);
 hipError_t launch_synthetic_q4_k(hipStream_t s, uint8_t *tiled, size_t rows, size_t cols,

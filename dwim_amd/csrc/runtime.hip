@@ -58,6 +58,7 @@ void dwim_dev_release(dwim_dev *dev) {
     hipStreamSynchronize(dev->stream);
     if (dev->partials) hipFree(dev->partials);
     if (dev->argmax_buf) hipFree(dev->argmax_buf);
+    if (dev->tokens) hipFree(dev->tokens);
     hipStreamDestroy(dev->stream);
     delete dev;
 }
@@ -473,6 +474,29 @@ extern "C" int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, c
     if (n)
         LAUNCH(launch_delta_net(dev->stream, out->data, q->data, k->data, v->data, gates->data, decay->data,
                                 state->data, n, n_k_heads, n_v_heads, head_dim));
+    return 0;
+}
+
+extern "C" int dwim_embed(dwim_dev *dev, dwim_buf *out, const dwim_weight *table, const uint32_t *tokens,
+                          size_t n) {
+    DWIM_CHECK(out->len == n * table->cols, "embed: out must hold a row per token");
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] >= table->rows)
+            return dwim_fail("embed: token " + std::to_string(tokens[i]) + " is past the table's " +
+                             std::to_string(table->rows) + " rows");
+    if (n == 0) return 0;
+    if (dev->tokens_cap < n) {
+        DWIM_HIP(hipStreamSynchronize(dev->stream));
+        if (dev->tokens) hipFree(dev->tokens);
+        dev->tokens = nullptr;
+        dev->tokens_cap = 0;
+        DWIM_HIP(hipMalloc(&dev->tokens, n * 4));
+        dev->tokens_cap = n;
+    }
+    // the ids go through the stream, after whatever still reads the previous ones
+    DWIM_HIP(hipMemcpyAsync(dev->tokens, tokens, n * 4, hipMemcpyHostToDevice, dev->stream));
+    DWIM_HIP(hipStreamSynchronize(dev->stream));
+    LAUNCH(launch_embed(dev->stream, out->data, table, dev->tokens, n));
     return 0;
 }
 

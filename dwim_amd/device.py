@@ -78,6 +78,7 @@ SIGNATURES = {
     "dwim_conv": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "dwim_delta_net": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz]),
     "dwim_argmax": (_int, [_vp, _vp, _sz, _u32p]),
+    "dwim_embed": (_int, [_vp, _vp, _vp, _u32p, _sz]),
     "dwim_quantize_q4_0_row": (None, [_f32p, _sz, _u16p, _u8p]),
     "dwim_quantize_q8_0_row": (None, [_f32p, _sz, _u16p, _i8p]),
     "dwim_quantize_q4_k_row": (None, [_f32p, _sz, _u8p]),
@@ -390,6 +391,10 @@ class Hip:
                   state: Buffer, n_k_heads: int, n_v_heads: int, head_dim: int):
         _check(self.L.dwim_delta_net(self.h, out.h, q.h, k.h, v.h, gates.h, decay.h, state.h,
                                      n_k_heads, n_v_heads, head_dim))
+
+    def embed(self, out: Buffer, table: Weight, tokens):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        _check(self.L.dwim_embed(self.h, out.h, table.h, _ptr(t, _u32p), t.size))
 
     def argmax(self, logits: Buffer, rows: int = 1) -> np.ndarray:
         out = np.empty(rows, np.uint32)

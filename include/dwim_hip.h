@@ -151,6 +151,51 @@ int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_b
  * `rows` indices to `out` (host memory) and waits. */
 int dwim_argmax(dwim_dev *dev, const dwim_buf *logits, size_t rows, uint32_t *out);
 
+/* out[t] = row tokens[t] of `table` (a rows×cols weight of any format),
+ * dequantized: the embedding lookup, which the reference does on the host from
+ * the mapped GGUF (qwen35::Pass::embed, inference/qwen35/mod.rs:526-535), on
+ * the device so that no embedding table stays on the host.  `tokens` is host
+ * memory; out must hold n·cols activations. */
+int dwim_embed(dwim_dev *dev, dwim_buf *out, const dwim_weight *table, const uint32_t *tokens,
+               size_t n);
+
+/* ---- the qwen35 model (inference/qwen35/mod.rs) on this device ----
+ * A C++ restatement of the reference's `Model<D: Device>` over the operations
+ * above, in the reference's order, for a random-initialised model built on
+ * the device (no GGUF file: see dwim_model_synthetic). */
+typedef struct dwim_model dwim_model;
+
+/* qwen35::Config (inference/qwen35/mod.rs:29-56) */
+typedef struct {
+    size_t hidden, intermediate, layers;
+    size_t heads, kv_heads, head_dim, rot_dim;
+    float rope_theta;
+    size_t full_attention_interval;
+    size_t k_heads, v_heads, state_dim;
+    float eps;
+    size_t vocab;
+    int drafter; /* the layer that predicts the token after the next */
+} dwim_qwen35_config;
+
+/* A model with every tensor drawn from `seed` (stream per tensor name, values
+ * as dwim_synthetic_values makes them), matrices in `body_format` (the output
+ * head in `head_format`), state for sequences of up to max_len tokens. */
+int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg, uint64_t seed,
+                         int body_format, int head_format, size_t max_len, dwim_model **out);
+void dwim_model_free(dwim_model *m);
+/* Device::batch as the model uses it: most tokens per forward batch. */
+size_t dwim_model_batch(const dwim_model *m);
+/* LanguageModel::forward (qwen35/mod.rs:1021-1038): runs the tokens from
+ * position `pos` in batches; writes the logits after the last token (vocab
+ * floats) to `logits` unless it is NULL. */
+int dwim_model_forward(dwim_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits);
+/* forward, then the greedy next token (first maximum, qwen35::argmax) taken on
+ * the device: only 4 bytes come back. */
+int dwim_model_forward_greedy(dwim_model *m, const uint32_t *tokens, size_t n, size_t pos,
+                              uint32_t *next);
+/* LanguageModel::reset (qwen35/mod.rs:1230-1246). */
+int dwim_model_reset(dwim_model *m);
+
 /* Host-side quantizers, the product's own (gpu/quant.rs restated for the host
  * loader, plus the K formats).  `x` holds `cols` weights. */
 void dwim_quantize_q4_0_row(const float *x, size_t cols, uint16_t *scales, uint8_t *quants);

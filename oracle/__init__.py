@@ -438,3 +438,73 @@ def rope_table(max_len, rot_dim, theta):
 
 def threads() -> int:
     return lib().or_threads()
+
+
+# ---- the qwen35 forward pass (inference/qwen35/mod.rs), oracle/model.c ----
+class Qwen35Config(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _sz), ("intermediate", _sz), ("layers", _sz), ("heads", _sz), ("kv_heads", _sz),
+        ("head_dim", _sz), ("rot_dim", _sz), ("rope_theta", ctypes.c_float), ("full_attention_interval", _sz),
+        ("k_heads", _sz), ("v_heads", _sz), ("state_dim", _sz), ("eps", ctypes.c_float), ("vocab", _sz),
+        ("drafter", ctypes.c_int),
+    ]
+
+
+def _declare_model(L):
+    if getattr(L, "_model_declared", False):
+        return
+    vp = ctypes.c_void_p
+    u32p = ctypes.POINTER(ctypes.c_uint32)
+    L.or_model_synthetic.restype = vp
+    L.or_model_synthetic.argtypes = [ctypes.POINTER(Qwen35Config), ctypes.c_uint64, ctypes.c_int, ctypes.c_int, _sz, _sz]
+    L.or_model_free.restype = None
+    L.or_model_free.argtypes = [vp]
+    L.or_model_forward.restype = None
+    L.or_model_forward.argtypes = [vp, u32p, _sz, _sz, _f32p]
+    L.or_model_draft.restype = _sz
+    L.or_model_draft.argtypes = [vp, ctypes.c_uint32, _sz, _sz, u32p]
+    L.or_model_reset.restype = None
+    L.or_model_reset.argtypes = [vp]
+    L.or_synthetic_values.restype = None
+    L.or_synthetic_values.argtypes = [ctypes.c_uint64, ctypes.c_uint64, _sz, ctypes.c_float, _f32p]
+    L._model_declared = True
+
+
+def synthetic_values(seed, first, n, sigma):
+    L = lib()
+    _declare_model(L)
+    out = np.empty(n, np.float32)
+    L.or_synthetic_values(seed, first, n, sigma, _p(out, _f32p))
+    return out
+
+
+class Model:
+    """The oracle's qwen35 model for the same synthetic weights as the
+    product's dwim_model_synthetic (fields as dwim_qwen35_config)."""
+
+    def __init__(self, cfg: dict, seed: int, body_fmt=Q4_K, head_fmt=Q6_K, max_len=64, batch=64):
+        L = lib()
+        _declare_model(L)
+        self.L, self.vocab = L, cfg["vocab"]
+        self.cfg = Qwen35Config(**cfg)
+        self.h = L.or_model_synthetic(ctypes.byref(self.cfg), seed, body_fmt, head_fmt, max_len, batch)
+
+    def forward(self, tokens, pos):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.vocab, np.float32)
+        self.L.or_model_forward(self.h, t.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), t.size, pos,
+                                _p(out, _f32p))
+        return out
+
+    def draft(self, token, pos, k):
+        out = np.zeros(max(k, 1), np.uint32)
+        n = self.L.or_model_draft(self.h, token, pos, k, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+        return list(out[:n])
+
+    def reset(self):
+        self.L.or_model_reset(self.h)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.or_model_free(self.h)
+            self.h = None

@@ -99,6 +99,27 @@ void or_rope_table(float *table, size_t max_len, size_t rot_dim, float theta);
 
 int or_threads(void);
 
+/* ---- the qwen35 forward pass (inference/qwen35/mod.rs), for the random model
+ * the product builds with dwim_model_synthetic (same tensor names and streams) ---- */
+typedef struct {
+    size_t hidden, intermediate, layers;
+    size_t heads, kv_heads, head_dim, rot_dim;
+    float rope_theta;
+    size_t full_attention_interval;
+    size_t k_heads, v_heads, state_dim;
+    float eps;
+    size_t vocab;
+    int drafter;
+} or_qwen35_config;
+typedef struct or_model or_model;
+void or_synthetic_values(uint64_t seed, uint64_t first, size_t n, float sigma, float *out);
+or_model *or_model_synthetic(const or_qwen35_config *cfg, uint64_t seed, int body_fmt, int head_fmt,
+                             size_t max_len, size_t batch);
+void or_model_free(or_model *m);
+void or_model_forward(or_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits);
+size_t or_model_draft(or_model *m, uint32_t token, size_t pos, size_t k, uint32_t *drafts);
+void or_model_reset(or_model *m);
+
 #ifdef __cplusplus
 }
 #endif

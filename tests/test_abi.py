@@ -25,7 +25,9 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
     # and the Python mirror binds each of them
-    assert set(names) == set(D.SIGNATURES), set(names) ^ set(D.SIGNATURES)
+    from dwim_amd import model as M
+    bound = set(D.SIGNATURES) | set(M.MODEL_SIGNATURES)
+    assert set(names) == bound, set(names) ^ bound
 
 
 def test_opening_without_a_gpu_fails_cleanly():
@@ -93,6 +95,12 @@ def test_synthetic_values_are_deterministic_and_normal():
     assert np.array_equal(a[1000:2000], b)
     assert abs(a.mean()) < 2e-4 and abs(a.std() - 0.02) < 2e-4
     assert not np.array_equal(a[:1000], D.synthetic_values(6, 0, 1000, 0.02))
+
+
+def test_synthetic_streams_match_the_oracles_restatement():
+    for seed, first, sigma in ((1, 0, 0.02), (2 ** 63 + 5, 10 ** 9, 1.0), (77, 12345, 0.3)):
+        assert np.array_equal(D.synthetic_values(seed, first, 4096, sigma),
+                              O.synthetic_values(seed, first, 4096, sigma))
 
 
 def test_selecting_rows_and_column_groups_reorders_every_format():
