@@ -1,0 +1,232 @@
+"""Benchmark: decode and prefill throughput of the 27B-shape Q4_K hybrid qwen35
+model on one MI355X, with the roofline of the
+dominant decode kernel and the CPU oracle timed on the same host.
+
+A step is one decode token (batch 1) at 4k context: the model is random-init
+(synthetic weights of the 27B shape, Q4_K body, Q6_K head, generated on the
+device), a 4096-token prompt of uniform random ids is prefilled (timed, as
+prefill tok/s), then W untimed and K timed greedy decode steps run.
+`value` is decode tokens/s.
+
+Prints one JSON line.  --gpus above 1 is refused: this build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def hip():
+    from dwim_amd.timing import hip as h
+    L = h()
+    vp = ctypes.c_void_p
+    L.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+    L.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+    L.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]
+    L.hipGraphLaunch.argtypes = [vp, vp]
+    L.hipGraphExecDestroy.argtypes = [vp]
+    L.hipGraphDestroy.argtypes = [vp]
+    return L
+
+
+def kernel_roofline(dev, D, iters=200, copies=8):
+    """The decode matvec (Q4_K, 17408×5120, one token) on its own: `copies`
+    distinct weights (> 256 MB, past the Infinity Cache) in turn, captured in
+    a HIP graph so the launches follow each other without host gaps, timed
+    with HIP events on the device's stream."""
+    from dwim_amd.timing import Event
+    rows, cols = 17408, 5120
+    ws = [dev.upload_synthetic(D.Q4_K, rows, cols, seed=100 + i, sigma=0.02) for i in range(copies)]
+    x = dev.buffer(D.synthetic_values(9, 0, cols, 1.0))
+    out = dev.alloc(rows)
+    for i in range(2 * copies):
+        dev.matmul(out, ws[i % copies], x)
+    dev.sync()
+    L = hip()
+    st = ctypes.c_void_p(dev.stream())
+    graph, execg = ctypes.c_void_p(), ctypes.c_void_p()
+    if L.hipStreamBeginCapture(st, 0) != 0:
+        raise RuntimeError("hipStreamBeginCapture failed")
+    for i in range(iters):
+        dev.matmul(out, ws[i % copies], x)
+    if L.hipStreamEndCapture(st, ctypes.byref(graph)) != 0:
+        raise RuntimeError("hipStreamEndCapture failed")
+    if L.hipGraphInstantiate(ctypes.byref(execg), graph, None, None, 0) != 0:
+        raise RuntimeError("hipGraphInstantiate failed")
+    L.hipGraphLaunch(execg, st)
+    dev.sync()
+    a, b = Event(), Event()
+    a.record(st.value)
+    L.hipGraphLaunch(execg, st)
+    b.record(st.value)
+    ms = a.elapsed_ms(b) / iters
+    L.hipGraphExecDestroy(execg)
+    L.hipGraphDestroy(graph)
+    # algorithmic bytes per launch: the Q4_K weights (144 B per 256), x and y in f32
+    weight_bytes = rows * cols // 256 * 144
+    algo = weight_bytes + 4 * cols + 4 * rows
+    achieved = algo / (ms * 1e-3) / 1e9
+    return {"kernel": "k_mv_q4kt<1> Q4_K matvec 17408x5120 n=1", "us": ms * 1e3, "achieved": achieved,
+            "bytes": algo}
+
+
+def cpu_baseline(threads_note=True):
+    """The oracle (C restatement of dwim's CPU path, OpenMP over rows/heads as
+    rayon does) timed per operation at the model's decode shapes, times the
+    calls per token — the reference's own per-op methodology
+    (gpu/tests.rs:429-609 kernel_speed) — giving CPU ms per decode token."""
+    import oracle as O
+    rng = np.random.default_rng(0)
+    H, F, V = 5120, 17408, 248320
+    t0 = time.time()
+
+    def q4k(rows, cols):
+        vals = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
+        return O.Weight.quantized(O.Q4_K, vals)
+
+    def timed(fn, reps):
+        fn()
+        s = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - s) / reps
+
+    per_token = 0.0
+    # matmuls: (rows, cols, calls per token) of the 64-layer body
+    shapes = [(17408, 5120, 128), (5120, 17408, 64), (10240, 5120, 48), (6144, 5120, 48 + 32), (5120, 6144, 64),
+              (1024, 5120, 32)]
+    for rows, cols, calls in shapes:
+        w = q4k(rows, cols)
+        x = rng.standard_normal(cols, dtype=np.float32)
+        per_token += calls * timed(lambda: O.matmul(w, x), 2)
+    # Q6_K head: time a 1/16 slice of its rows, scale up
+    vals = rng.standard_normal((V // 16, H), dtype=np.float32) * 0.02
+    head = O.Weight.quantized(O.Q6_K, vals)
+    x = rng.standard_normal(H, dtype=np.float32)
+    per_token += 16 * timed(lambda: O.matmul(head, x), 2)
+    # DeltaNet step (48 layers) and attention at 4k (16 layers)
+    nk, nv, d = 16, 48, 128
+    q = O.l2norm(rng.standard_normal(nk * d, dtype=np.float32), d, 1e-6)
+    k = O.l2norm(rng.standard_normal(nk * d, dtype=np.float32), d, 1e-6)
+    v = rng.standard_normal(nv * d, dtype=np.float32)
+    gates = rng.standard_normal(2 * nv, dtype=np.float32)
+    decay = np.concatenate([-rng.uniform(0.1, 1, nv), rng.uniform(-4, 4, nv)]).astype(np.float32)
+    state = rng.standard_normal(nv * d * d, dtype=np.float32) * 0.1
+    per_token += 48 * timed(lambda: O.delta_net(q, k, v, gates, decay, state, nk, nv, d), 2)
+    L = 4096
+    kd = rng.standard_normal(L * 1024, dtype=np.float32)
+    kc, vc = O.cache_of(kd, 0), O.cache_of(kd[::-1].copy(), 0)
+    qa = rng.standard_normal(24 * 256, dtype=np.float32)
+    per_token += 16 * timed(lambda: O.attention(qa, kc, vc, L - 1, 24, 256, 4), 2)
+    return {"value": 1.0 / per_token, "unit": "tok/s", "cores": O.threads(), "kind": "port",
+            "sample": "C restatement of dwim gpu/cpu.rs (OpenMP): each decode op of the 27B shape at 4k context "
+                      "timed once on the host (matmuls, Q6_K head on a 1/16 row slice, DeltaNet step, attention), "
+                      "times its calls per token; elementwise ops omitted",
+            "seconds": time.time() - t0}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--prompt", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true", help="only the decode-matvec roofline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
+        sys.exit(2)
+
+    from dwim_amd import device as D
+    from dwim_amd import model as M
+
+    dev = D.Hip(0)
+    roof = kernel_roofline(dev, D)
+    if args.kernel_only:
+        print(json.dumps({"roofline_kernel": roof}), flush=True)
+        return
+
+    cfg = M.config_27b(drafter=False)
+    max_len = args.prompt + args.warmup + args.steps + 8
+    t0 = time.time()
+    model = M.Model(dev, cfg, seed=1234, body_format=D.Q4_K, head_format=D.Q6_K, max_len=max_len)
+    build_s = time.time() - t0
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, cfg.vocab, args.prompt).astype(np.uint32)
+
+    # prefill, timed
+    dev.sync()
+    t0 = time.perf_counter()
+    tok = model.forward_greedy(prompt, 0)
+    dev.sync()
+    prefill_s = time.perf_counter() - t0
+    pos = args.prompt
+    for _ in range(args.warmup):
+        tok = model.forward_greedy([tok], pos)
+        pos += 1
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tok = model.forward_greedy([tok], pos)
+        pos += 1
+    dev.sync()
+    decode_s = time.perf_counter() - t0
+    ms_per_step = decode_s / args.steps * 1e3
+    decode_tps = args.steps / decode_s
+    # bytes a decode token must read: the Q4_K body, Q6_K head, DeltaNet states
+    # (read and written) and the Q8 KV caches at the context depth
+    body = 64 * (3 * 0 + 0)
+    per_layer_ffn = 3 * 17408 * 5120
+    lin = 48 * ((10240 + 6144) * 5120 + 5120 * 6144 + per_layer_ffn)
+    att = 16 * ((6144 * 2 + 1024 * 2) * 5120 + 5120 * 6144 + per_layer_ffn)
+    body = (lin + att) * 144 // 256 + 48 * 96 * 5120 * 2
+    head = 248320 * 5120 * 210 // 256
+    states = 48 * 2 * (48 * 128 * 128 * 4)
+    kv = 16 * 2 * (pos * 1024 * 34 // 32)
+    token_bytes = body + head + states + kv
+    result = {
+        "metric": "decode tok/s & prefill tok/s, 27B-shape Q4_K hybrid, 1xMI355X; % HBM peak",
+        "value": decode_tps,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights, f32 activations",
+        "data": "synthetic: random-init 27B-shape weights (seeded, generated on the device), uniform random prompt ids",
+        "config": {"workload": "27B-shape qwen35 hybrid, prefill 4096 then greedy decode at 4k context",
+                   "model": "qwen35-27B-shape", "global_batch": 1, "seq_len": args.prompt,
+                   "layers": 64, "hidden": 5120, "ffn": 17408, "vocab": 248320, "weights": "Q4_K body, Q6_K head",
+                   "parallelism": "none (1 GPU)"},
+        "prefill_tok_s": args.prompt / prefill_s,
+        "prefill_s": prefill_s,
+        "decode_hbm_frac": token_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "decode_bytes_per_token": token_bytes,
+        "model_build_s": build_s,
+        "roofline": {"bound": "hbm", "achieved": roof["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": roof["achieved"] / HBM_PEAK_GBS, "traffic": None, "kernel": roof["kernel"],
+                     "kernel_us": roof["us"], "algorithmic_bytes": roof["bytes"]},
+    }
+    model.close()
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
