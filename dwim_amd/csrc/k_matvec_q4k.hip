@@ -69,17 +69,25 @@ DEV void load16f(const float *p, float *dst) {
     for (int k = 0; k < 16; k += 4) *(float4 *)(dst + k) = *(const float4 *)(p + k);
 }
 
+// LDS image of the activations: position p at p + 4·(p / 64) (the four
+// 64-float runs a wave reads at once start on different banks), per token,
+// then the tokens' sub-block sums.
+__host__ __device__ inline size_t xpad(size_t p) { return p + 4 * (p >> 6); }
+__host__ __device__ inline size_t xlds_floats(size_t cols) { return xpad(cols); }
+
 template <int T>
 __global__ void __launch_bounds__(kMaxS * 64) k_mv_q4kt(const uint8_t *__restrict__ wq, size_t rows, size_t nb,
-                                                        const float *__restrict__ x, float *out, int add,
+                                                        const float *__restrict__ xg, float *out, int add,
                                                         uint32_t lo_mask, uint32_t hi_mask) {
+    extern __shared__ float xl_s[];
     __shared__ float red[kMaxS][T][16];
     const int S = (int)(blockDim.x >> 6);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const size_t tile = blockIdx.x;
-    const size_t cols = nb * 256;
+    const size_t cols = nb * 256, per_tok = xlds_floats(cols), sbs = cols / 32;
     const size_t b0 = (size_t)wave * nb / S, b1 = (size_t)(wave + 1) * nb / S;
+    float *xsum_s = xl_s + T * per_tok;
     float acc[T];
 #pragma unroll
     for (int t = 0; t < T; t++) acc[t] = 0.0f;
@@ -94,6 +102,26 @@ __global__ void __launch_bounds__(kMaxS * 64) k_mv_q4kt(const uint8_t *__restric
         qq0[i] = *(const uint4 *)(u + q4kt::qs_off(g, 0, r));
         qq1[i] = *(const uint4 *)(u + q4kt::qs_off(g, 1, r));
     }
+    // the activations into LDS while the weights are on their way, then each
+    // sub-block's sum
+    const int nthreads = (int)blockDim.x;
+    for (size_t i = threadIdx.x * 4; i < T * cols; i += (size_t)nthreads * 4) {
+        const size_t t = i / cols, p = i % cols;
+        *(float4 *)(xl_s + t * per_tok + xpad(p)) = *(const float4 *)(xg + i);
+    }
+    __syncthreads();
+    for (size_t i = threadIdx.x; i < T * sbs; i += nthreads) {
+        const size_t t = i / sbs, sb = i % sbs;
+        const float *p = xl_s + t * per_tok + xpad(sb * 32);
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; k += 4) {
+            const float4 v = *(const float4 *)(p + k);
+            s += (v.x + v.y) + (v.z + v.w);
+        }
+        xsum_s[i] = s;
+    }
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < kBlocksPerWave; i++) {
         const size_t b = b0 + i;
@@ -107,13 +135,9 @@ __global__ void __launch_bounds__(kMaxS * 64) k_mv_q4kt(const uint8_t *__restric
         const float d2 = (d * sc2) * 0.0625f, m2 = dmin * mn2;  // high nibbles arrive as 16·q
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            const float *xb = x + t * cols + b * 256 + 64 * g;
-            // sub-block sums: lane r adds x[4r..4r+3] of the group's 64;
-            // lanes 0-7 make sub-block 2g, lanes 8-15 sub-block 2g+1
-            const float4 x4 = *(const float4 *)(xb + 4 * r);
-            const float own = group_sum<8>((x4.x + x4.y) + (x4.z + x4.w));
-            const float other = __shfl_xor(own, 8, 64);
-            const float xs_lo = r < 8 ? own : other, xs_hi = r < 8 ? other : own;
+            // the group's 64 activations are one padded run of the LDS image
+            const float *xb = xl_s + t * per_tok + xpad(b * 256 + 64 * g);
+            const float xs_lo = xsum_s[t * sbs + b * 8 + 2 * g], xs_hi = xsum_s[t * sbs + b * 8 + 2 * g + 1];
             float sl = 0.0f, sh = 0.0f;
             float xl[16], xh[16];
             load16f(xb, xl);
@@ -156,21 +180,32 @@ hipError_t launch_matvec_q4k(hipStream_t s, const dwim_weight *w, float *out, co
     const unsigned threads = (unsigned)(waves * 64);
     const uint8_t *wq = (const uint8_t *)w->q;
     const uint32_t lo = 0x0f0f0f0fu, hi = 0xf0f0f0f0u;
+    const size_t sbs = w->cols / 32;
+    auto lds_of = [&](size_t tt) { return (tt * xlds_floats(w->cols) + tt * sbs) * sizeof(float); };
+    constexpr size_t kLdsMax = 144 * 1024;  // of gfx950's 160 KB, beside the 4 KB reduction
+    static bool raised[3] = {false, false, false};
     size_t t = 0;
     while (t < n) {
         const size_t left = n - t;
+        size_t tt = left >= 4 && lds_of(4) <= kLdsMax ? 4 : left >= 2 && lds_of(2) <= kLdsMax ? 2 : 1;
+        const size_t lds = lds_of(tt);
+        const int idx = tt == 4 ? 2 : tt == 2 ? 1 : 0;
+        const void *fn = tt == 4 ? (const void *)k_mv_q4kt<4> : tt == 2 ? (const void *)k_mv_q4kt<2>
+                                                                          : (const void *)k_mv_q4kt<1>;
+        if (lds > 64 * 1024 && !raised[idx]) {
+            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+            if (e != hipSuccess) return e;
+            raised[idx] = true;
+        }
         const float *xt = x + t * w->cols;
         float *ot = out + t * w->rows;
-        if (left >= 4) {
-            k_mv_q4kt<4><<<(unsigned)tiles, threads, 0, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
-            t += 4;
-        } else if (left >= 2) {
-            k_mv_q4kt<2><<<(unsigned)tiles, threads, 0, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
-            t += 2;
-        } else {
-            k_mv_q4kt<1><<<(unsigned)tiles, threads, 0, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
-            t += 1;
-        }
+        if (tt == 4)
+            k_mv_q4kt<4><<<(unsigned)tiles, threads, lds, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
+        else if (tt == 2)
+            k_mv_q4kt<2><<<(unsigned)tiles, threads, lds, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
+        else
+            k_mv_q4kt<1><<<(unsigned)tiles, threads, lds, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
+        t += tt;
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
