@@ -270,6 +270,8 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
 
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out, float *scratch,
                          const float *x, size_t n) {
+    if (gate->fmt == DWIM_Q4_K && up->fmt == DWIM_Q4_K && gate->cols <= 16 * 5 * 256 / 2)
+        return launch_swiglu_q4k(dev->stream, gate, up, out, x, n, nullptr, 0.0f);
     hipError_t e = launch_matvec(dev, gate, out, x, n, 0);
     if (e == hipSuccess) e = launch_matvec(dev, up, scratch, x, n, 0);
     if (e == hipSuccess) e = launch_silu_mul(dev->stream, out, scratch, n * gate->rows);

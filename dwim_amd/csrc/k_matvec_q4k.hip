@@ -5,17 +5,25 @@
 // The weights are in the tiled layout of layout.h.  A workgroup of S waves
 // owns a tile of 16 rows: lane 16g + r of a wave takes 32-byte quant group g
 // (sub-blocks 2g and 2g+1, 64 weights) of row r, and wave w takes the tile's
-// blocks (256 columns) b ∈ [w·nb/S, (w+1)·nb/S), about five of them, so that a
-// launch has thousands of waves.  Per block a lane makes three 16-byte weight
-// loads (a quarter-wave's load is 256 contiguous bytes) and reads its 64
-// activations through L1 (a wave touches four 256-byte runs of x).  The
-// sub-block sums of x (for the folded-out mins) come from one float4 per lane
-// and a reduction over 8 lanes.  The four lanes of a row meet by shuffles and
-// the S waves in LDS, in a fixed order: results are deterministic.
+// blocks (256 columns) b ∈ [w·nb/S, (w+1)·nb/S), at most five, so that a
+// launch has thousands of waves.  A wave issues all its weight loads (three
+// 16-byte loads per block; a quarter-wave's load is 256 contiguous bytes)
+// before anything else; meanwhile the workgroup stages the activations in
+// LDS (padded so that the four 64-float runs a wave reads start on different
+// banks) with each sub-block's sum, for the folded-out mins.  The four lanes of
+// a row meet by shuffles and the S waves in LDS, in a fixed order: results are
+// deterministic.
 //
 // Per weight: one v_cvt_f32_ubyte (low nibbles from w & 0x0f0f0f0f, high ones
 // from w & 0xf0f0f0f0 as 16·q, their scale divided by 16) and one v_fmac.
 // Per sub-block of 32: out += d1·Σq·x − m1·Σx (the weight is d1·q − m1).
+//
+// One launch may serve several matrices that read the same activations (the
+// projections of a layer's input), each workgroup finding its matrix from its
+// index; it may first RMS-normalize the activations (x · (1/rms(x) · w), as
+// the reference's `normalize` does before those projections); and it may pair
+// two matrices row for row, gate and up, writing silu(gate·x) · (up·x) (the
+// reference's `swiglu`, gpu/mod.rs:274-285).
 #include "device_util.h"
 #include "layout.h"
 #include "quant_math.h"
@@ -25,6 +33,7 @@ namespace {
 
 constexpr int kMaxS = 16;
 constexpr int kBlocksPerWave = 5;
+constexpr size_t kLdsMax = 144 * 1024;  // of gfx950's 160 KB
 
 DEV float ub0(uint32_t v) { return (float)(v & 0xffu); }
 DEV float ub1(uint32_t v) { return (float)((v >> 8) & 0xffu); }
@@ -69,45 +78,97 @@ DEV void load16f(const float *p, float *dst) {
     for (int k = 0; k < 16; k += 4) *(float4 *)(dst + k) = *(const float4 *)(p + k);
 }
 
-// LDS image of the activations: position p at p + 4·(p / 64) (the four
-// 64-float runs a wave reads at once start on different banks), per token,
+// LDS image of the activations: position p at p + 4·(p / 64), per token,
 // then the tokens' sub-block sums.
 __host__ __device__ inline size_t xpad(size_t p) { return p + 4 * (p >> 6); }
-__host__ __device__ inline size_t xlds_floats(size_t cols) { return xpad(cols); }
+
+struct Job {
+    const uint8_t *w;
+    size_t rows;
+    float *out;
+    int add;
+};
+
+struct Args {
+    Job job[4];
+    unsigned first_tile[5];  // workgroup index where each job's tiles start
+    int njobs;
+    int swiglu;              // jobs 0 and 1 paired: job 0's out = silu(gate·x)·(up·x)
+    size_t nb;               // blocks per row (all jobs share the row length)
+    const float *x;
+    const float *norm;       // RMS-normalize x by this weight first, if set
+    float *xn_out;           // and have workgroup 0 write the normalized x here, if set
+    float eps;
+    int waves;               // waves per matrix (a swiglu workgroup has twice as many)
+    uint32_t lo_mask, hi_mask;
+};
 
 template <int T>
-__global__ void __launch_bounds__(kMaxS * 64) k_mv_q4kt(const uint8_t *__restrict__ wq, size_t rows, size_t nb,
-                                                        const float *__restrict__ xg, float *out, int add,
-                                                        uint32_t lo_mask, uint32_t hi_mask) {
+__global__ void __launch_bounds__(1024) k_mv_q4kt(const Args a) {
     extern __shared__ float xl_s[];
-    __shared__ float red[kMaxS][T][16];
-    const int S = (int)(blockDim.x >> 6);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ float red[2 * kMaxS][T][16];
+    __shared__ float norm_red[16][T];
+    const int lane = threadIdx.x & 63, wave_all = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const size_t tile = blockIdx.x;
-    const size_t cols = nb * 256, per_tok = xlds_floats(cols), sbs = cols / 32;
+    const int S = a.waves;
+    // which matrix and tile
+    int j = 0;
+    while (j + 1 < a.njobs && blockIdx.x >= a.first_tile[j + 1]) j++;
+    const size_t tile = blockIdx.x - a.first_tile[j];
+    const int pairj = (a.swiglu && wave_all >= S) ? 1 : 0;  // the up half of a swiglu workgroup
+    const int wave = wave_all - pairj * S;
+    const Job job = a.job[j + pairj];
+    const size_t nb = a.nb, cols = nb * 256, per_tok = xpad(cols), sbs = cols / 32;
     const size_t b0 = (size_t)wave * nb / S, b1 = (size_t)(wave + 1) * nb / S;
     float *xsum_s = xl_s + T * per_tok;
-    float acc[T];
-#pragma unroll
-    for (int t = 0; t < T; t++) acc[t] = 0.0f;
-    // every weight load of the wave goes out before any arithmetic: one
-    // memory round trip per wave, not one per block
+
+    // every weight load of the wave goes out first: one memory round trip per
+    // wave, not one per block
     uint4 mm[kBlocksPerWave], qq0[kBlocksPerWave], qq1[kBlocksPerWave];
 #pragma unroll
     for (int i = 0; i < kBlocksPerWave; i++) {
         const size_t b = b0 + i < b1 ? b0 + i : b0;
-        const uint8_t *u = wq + q4kt::unit(tile, b, nb);
+        const uint8_t *u = job.w + q4kt::unit(tile, b, nb);
         mm[i] = *(const uint4 *)(u + q4kt::meta_off(r));
         qq0[i] = *(const uint4 *)(u + q4kt::qs_off(g, 0, r));
         qq1[i] = *(const uint4 *)(u + q4kt::qs_off(g, 1, r));
     }
-    // the activations into LDS while the weights are on their way, then each
-    // sub-block's sum
+    // the activations into LDS (and their squares' sums when normalizing)
     const int nthreads = (int)blockDim.x;
+    float ss[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) ss[t] = 0.0f;
     for (size_t i = threadIdx.x * 4; i < T * cols; i += (size_t)nthreads * 4) {
         const size_t t = i / cols, p = i % cols;
-        *(float4 *)(xl_s + t * per_tok + xpad(p)) = *(const float4 *)(xg + i);
+        const float4 v = *(const float4 *)(a.x + i);
+        *(float4 *)(xl_s + t * per_tok + xpad(p)) = v;
+#pragma unroll
+        for (int tt = 0; tt < T; tt++)
+            if (tt == (int)t) ss[tt] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+    if (a.norm) {
+        // x · (1/sqrt(mean(x²) + eps) · w), the reference's rmsnorm (gpu/cpu.rs:157-166)
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const float s = group_sum<64>(ss[t]);
+            if (lane == 0) norm_red[wave_all][t] = s;
+        }
+        __syncthreads();
+        for (size_t i = threadIdx.x * 4; i < T * cols; i += (size_t)nthreads * 4) {
+            const size_t t = i / cols, p = i % cols;
+            float tot = 0.0f;
+            for (int w = 0; w < nthreads / 64; w++) tot += norm_red[w][t];
+            const float scale = 1.0f / sqrtf(tot / (float)cols + a.eps);
+            float4 *dst = (float4 *)(xl_s + t * per_tok + xpad(p));
+            const float4 nw = *(const float4 *)(a.norm + p);
+            float4 v = *dst;
+            v.x *= scale * nw.x;
+            v.y *= scale * nw.y;
+            v.z *= scale * nw.z;
+            v.w *= scale * nw.w;
+            *dst = v;
+            if (a.xn_out && blockIdx.x == 0) *(float4 *)(a.xn_out + i) = v;
+        }
     }
     __syncthreads();
     for (size_t i = threadIdx.x; i < T * sbs; i += nthreads) {
@@ -122,6 +183,10 @@ __global__ void __launch_bounds__(kMaxS * 64) k_mv_q4kt(const uint8_t *__restric
         xsum_s[i] = s;
     }
     __syncthreads();
+
+    float acc[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[t] = 0.0f;
 #pragma unroll
     for (int i = 0; i < kBlocksPerWave; i++) {
         const size_t b = b0 + i;
@@ -142,10 +207,10 @@ __global__ void __launch_bounds__(kMaxS * 64) k_mv_q4kt(const uint8_t *__restric
             float xl[16], xh[16];
             load16f(xb, xl);
             load16f(xb + 32, xh);
-            chunk_dot(q0, xl, xh, lo_mask, hi_mask, sl, sh);
+            chunk_dot(q0, xl, xh, a.lo_mask, a.hi_mask, sl, sh);
             load16f(xb + 16, xl);
             load16f(xb + 48, xh);
-            chunk_dot(q1, xl, xh, lo_mask, hi_mask, sl, sh);
+            chunk_dot(q1, xl, xh, a.lo_mask, a.hi_mask, sl, sh);
             acc[t] += d1 * sl - m1 * xs_lo + d2 * sh - m2 * xs_hi;
         }
     }
@@ -155,39 +220,51 @@ __global__ void __launch_bounds__(kMaxS * 64) k_mv_q4kt(const uint8_t *__restric
         float v = acc[t];
         v += __shfl_xor(v, 16, 64);
         v += __shfl_xor(v, 32, 64);
-        if (g == 0) red[wave][t][r] = v;
+        if (g == 0) red[wave_all][t][r] = v;
     }
     __syncthreads();
+    const Job out_job = a.job[j];
     const size_t row = tile * 16 + r;
-    if (wave == 0 && g == 0 && row < rows) {
+    if (wave_all == 0 && g == 0 && row < out_job.rows) {
 #pragma unroll
         for (int t = 0; t < T; t++) {
             float v = 0.0f;
             for (int w = 0; w < S; w++) v += red[w][t][r];
-            float *o = out + t * rows + row;
-            *o = add ? *o + v : v;
+            if (a.swiglu) {
+                float u = 0.0f;
+                for (int w = S; w < 2 * S; w++) u += red[w][t][r];
+                v = v * sigmoidf_(v) * u;  // silu(gate) · up (gpu/cpu.rs:238-242)
+            }
+            float *o = out_job.out + t * out_job.rows + row;
+            *o = out_job.add ? *o + v : v;
         }
     }
 }
 
-}  // namespace
-
-hipError_t launch_matvec_q4k(hipStream_t s, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
-    const size_t nb = w->cols / 256, tiles = q4kt::tiles(w->rows);
-    // waves per tile: about kBlocksPerWave blocks each, at most kMaxS
+// Launches T-token passes of `a` over n tokens (a.x and the outs advance by a
+// row per token).
+hipError_t run(hipStream_t s, Args a, size_t n) {
+    const size_t nb = a.nb, cols = nb * 256, sbs = cols / 32;
     size_t waves = (nb + kBlocksPerWave - 1) / kBlocksPerWave;
     if (waves > (size_t)kMaxS) return hipErrorInvalidValue;  // rows of at most 80 blocks (checked at upload)
-    const unsigned threads = (unsigned)(waves * 64);
-    const uint8_t *wq = (const uint8_t *)w->q;
-    const uint32_t lo = 0x0f0f0f0fu, hi = 0xf0f0f0f0u;
-    const size_t sbs = w->cols / 32;
-    auto lds_of = [&](size_t tt) { return (tt * xlds_floats(w->cols) + tt * sbs) * sizeof(float); };
-    constexpr size_t kLdsMax = 144 * 1024;  // of gfx950's 160 KB, beside the 4 KB reduction
+    a.waves = (int)waves;
+    const unsigned threads = (unsigned)(waves * 64 * (a.swiglu ? 2 : 1));
+    if (threads > 1024) return hipErrorInvalidValue;
+    unsigned total = 0;
+    const int jobs = a.swiglu ? 1 : a.njobs;  // a swiglu launch walks the gate's tiles
+    for (int j = 0; j < jobs; j++) {
+        a.first_tile[j] = total;
+        total += (unsigned)q4kt::tiles(a.job[j].rows);
+    }
+    a.first_tile[jobs] = total;
+    if (a.swiglu) a.njobs = 1;  // workgroups index tiles of job 0; job 1 is read beside it
+    auto lds_of = [&](size_t tt) { return (tt * xpad(cols) + tt * sbs) * sizeof(float); };
     static bool raised[3] = {false, false, false};
     size_t t = 0;
+    Args b = a;
     while (t < n) {
         const size_t left = n - t;
-        size_t tt = left >= 4 && lds_of(4) <= kLdsMax ? 4 : left >= 2 && lds_of(2) <= kLdsMax ? 2 : 1;
+        const size_t tt = left >= 4 && lds_of(4) <= kLdsMax ? 4 : left >= 2 && lds_of(2) <= kLdsMax ? 2 : 1;
         const size_t lds = lds_of(tt);
         const int idx = tt == 4 ? 2 : tt == 2 ? 1 : 0;
         const void *fn = tt == 4 ? (const void *)k_mv_q4kt<4> : tt == 2 ? (const void *)k_mv_q4kt<2>
@@ -197,17 +274,64 @@ hipError_t launch_matvec_q4k(hipStream_t s, const dwim_weight *w, float *out, co
             if (e != hipSuccess) return e;
             raised[idx] = true;
         }
-        const float *xt = x + t * w->cols;
-        float *ot = out + t * w->rows;
-        if (tt == 4)
-            k_mv_q4kt<4><<<(unsigned)tiles, threads, lds, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
-        else if (tt == 2)
-            k_mv_q4kt<2><<<(unsigned)tiles, threads, lds, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
-        else
-            k_mv_q4kt<1><<<(unsigned)tiles, threads, lds, s>>>(wq, w->rows, nb, xt, ot, add, lo, hi);
-        t += tt;
+        b.x = a.x + t * cols;
+        if (a.xn_out) b.xn_out = a.xn_out + t * cols;
+        for (int j = 0; j < 4; j++)
+            if (a.job[j].out) b.job[j].out = a.job[j].out + t * a.job[j].rows;
+        if (tt == 4) k_mv_q4kt<4><<<total, threads, lds, s>>>(b);
+        else if (tt == 2) k_mv_q4kt<2><<<total, threads, lds, s>>>(b);
+        else k_mv_q4kt<1><<<total, threads, lds, s>>>(b);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+        t += tt;
     }
     return hipSuccess;
+}
+
+Args base_args(size_t cols) {
+    Args a{};
+    a.nb = cols / 256;
+    a.lo_mask = 0x0f0f0f0fu;
+    a.hi_mask = 0xf0f0f0f0u;
+    return a;
+}
+
+}  // namespace
+
+hipError_t launch_matvec_q4k(hipStream_t s, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
+    Args a = base_args(w->cols);
+    a.job[0] = Job{(const uint8_t *)w->q, w->rows, out, add};
+    a.njobs = 1;
+    a.x = x;
+    return run(s, a, n);
+}
+
+hipError_t launch_matvec_q4k_multi(hipStream_t s, const dwim_weight *const *ws, float *const *outs, int count,
+                                   const float *x, size_t n, const float *norm, float eps, float *xn_out) {
+    if (count < 1 || count > 4) return hipErrorInvalidValue;
+    Args a = base_args(ws[0]->cols);
+    for (int j = 0; j < count; j++) {
+        if (ws[j]->cols != ws[0]->cols || ws[j]->fmt != DWIM_Q4_K) return hipErrorInvalidValue;
+        a.job[j] = Job{(const uint8_t *)ws[j]->q, ws[j]->rows, outs[j], 0};
+    }
+    a.njobs = count;
+    a.x = x;
+    a.norm = norm;
+    a.xn_out = norm ? xn_out : nullptr;
+    a.eps = eps;
+    return run(s, a, n);
+}
+
+hipError_t launch_swiglu_q4k(hipStream_t s, const dwim_weight *gate, const dwim_weight *up, float *out, const float *x,
+                             size_t n, const float *norm, float eps) {
+    if (gate->rows != up->rows || gate->cols != up->cols) return hipErrorInvalidValue;
+    Args a = base_args(gate->cols);
+    a.job[0] = Job{(const uint8_t *)gate->q, gate->rows, out, 0};
+    a.job[1] = Job{(const uint8_t *)up->q, up->rows, nullptr, 0};
+    a.njobs = 2;
+    a.swiglu = 1;
+    a.x = x;
+    a.norm = norm;
+    a.eps = eps;
+    return run(s, a, n);
 }

@@ -78,6 +78,7 @@ struct dwim_model {
     dwim_buf *norm = nullptr;
     dwim_weight *head = nullptr, *embd = nullptr;
     bool has_draft = false;
+    bool fuse = true;  // fused decode launches where the formats allow
     Draft draft;
     // State (qwen35/mod.rs:1298-1344): per-token buffers for `most` tokens
     size_t most = 0;
@@ -210,20 +211,43 @@ struct dwim_model {
         return dwim_normalize(dev, out, in, weight, rows * c.hidden, c.eps);
     }
 
+    // Q4_K projections of a layer's input fused with its normalization: one
+    // launch normalizes x in LDS and runs every matrix that reads it
+    bool fusable(const Layer &l) const {
+        return fuse && (l.attention ? l.q->fmt : l.qkv->fmt) == DWIM_Q4_K && l.gate->fmt == DWIM_Q4_K &&
+               c.hidden % 256 == 0 && c.hidden <= 10240;
+    }
+    int projections(const dwim_weight *const *ws, dwim_buf *const *outs, int count, const dwim_buf *norm_w,
+                    size_t n, dwim_buf *xn_out) {
+        float *o[4];
+        for (int i = 0; i < count; i++) o[i] = outs[i]->data;
+        DWIM_HIP(launch_matvec_q4k_multi(dev->stream, ws, o, count, x->data, n, norm_w->data, c.eps,
+                                         xn_out ? xn_out->data : nullptr));
+        return 0;
+    }
+
     // Pass::layer (qwen35/mod.rs:541-655), the verify-free path
     int layer(const Layer &l, size_t n, size_t pos) {
         const float eps = c.eps;
-        TRY(normalize(xh, x, l.attn_norm, n));
+        const bool fused = fusable(l);
+        if (!fused || !l.attention) TRY(dwim_resize(dev, xh, n * c.hidden));
+        if (!fused) TRY(normalize(xh, x, l.attn_norm, n));
         if (l.attention) {
             TRY(dwim_resize(dev, q, n * q_dim()));
             TRY(dwim_resize(dev, gate, n * q_dim()));
             TRY(dwim_resize(dev, k, n * kv_dim()));
             TRY(dwim_resize(dev, v, n * kv_dim()));
             TRY(dwim_resize(dev, att, n * q_dim()));
-            TRY(dwim_matmul(dev, q, l.q, xh));
-            TRY(dwim_matmul(dev, gate, l.qgate, xh));
-            TRY(dwim_matmul(dev, k, l.k, xh));
-            TRY(dwim_matmul(dev, v, l.v, xh));
+            if (fused) {
+                const dwim_weight *ws[4] = {l.q, l.qgate, l.k, l.v};
+                dwim_buf *outs[4] = {q, gate, k, v};
+                TRY(projections(ws, outs, 4, l.attn_norm, n, nullptr));
+            } else {
+                TRY(dwim_matmul(dev, q, l.q, xh));
+                TRY(dwim_matmul(dev, gate, l.qgate, xh));
+                TRY(dwim_matmul(dev, k, l.k, xh));
+                TRY(dwim_matmul(dev, v, l.v, xh));
+            }
             TRY(dwim_rmsnorm(dev, q, l.q_norm, eps));
             TRY(dwim_rmsnorm(dev, k, l.k_norm, eps));
             TRY(dwim_rope(dev, q, rope, pos, c.heads, c.head_dim, c.rot_dim));
@@ -239,8 +263,14 @@ struct dwim_model {
             TRY(dwim_resize(dev, k, n * k_dim()));
             TRY(dwim_resize(dev, v, n * v_dim()));
             TRY(dwim_resize(dev, att, n * v_dim()));
-            TRY(dwim_matmul(dev, qkv, l.qkv, xh));
-            TRY(dwim_matmul(dev, z, l.z, xh));
+            if (fused) {
+                const dwim_weight *ws[2] = {l.qkv, l.z};
+                dwim_buf *outs[2] = {qkv, z};
+                TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
+            } else {
+                TRY(dwim_matmul(dev, qkv, l.qkv, xh));
+                TRY(dwim_matmul(dev, z, l.z, xh));
+            }
             TRY(dwim_matmul(dev, ab, l.ab, xh));
             auto &pair = seq.conv_state[l.slot];
             dwim_buf *state = seq.parity ? pair[0] : pair[1];
@@ -254,8 +284,12 @@ struct dwim_model {
             TRY(dwim_silu_mul(dev, z, att));
             TRY(dwim_matmul_add(dev, x, l.out, z, xb));
         }
-        TRY(normalize(xh, x, l.mlp_norm, n));
-        TRY(dwim_swiglu(dev, up, l.gate, l.up, xh, gate_ffn));
+        if (fused) {
+            DWIM_HIP(launch_swiglu_q4k(dev->stream, l.gate, l.up, up->data, x->data, n, l.mlp_norm->data, eps));
+        } else {
+            TRY(normalize(xh, x, l.mlp_norm, n));
+            TRY(dwim_swiglu(dev, up, l.gate, l.up, xh, gate_ffn));
+        }
         TRY(dwim_matmul_add(dev, x, l.down, up, xb));
         return 0;
     }

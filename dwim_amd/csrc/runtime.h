@@ -87,6 +87,14 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *w, float *out, const 
                          int add);
 hipError_t launch_matvec_q4k(hipStream_t s, const dwim_weight *w, float *out, const float *x, size_t n,
                              int add);
+// Up to four Q4_K matrices of one row length over the same x in one launch,
+// x first RMS-normalized by `norm` (when given; the normalized rows are also
+// written to xn_out when that is given).
+hipError_t launch_matvec_q4k_multi(hipStream_t s, const dwim_weight *const *ws, float *const *outs, int count,
+                                   const float *x, size_t n, const float *norm, float eps, float *xn_out);
+// out = silu(gate·x) · (up·x) for Q4_K gate and up, x optionally RMS-normalized
+hipError_t launch_swiglu_q4k(hipStream_t s, const dwim_weight *gate, const dwim_weight *up, float *out,
+                             const float *x, size_t n, const float *norm, float eps);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
