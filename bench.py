@@ -81,7 +81,33 @@ def kernel_roofline(dev, D, iters=200, copies=8):
             "bytes": algo}
 
 
-def cpu_baseline(threads_note=True):
+def copy_calibration(dev, mib=256, reps=8):
+    """A plain device copy of known size (torch's copy kernel, `mib` MiB read
+    and written per launch) for scaling the FETCH_SIZE / WRITE_SIZE counters
+    of the matvec into bytes."""
+    import torch
+    n = mib * 1024 * 1024 // 4
+    a = torch.ones(n, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"copy_bytes_per_launch": 4 * n}
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 PMC passes (FETCH_SIZE, WRITE_SIZE, each scaled by the copy
+    calibration): profiles/q4k_matvec_17408x5120_traffic.json, or None."""
+    p = os.path.join(ROOT, "profiles", "q4k_matvec_17408x5120_traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f)["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def cpu_baseline():
     """The oracle (C restatement of dwim's CPU path, OpenMP over rows/heads as
     rayon does) timed per operation at the model's decode shapes, times the
     calls per token — the reference's own per-op methodology
@@ -155,7 +181,7 @@ def main():
     dev = D.Hip(0)
     roof = kernel_roofline(dev, D)
     if args.kernel_only:
-        print(json.dumps({"roofline_kernel": roof}), flush=True)
+        print(json.dumps({"roofline_kernel": roof, "calibration": copy_calibration(dev)}), flush=True)
         return
 
     cfg = M.config_27b(drafter=False)
@@ -187,7 +213,6 @@ def main():
     decode_tps = args.steps / decode_s
     # bytes a decode token must read: the Q4_K body, Q6_K head, DeltaNet states
     # (read and written) and the Q8 KV caches at the context depth
-    body = 64 * (3 * 0 + 0)
     per_layer_ffn = 3 * 17408 * 5120
     lin = 48 * ((10240 + 6144) * 5120 + 5120 * 6144 + per_layer_ffn)
     att = 16 * ((6144 * 2 + 1024 * 2) * 5120 + 5120 * 6144 + per_layer_ffn)
@@ -219,7 +244,7 @@ def main():
         "decode_bytes_per_token": token_bytes,
         "model_build_s": build_s,
         "roofline": {"bound": "hbm", "achieved": roof["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": roof["achieved"] / HBM_PEAK_GBS, "traffic": None, "kernel": roof["kernel"],
+                     "frac": roof["achieved"] / HBM_PEAK_GBS, "traffic": measured_traffic(), "kernel": roof["kernel"],
                      "kernel_us": roof["us"], "algorithmic_bytes": roof["bytes"]},
     }
     model.close()
