@@ -41,17 +41,19 @@ def hip():
 
 
 def kernel_roofline(dev, D, iters=200, copies=8):
-    """The decode matvec (Q4_K, 17408×5120, one token) on its own: `copies`
-    distinct weights (> 256 MB, past the Infinity Cache) in turn, captured in
-    a HIP graph so the launches follow each other without host gaps, timed
+    """The decode matvec (Q4_K, 17408×5120, one token) on its own: the token's
+    activations are prepared once (int8 planes), then `copies` distinct
+    weights (> 256 MB, past the Infinity Cache) are applied in turn, captured
+    in a HIP graph so the launches follow each other without host gaps, timed
     with HIP events on the device's stream."""
     from dwim_amd.timing import Event
     rows, cols = 17408, 5120
     ws = [dev.upload_synthetic(D.Q4_K, rows, cols, seed=100 + i, sigma=0.02) for i in range(copies)]
     x = dev.buffer(D.synthetic_values(9, 0, cols, 1.0))
     out = dev.alloc(rows)
+    dev.prepare(x)
     for i in range(2 * copies):
-        dev.matmul(out, ws[i % copies], x)
+        dev.matmul_prepared(out, ws[i % copies])
     dev.sync()
     L = hip()
     st = ctypes.c_void_p(dev.stream())
@@ -59,7 +61,7 @@ def kernel_roofline(dev, D, iters=200, copies=8):
     if L.hipStreamBeginCapture(st, 0) != 0:
         raise RuntimeError("hipStreamBeginCapture failed")
     for i in range(iters):
-        dev.matmul(out, ws[i % copies], x)
+        dev.matmul_prepared(out, ws[i % copies])
     if L.hipStreamEndCapture(st, ctypes.byref(graph)) != 0:
         raise RuntimeError("hipStreamEndCapture failed")
     if L.hipGraphInstantiate(ctypes.byref(execg), graph, None, None, 0) != 0:
@@ -77,7 +79,7 @@ def kernel_roofline(dev, D, iters=200, copies=8):
     weight_bytes = rows * cols // 256 * 144
     algo = weight_bytes + 4 * cols + 4 * rows
     achieved = algo / (ms * 1e-3) / 1e9
-    return {"kernel": "k_mv_q4kt<1> Q4_K matvec 17408x5120 n=1", "us": ms * 1e3, "achieved": achieved,
+    return {"kernel": "k_mv_q4k_mfma<5> Q4_K matvec 17408x5120 n=1 (int8 MFMA)", "us": ms * 1e3, "achieved": achieved,
             "bytes": algo}
 
 

@@ -313,7 +313,7 @@ __device__ float weight_at(const dwim_weight w, size_t row, size_t col) {
         const uint8_t *u = (const uint8_t *)w.q + q4kt::unit(row / q4kt::kTile, b, nb);
         const size_t r = row % q4kt::kTile;
         const int g = (int)(pos / 64), within = (int)(pos % 64), hi = within >= 32, l = within % 32;
-        const uint8_t byte = u[q4kt::qs_off(g, l / 16, r) + l % 16];
+        const uint8_t byte = q4kt::stored(u[q4kt::qs_off(g, r) + l]);
         const int q = hi ? (byte >> 4) : (byte & 0xf);
         const uint8_t *m = u + q4kt::meta_off(r);
         int sc, mn;

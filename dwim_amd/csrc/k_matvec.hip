@@ -260,7 +260,7 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
     hipStream_t s = dev->stream;
     Weights w{wt->q, wt->s, wt->s2, wt->s3, wt->rows, wt->cols};
     switch (wt->fmt) {
-    case DWIM_Q4_K: return launch_matvec_q4k(s, wt, out, x, n, add);
+    case DWIM_Q4_K: return launch_matvec_q4k(dev, wt, out, x, n, add);
     case DWIM_Q6_K: return launch_fmt<DWIM_Q6_K>(s, w, x, out, n, add);
     case DWIM_Q4_0: return launch_fmt<DWIM_Q4_0>(s, w, x, out, n, add);
     case DWIM_Q8_0: return launch_fmt<DWIM_Q8_0>(s, w, x, out, n, add);
@@ -271,7 +271,7 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out, float *scratch,
                          const float *x, size_t n) {
     if (gate->fmt == DWIM_Q4_K && up->fmt == DWIM_Q4_K && gate->cols <= 16 * 5 * 256 / 2)
-        return launch_swiglu_q4k(dev->stream, gate, up, out, x, n, nullptr, 0.0f);
+        return launch_swiglu_q4k(dev, gate, up, out, x, n, nullptr, 0.0f);
     hipError_t e = launch_matvec(dev, gate, out, x, n, 0);
     if (e == hipSuccess) e = launch_matvec(dev, up, scratch, x, n, 0);
     if (e == hipSuccess) e = launch_silu_mul(dev->stream, out, scratch, n * gate->rows);

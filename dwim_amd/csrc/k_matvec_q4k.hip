@@ -130,8 +130,14 @@ __global__ void __launch_bounds__(1024) k_mv_q4kt(const Args a) {
         const size_t b = b0 + i < b1 ? b0 + i : b0;
         const uint8_t *u = job.w + q4kt::unit(tile, b, nb);
         mm[i] = *(const uint4 *)(u + q4kt::meta_off(r));
-        qq0[i] = *(const uint4 *)(u + q4kt::qs_off(g, 0, r));
-        qq1[i] = *(const uint4 *)(u + q4kt::qs_off(g, 1, r));
+        qq0[i] = *(const uint4 *)(u + q4kt::qs_off(g, r));
+        qq1[i] = *(const uint4 *)(u + q4kt::qs_off(g, r) + 16);
+    }
+    // the stored high nibbles are XOR 8: back to ggml's bytes
+#pragma unroll
+    for (int i = 0; i < kBlocksPerWave; i++) {
+        qq0[i] = make_uint4(qq0[i].x ^ 0x80808080u, qq0[i].y ^ 0x80808080u, qq0[i].z ^ 0x80808080u, qq0[i].w ^ 0x80808080u);
+        qq1[i] = make_uint4(qq1[i].x ^ 0x80808080u, qq1[i].y ^ 0x80808080u, qq1[i].z ^ 0x80808080u, qq1[i].w ^ 0x80808080u);
     }
     // the activations into LDS (and their squares' sums when normalizing)
     const int nthreads = (int)blockDim.x;
@@ -298,33 +304,49 @@ Args base_args(size_t cols) {
 
 }  // namespace
 
-hipError_t launch_matvec_q4k(hipStream_t s, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
+hipError_t launch_matvec_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
+    if (n == 1) {
+        hipError_t e = launch_planes(dev, x, w->cols, nullptr, 0.0f, nullptr);
+        if (e != hipSuccess) return e;
+        return launch_mv_q4k_mfma(dev, &w, &out, &add, 1, 0);
+    }
     Args a = base_args(w->cols);
     a.job[0] = Job{(const uint8_t *)w->q, w->rows, out, add};
     a.njobs = 1;
     a.x = x;
-    return run(s, a, n);
+    return run(dev->stream, a, n);
 }
 
-hipError_t launch_matvec_q4k_multi(hipStream_t s, const dwim_weight *const *ws, float *const *outs, int count,
+hipError_t launch_matvec_q4k_multi(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, int count,
                                    const float *x, size_t n, const float *norm, float eps, float *xn_out) {
     if (count < 1 || count > 4) return hipErrorInvalidValue;
-    Args a = base_args(ws[0]->cols);
-    for (int j = 0; j < count; j++) {
+    for (int j = 0; j < count; j++)
         if (ws[j]->cols != ws[0]->cols || ws[j]->fmt != DWIM_Q4_K) return hipErrorInvalidValue;
-        a.job[j] = Job{(const uint8_t *)ws[j]->q, ws[j]->rows, outs[j], 0};
+    if (n == 1) {
+        hipError_t e = launch_planes(dev, x, ws[0]->cols, norm, eps, norm ? xn_out : nullptr);
+        if (e != hipSuccess) return e;
+        return launch_mv_q4k_mfma(dev, ws, outs, nullptr, count, 0);
     }
+    Args a = base_args(ws[0]->cols);
+    for (int j = 0; j < count; j++) a.job[j] = Job{(const uint8_t *)ws[j]->q, ws[j]->rows, outs[j], 0};
     a.njobs = count;
     a.x = x;
     a.norm = norm;
     a.xn_out = norm ? xn_out : nullptr;
     a.eps = eps;
-    return run(s, a, n);
+    return run(dev->stream, a, n);
 }
 
-hipError_t launch_swiglu_q4k(hipStream_t s, const dwim_weight *gate, const dwim_weight *up, float *out, const float *x,
+hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out, const float *x,
                              size_t n, const float *norm, float eps) {
     if (gate->rows != up->rows || gate->cols != up->cols) return hipErrorInvalidValue;
+    if (n == 1) {
+        hipError_t e = launch_planes(dev, x, gate->cols, norm, eps, nullptr);
+        if (e != hipSuccess) return e;
+        const dwim_weight *ws[2] = {gate, up};
+        float *outs[2] = {out, nullptr};
+        return launch_mv_q4k_mfma(dev, ws, outs, nullptr, 2, 1);
+    }
     Args a = base_args(gate->cols);
     a.job[0] = Job{(const uint8_t *)gate->q, gate->rows, out, 0};
     a.job[1] = Job{(const uint8_t *)up->q, up->rows, nullptr, 0};
@@ -333,5 +355,5 @@ hipError_t launch_swiglu_q4k(hipStream_t s, const dwim_weight *gate, const dwim_
     a.x = x;
     a.norm = norm;
     a.eps = eps;
-    return run(s, a, n);
+    return run(dev->stream, a, n);
 }

@@ -221,7 +221,7 @@ struct dwim_model {
                     size_t n, dwim_buf *xn_out) {
         float *o[4];
         for (int i = 0; i < count; i++) o[i] = outs[i]->data;
-        DWIM_HIP(launch_matvec_q4k_multi(dev->stream, ws, o, count, x->data, n, norm_w->data, c.eps,
+        DWIM_HIP(launch_matvec_q4k_multi(dev, ws, o, count, x->data, n, norm_w->data, c.eps,
                                          xn_out ? xn_out->data : nullptr));
         return 0;
     }
@@ -285,7 +285,7 @@ struct dwim_model {
             TRY(dwim_matmul_add(dev, x, l.out, z, xb));
         }
         if (fused) {
-            DWIM_HIP(launch_swiglu_q4k(dev->stream, l.gate, l.up, up->data, x->data, n, l.mlp_norm->data, eps));
+            DWIM_HIP(launch_swiglu_q4k(dev, l.gate, l.up, up->data, x->data, n, l.mlp_norm->data, eps));
         } else {
             TRY(normalize(xh, x, l.mlp_norm, n));
             TRY(dwim_swiglu(dev, up, l.gate, l.up, xh, gate_ffn));

@@ -23,6 +23,8 @@ struct dwim_dev {
     size_t argmax_cap = 0;
     uint32_t *tokens = nullptr;  // token ids for the embedding lookup
     size_t tokens_cap = 0;
+    void *planes = nullptr;  // one token's int8 activation planes (planes_scratch_bytes())
+    size_t prepared = 0;     // width of the planes dwim_prepare wrote (0: none, or replaced)
     // The open handle and every live buffer, weight and cache hold a
     // reference: the device (its stream) outlives whatever was made on it,
     // whichever order a binding frees them in.
@@ -85,16 +87,25 @@ hipError_t launch_rope(hipStream_t s, float *x, const float *table, size_t n, si
 hipError_t launch_store(hipStream_t s, int8_t *cq, uint16_t *cs, const float *src, size_t blocks);
 hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n,
                          int add);
-hipError_t launch_matvec_q4k(hipStream_t s, const dwim_weight *w, float *out, const float *x, size_t n,
+hipError_t launch_matvec_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n,
                              int add);
 // Up to four Q4_K matrices of one row length over the same x in one launch,
 // x first RMS-normalized by `norm` (when given; the normalized rows are also
 // written to xn_out when that is given).
-hipError_t launch_matvec_q4k_multi(hipStream_t s, const dwim_weight *const *ws, float *const *outs, int count,
+hipError_t launch_matvec_q4k_multi(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, int count,
                                    const float *x, size_t n, const float *norm, float eps, float *xn_out);
 // out = silu(gate·x) · (up·x) for Q4_K gate and up, x optionally RMS-normalized
-hipError_t launch_swiglu_q4k(hipStream_t s, const dwim_weight *gate, const dwim_weight *up, float *out,
+hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                              const float *x, size_t n, const float *norm, float eps);
+// One token on the int8 matrix cores: launch_planes writes x's planes (RMS-
+// normalized by `norm` when given, the normalized x also to xn_out when
+// given) into the device's scratch; launch_mv_q4k_mfma then runs up to four
+// matrices over them (outs[j] += or = W_j·x by adds[j]), or gate and up as a
+// SwiGLU pair (swiglu = 1, count = 2, the result in outs[0]).
+size_t planes_scratch_bytes();
+hipError_t launch_planes(dwim_dev *dev, const float *x, size_t cols, const float *norm, float eps, float *xn_out);
+hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
+                              int count, int swiglu);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,

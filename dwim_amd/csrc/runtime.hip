@@ -48,6 +48,14 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
         delete dev;
         return dwim_fail("creating a stream failed");
     }
+    // the activation planes of one-token matrix products (its zero bytes stay zero)
+    if (hipMalloc(&dev->planes, planes_scratch_bytes()) != hipSuccess ||
+        hipMemset(dev->planes, 0, planes_scratch_bytes()) != hipSuccess) {
+        if (dev->planes) hipFree(dev->planes);
+        hipStreamDestroy(dev->stream);
+        delete dev;
+        return dwim_fail("allocating the activation planes failed");
+    }
     *out = dev;
     return 0;
 }
@@ -59,6 +67,7 @@ void dwim_dev_release(dwim_dev *dev) {
     if (dev->partials) hipFree(dev->partials);
     if (dev->argmax_buf) hipFree(dev->argmax_buf);
     if (dev->tokens) hipFree(dev->tokens);
+    if (dev->planes) hipFree(dev->planes);
     hipStreamDestroy(dev->stream);
     delete dev;
 }
@@ -362,6 +371,24 @@ extern "C" int dwim_matmul_add(dwim_dev *dev, dwim_buf *x, const dwim_weight *w,
     DWIM_CHECK(scratch->cap >= x->len, "the scratch buffer is shorter than x");
     if (n == 0) return 0;
     LAUNCH(launch_matvec(dev, w, x->data, input->data, n, 1));
+    return 0;
+}
+
+extern "C" int dwim_prepare(dwim_dev *dev, const dwim_buf *x) {
+    DWIM_CHECK(x->len > 0 && x->len % 256 == 0 && x->len <= 80 * 256,
+               "prepare: one token of whole 256-blocks, at most 20480");
+    LAUNCH(launch_planes(dev, x->data, x->len, nullptr, 0.0f, nullptr));
+    dev->prepared = x->len;
+    return 0;
+}
+
+extern "C" int dwim_matmul_prepared(dwim_dev *dev, dwim_buf *out, const dwim_weight *w) {
+    DWIM_CHECK(w->fmt == DWIM_Q4_K, "matmul_prepared: a Q4_K weight");
+    DWIM_CHECK(dev->prepared == w->cols, "matmul_prepared: no activations of the weight's width prepared");
+    DWIM_CHECK(out->len == w->rows, "matmul_prepared: out must hold one row of results");
+    const int add = 0;
+    float *o = out->data;
+    LAUNCH(launch_mv_q4k_mfma(dev, &w, &o, &add, 1, 0));
     return 0;
 }
 

@@ -78,6 +78,8 @@ SIGNATURES = {
     "dwim_conv": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "dwim_delta_net": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz]),
     "dwim_argmax": (_int, [_vp, _vp, _sz, _u32p]),
+    "dwim_prepare": (_int, [_vp, _vp]),
+    "dwim_matmul_prepared": (_int, [_vp, _vp, _vp]),
     "dwim_embed": (_int, [_vp, _vp, _vp, _u32p, _sz]),
     "dwim_quantize_q4_0_row": (None, [_f32p, _sz, _u16p, _u8p]),
     "dwim_quantize_q8_0_row": (None, [_f32p, _sz, _u16p, _i8p]),
@@ -395,6 +397,14 @@ class Hip:
     def embed(self, out: Buffer, table: Weight, tokens):
         t = np.ascontiguousarray(tokens, np.uint32)
         _check(self.L.dwim_embed(self.h, out.h, table.h, _ptr(t, _u32p), t.size))
+
+    def prepare(self, x: Buffer):
+        """One token's activations as the device's int8 planes, for
+        matmul_prepared (several Q4_K matrices over one x)."""
+        _check(self.L.dwim_prepare(self.h, x.h))
+
+    def matmul_prepared(self, out: Buffer, w: Weight):
+        _check(self.L.dwim_matmul_prepared(self.h, out.h, w.h))
 
     def argmax(self, logits: Buffer, rows: int = 1) -> np.ndarray:
         out = np.empty(rows, np.uint32)

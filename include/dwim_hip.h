@@ -151,6 +151,15 @@ int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_b
  * `rows` indices to `out` (host memory) and waits. */
 int dwim_argmax(dwim_dev *dev, const dwim_buf *logits, size_t rows, uint32_t *out);
 
+/* One activation vector for several Q4_K matrices: dwim_prepare converts the
+ * `cols` activations of x (one token) into the device's int8 planes, which
+ * dwim_matmul_prepared then multiplies by a Q4_K weight of that many columns,
+ * out = w · x, as dwim_matmul does for one token.  The planes are the
+ * device's: the next dwim_prepare, or a one-token Q4_K dwim_matmul,
+ * dwim_matmul_add or dwim_swiglu, replaces them. */
+int dwim_prepare(dwim_dev *dev, const dwim_buf *x);
+int dwim_matmul_prepared(dwim_dev *dev, dwim_buf *out, const dwim_weight *w);
+
 /* out[t] = row tokens[t] of `table` (a rows×cols weight of any format),
  * dequantized: the embedding lookup, which the reference does on the host from
  * the mapped GGUF (qwen35::Pass::embed, inference/qwen35/mod.rs:526-535), on

@@ -158,6 +158,72 @@ def test_q4_k_matvec_at_the_model_shapes(gpu, rows, cols):
     close(gpu.read(out)[::97], want, 1e-4)
 
 
+def test_q4_k_one_token_at_the_edges_of_its_activations(gpu):
+    # one token runs on the int8 matrix cores with x held as 24-bit planes
+    # scaled by max|x|: zeros, one outlier among tiny values, sign patterns
+    rows, cols = 300, 2048
+    w = _k_quantized(O.Q4_K, 45)(rows, cols)
+    gw = gpu.upload(to_tensor(w))
+    rng = np.random.default_rng(7)
+    cases = {"zeros": np.zeros(cols, np.float32),
+             "outlier": np.where(np.arange(cols) == 1000, 3e4, rng.normal(0, 1e-3, cols)).astype(np.float32),
+             "tiny": (rng.normal(0, 1, cols) * 1e-30).astype(np.float32),
+             "signs": np.where(np.arange(cols) % 2, 1.0, -1.0).astype(np.float32),
+             "wide": (rng.normal(0, 1, cols) * 10.0 ** rng.uniform(-6, 3, cols)).astype(np.float32)}
+    for name, x in cases.items():
+        want = O.matmul(w, x)
+        out = gpu.alloc(rows)
+        gpu.matmul(out, gw, gpu.buffer(x))
+        got = gpu.read(out)
+        if name == "tiny":
+            close(got / 1e-30, want / 1e-30, 1e-4)
+        else:
+            close(got, want, 1e-4)
+
+
+def test_prepared_activations_serve_several_matrices(gpu):
+    cols = 1536
+    make = _k_quantized(O.Q4_K, 61)
+    ws = [make(rows, cols) for rows in (64, 300)]
+    x = O.Rng(62).floats(cols)
+    gx = gpu.buffer(x)
+    gws = [gpu.upload(to_tensor(w)) for w in ws]
+    gpu.prepare(gx)
+    for w, gw in zip(ws, gws):
+        out = gpu.alloc(w.rows)
+        gpu.matmul_prepared(out, gw)
+        close(gpu.read(out), O.matmul(w, x), 1e-4)
+    # a one-token matmul replaces the planes: matmul_prepared then refuses
+    gpu.matmul(gpu.alloc(64), gws[0], gx)
+    with pytest.raises(D.DwimError):
+        gpu.matmul_prepared(gpu.alloc(64), gws[0])
+
+
+def test_q4_k_swiglu_and_matmul_add_match_cpu(gpu):
+    rng = O.Rng(24)
+    for rows, cols, n in [(256, 5120, 1), (1024, 1024, 1), (512, 1280, 3), (256, 512, 9)]:
+        make = _k_quantized(O.Q4_K, rows + n)
+        gate, up = make(rows, cols), make(rows, cols)
+        x = rng.floats(n * cols)
+        want = O.silu_mul(O.matmul(gate, x), O.matmul(up, x))
+        out, scratch = gpu.alloc(n * rows), gpu.alloc(n * rows)
+        gpu.swiglu(out, gpu.upload(to_tensor(gate)), gpu.upload(to_tensor(up)), gpu.buffer(x), scratch)
+        if n == 1:
+            close(gpu.read(out), want, 1e-4)
+        else:
+            close_batch(gpu.read(out), want, f"swiglu {rows}x{cols} n={n}")
+        w = make(cols, rows)
+        inp = rng.floats(n * rows)
+        res = rng.floats(n * cols)
+        want = O.add(res, O.matmul(w, inp))
+        out = gpu.buffer(res)
+        gpu.matmul_add(out, gpu.upload(to_tensor(w)), gpu.buffer(inp), gpu.alloc(n * cols))
+        if n == 1:
+            close(gpu.read(out), want, 1e-4)
+        else:
+            close_batch(gpu.read(out) - res, want - res, f"matmul_add {cols}x{rows} n={n}")
+
+
 @pytest.mark.parametrize("fmt", [D.Q4_K, D.Q6_K, D.BF16])
 def test_synthetic_weights_are_the_host_quantizers_bits(gpu, fmt):
     rows, cols = 333, 1024
