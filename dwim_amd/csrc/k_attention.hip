@@ -10,6 +10,7 @@
 // sum of exponentials and weighted values.  Pass 2, one block per (query
 // head, token), merges the chunks.  Each cache byte is read once per token.
 #include "device_util.h"
+#include "planes.h"
 #include "quant_math.h"
 #include "runtime.h"
 
@@ -132,9 +133,10 @@ __global__ void __launch_bounds__(kThreads) k_attn_partial(float *__restrict__ p
     }
 }
 
-// out[t][h] = Σ_c e^(m_c − M) o_c / Σ_c e^(m_c − M) l_c
+// out[t][h] = Σ_c e^(m_c − M) o_c / Σ_c e^(m_c − M) l_c, times sigmoid(gate)
+// when a gate is given (gpu/cpu.rs:244-248); with one token, its planes too.
 __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ out, const float *__restrict__ partials,
-                                                           Shape sh) {
+                                                           Shape sh, const float *__restrict__ gate, planes::View pv) {
     const size_t h = blockIdx.x, t = blockIdx.y;
     const int D = (int)sh.head_dim;
     const float *part = partials + (t * sh.n_heads + h) * sh.chunks * (size_t)(D + 2);
@@ -151,7 +153,11 @@ __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ o
             float m = part[c * (D + 2) + D];
             if (m != -INFINITY) acc += expf(m - M) * part[c * (D + 2) + d];
         }
-        out[(t * sh.n_heads + h) * D + d] = acc / L;
+        const size_t i = (t * sh.n_heads + h) * D + d;
+        float o = acc / L;
+        if (gate) o *= sigmoidf_(gate[i]);
+        out[i] = o;
+        if (pv.q) planes::write32(pv, i, o);  // D is whole groups of 32 lanes
     }
 }
 
@@ -159,6 +165,19 @@ __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ o
 
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k, const dwim_cache *v,
                             size_t n, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads) {
+    return launch_attention_gated(dev, out, q, k, v, n, pos, n_heads, head_dim, n_kv_heads, nullptr, -1);
+}
+
+hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
+                                  const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
+                                  size_t n_kv_heads, const float *gate, int area) {
+    planes::View pv{};
+    if (area >= 0) {
+        if (n != 1 || head_dim % 32 || n_heads * head_dim > planes::kMaxCols || (n_heads * head_dim) % 256)
+            return hipErrorInvalidValue;
+        pv = planes_area(dev, area, n_heads * head_dim);
+        dev->prepared = 0;
+    }
     size_t len = pos + n;
     // Chunks small enough that a lone token spreads over the GPU, at least 32
     // positions (a wave-step of the scoring loop), at most 256.
@@ -182,6 +201,6 @@ hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwi
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     dim3 g2((unsigned)n_heads, (unsigned)n);
-    k_attn_combine<<<g2, kThreads, 0, dev->stream>>>(out, dev->partials, sh);
+    k_attn_combine<<<g2, kThreads, 0, dev->stream>>>(out, dev->partials, sh, gate, pv);
     return hipGetLastError();
 }

@@ -238,55 +238,73 @@ hipError_t launch_conv(hipStream_t s, float *q, float *k, float *v, float *state
 
 // ---------------------------------------------------------------- argmax
 
-// One block per row: each thread scans its stride in increasing order keeping
-// the first maximum, then the block keeps the smallest index of the largest
-// value (qwen35::argmax's strict `>`).
-__global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ logits, size_t cols,
-                                                 uint32_t *__restrict__ out) {
-    __shared__ float bv[16];
-    __shared__ uint32_t bi[16];
-    const float *row = logits + (size_t)blockIdx.x * cols;
+// (best, index) pairs: the larger value wins, the smaller index on a tie; an
+// index of 0xffffffff is "none yet" (qwen35::argmax's strict `>` keeps the
+// first maximum).
+DEV void argmax_merge(float &best, uint32_t &idx, float ov, uint32_t oi) {
+    if (oi != 0xffffffffu && (idx == 0xffffffffu || ov > best || (ov == best && oi < idx))) {
+        best = ov;
+        idx = oi;
+    }
+}
+
+// Pass 1: block (part, row) scans its contiguous share of the row, each
+// thread its stride in increasing order, and leaves the part's first maximum.
+__global__ void __launch_bounds__(256) k_argmax_part(const float *__restrict__ logits, size_t cols, size_t per,
+                                                     float *__restrict__ pv, uint32_t *__restrict__ pi) {
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
+    const size_t row = blockIdx.y, part = blockIdx.x, parts = gridDim.x;
+    const float *r = logits + row * cols;
+    const size_t lo = part * per, hi = lo + per < cols ? lo + per : cols;
     float best = -INFINITY;
     uint32_t idx = 0xffffffffu;
-    for (size_t i = threadIdx.x; i < cols; i += 1024) {
-        float v = row[i];
+    for (size_t i = lo + threadIdx.x; i < hi; i += 256) {
+        const float v = r[i];
         if (idx == 0xffffffffu || v > best) {
             best = v;
             idx = (uint32_t)i;
         }
     }
 #pragma unroll
-    for (int m = 32; m > 0; m >>= 1) {
-        float ov = __shfl_xor(best, m, 64);
-        uint32_t oi = __shfl_xor(idx, m, 64);
-        bool take = oi != 0xffffffffu && (idx == 0xffffffffu || ov > best || (ov == best && oi < idx));
-        if (take) {
-            best = ov;
-            idx = oi;
-        }
-    }
-    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int m = 32; m > 0; m >>= 1) argmax_merge(best, idx, __shfl_xor(best, m, 64), __shfl_xor(idx, m, 64));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) {
         bv[wave] = best;
         bi[wave] = idx;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        float b = bv[0];
-        uint32_t id = bi[0];
-        for (int i = 1; i < 16; i++) {
-            if (bi[i] == 0xffffffffu) continue;
-            if (id == 0xffffffffu || bv[i] > b || (bv[i] == b && bi[i] < id)) {
-                b = bv[i];
-                id = bi[i];
-            }
-        }
-        out[blockIdx.x] = id == 0xffffffffu ? 0u : id;
+        for (int w = 1; w < 4; w++) argmax_merge(best, idx, bv[w], bi[w]);
+        pv[row * parts + part] = best;
+        pi[row * parts + part] = idx;
     }
 }
 
-hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols, uint32_t *out) {
-    k_argmax<<<(unsigned)rows, 1024, 0, s>>>(logits, cols, out);
+// Pass 2: a wave per row merges its parts (at most 64).
+__global__ void __launch_bounds__(64) k_argmax_merge(const float *__restrict__ pv, const uint32_t *__restrict__ pi,
+                                                     size_t parts, uint32_t *__restrict__ out) {
+    const size_t row = blockIdx.x;
+    const int lane = threadIdx.x;
+    float best = lane < (int)parts ? pv[row * parts + lane] : -INFINITY;
+    uint32_t idx = lane < (int)parts ? pi[row * parts + lane] : 0xffffffffu;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) argmax_merge(best, idx, __shfl_xor(best, m, 64), __shfl_xor(idx, m, 64));
+    if (lane == 0) out[row] = idx == 0xffffffffu ? 0u : idx;
+}
+
+size_t argmax_scratch_words(size_t rows) { return rows * (1 + 2 * 64); }
+
+// scratch: argmax_scratch_words(rows) words; the indices land in its first `rows`
+hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols, uint32_t *scratch) {
+    const size_t parts = cols >= 64 * 1024 ? 64 : (cols + 1023) / 1024;
+    const size_t per = (cols + parts - 1) / parts;
+    float *pv = (float *)(scratch + rows);
+    uint32_t *pi = scratch + rows + rows * 64;
+    k_argmax_part<<<dim3((unsigned)parts, (unsigned)rows), 256, 0, s>>>(logits, cols, per, pv, pi);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_argmax_merge<<<(unsigned)rows, 64, 0, s>>>(pv, pi, parts, scratch);
     return hipGetLastError();
 }
 

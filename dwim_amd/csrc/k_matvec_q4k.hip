@@ -306,9 +306,9 @@ Args base_args(size_t cols) {
 
 hipError_t launch_matvec_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
     if (n == 1) {
-        hipError_t e = launch_planes(dev, x, w->cols, nullptr, 0.0f, nullptr);
+        hipError_t e = launch_planes(dev, x, w->cols, nullptr, 0.0f, nullptr, 0);
         if (e != hipSuccess) return e;
-        return launch_mv_q4k_mfma(dev, &w, &out, &add, 1, 0);
+        return launch_mv_q4k_mfma(dev, &w, &out, &add, 1, 0, 0);
     }
     Args a = base_args(w->cols);
     a.job[0] = Job{(const uint8_t *)w->q, w->rows, out, add};
@@ -323,9 +323,9 @@ hipError_t launch_matvec_q4k_multi(dwim_dev *dev, const dwim_weight *const *ws, 
     for (int j = 0; j < count; j++)
         if (ws[j]->cols != ws[0]->cols || ws[j]->fmt != DWIM_Q4_K) return hipErrorInvalidValue;
     if (n == 1) {
-        hipError_t e = launch_planes(dev, x, ws[0]->cols, norm, eps, norm ? xn_out : nullptr);
+        hipError_t e = launch_planes(dev, x, ws[0]->cols, norm, eps, norm ? xn_out : nullptr, 0);
         if (e != hipSuccess) return e;
-        return launch_mv_q4k_mfma(dev, ws, outs, nullptr, count, 0);
+        return launch_mv_q4k_mfma(dev, ws, outs, nullptr, count, 0, 0);
     }
     Args a = base_args(ws[0]->cols);
     for (int j = 0; j < count; j++) a.job[j] = Job{(const uint8_t *)ws[j]->q, ws[j]->rows, outs[j], 0};
@@ -341,11 +341,11 @@ hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_
                              size_t n, const float *norm, float eps) {
     if (gate->rows != up->rows || gate->cols != up->cols) return hipErrorInvalidValue;
     if (n == 1) {
-        hipError_t e = launch_planes(dev, x, gate->cols, norm, eps, nullptr);
+        hipError_t e = launch_planes(dev, x, gate->cols, norm, eps, nullptr, 0);
         if (e != hipSuccess) return e;
         const dwim_weight *ws[2] = {gate, up};
         float *outs[2] = {out, nullptr};
-        return launch_mv_q4k_mfma(dev, ws, outs, nullptr, 2, 1);
+        return launch_mv_q4k_mfma(dev, ws, outs, nullptr, 2, 1, 0);
     }
     Args a = base_args(gate->cols);
     a.job[0] = Job{(const uint8_t *)gate->q, gate->rows, out, 0};

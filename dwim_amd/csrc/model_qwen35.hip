@@ -211,11 +211,19 @@ struct dwim_model {
         return dwim_normalize(dev, out, in, weight, rows * c.hidden, c.eps);
     }
 
-    // Q4_K projections of a layer's input fused with its normalization: one
-    // launch normalizes x in LDS and runs every matrix that reads it
+    // The fused path: Q4_K matrices with rows of whole 256-blocks, heads the
+    // fused kernels take.  One token goes through the int8 matrix cores, the
+    // activations of each product handed over as planes (plane area 0);
+    // several tokens through the f32 matrix kernels.
     bool fusable(const Layer &l) const {
-        return fuse && (l.attention ? l.q->fmt : l.qkv->fmt) == DWIM_Q4_K && l.gate->fmt == DWIM_Q4_K &&
-               c.hidden % 256 == 0 && c.hidden <= 10240;
+        const bool shapes = c.hidden % 256 == 0 && c.hidden <= 10240 && c.intermediate % 256 == 0 &&
+                            c.intermediate <= 80 * 256 && (c.state_dim == 128 || c.state_dim == 256) &&
+                            c.head_dim % 64 == 0 && c.head_dim <= 256 && q_dim() % 256 == 0 && v_dim() % 256 == 0;
+        const bool formats = (l.attention ? (l.q->fmt == DWIM_Q4_K && l.qgate->fmt == DWIM_Q4_K && l.k->fmt == DWIM_Q4_K &&
+                                             l.v->fmt == DWIM_Q4_K && l.o->fmt == DWIM_Q4_K)
+                                          : (l.qkv->fmt == DWIM_Q4_K && l.z->fmt == DWIM_Q4_K && l.out->fmt == DWIM_Q4_K)) &&
+                             l.gate->fmt == DWIM_Q4_K && l.up->fmt == DWIM_Q4_K && l.down->fmt == DWIM_Q4_K;
+        return fuse && shapes && formats;
     }
     int projections(const dwim_weight *const *ws, dwim_buf *const *outs, int count, const dwim_buf *norm_w,
                     size_t n, dwim_buf *xn_out) {
@@ -225,12 +233,19 @@ struct dwim_model {
                                          xn_out ? xn_out->data : nullptr));
         return 0;
     }
+    // x += w · (the activations in plane area 0), one token
+    int add_planes(const dwim_weight *w) {
+        float *o = x->data;
+        const int add = 1;
+        DWIM_HIP(launch_mv_q4k_mfma(dev, &w, &o, &add, 1, 0, 0));
+        return 0;
+    }
 
     // Pass::layer (qwen35/mod.rs:541-655), the verify-free path
     int layer(const Layer &l, size_t n, size_t pos) {
         const float eps = c.eps;
-        const bool fused = fusable(l);
-        if (!fused || !l.attention) TRY(dwim_resize(dev, xh, n * c.hidden));
+        const bool fused = fusable(l), one = fused && n == 1;
+        TRY(dwim_resize(dev, xh, n * c.hidden));
         if (!fused) TRY(normalize(xh, x, l.attn_norm, n));
         if (l.attention) {
             TRY(dwim_resize(dev, q, n * q_dim()));
@@ -238,51 +253,75 @@ struct dwim_model {
             TRY(dwim_resize(dev, k, n * kv_dim()));
             TRY(dwim_resize(dev, v, n * kv_dim()));
             TRY(dwim_resize(dev, att, n * q_dim()));
+            dwim_cache *kc = seq.k_cache[l.cache], *vc = seq.v_cache[l.cache];
             if (fused) {
                 const dwim_weight *ws[4] = {l.q, l.qgate, l.k, l.v};
                 dwim_buf *outs[4] = {q, gate, k, v};
                 TRY(projections(ws, outs, 4, l.attn_norm, n, nullptr));
+                DWIM_HIP(launch_qk_prep(dev->stream, q->data, k->data, v->data, l.q_norm->data, l.k_norm->data,
+                                        rope->data, n, pos, c.heads, c.kv_heads, c.head_dim, c.rot_dim, eps, kc, vc));
+                DWIM_HIP(launch_attention_gated(dev, att->data, q->data, kc, vc, n, pos, c.heads, c.head_dim,
+                                                c.kv_heads, gate->data, one ? 0 : -1));
+                if (one) TRY(add_planes(l.o));
+                else TRY(dwim_matmul_add(dev, x, l.o, att, xb));
             } else {
                 TRY(dwim_matmul(dev, q, l.q, xh));
                 TRY(dwim_matmul(dev, gate, l.qgate, xh));
                 TRY(dwim_matmul(dev, k, l.k, xh));
                 TRY(dwim_matmul(dev, v, l.v, xh));
+                TRY(dwim_rmsnorm(dev, q, l.q_norm, eps));
+                TRY(dwim_rmsnorm(dev, k, l.k_norm, eps));
+                TRY(dwim_rope(dev, q, rope, pos, c.heads, c.head_dim, c.rot_dim));
+                TRY(dwim_rope(dev, k, rope, pos, c.kv_heads, c.head_dim, c.rot_dim));
+                TRY(dwim_store(dev, kc, pos * kv_dim(), k));
+                TRY(dwim_store(dev, vc, pos * kv_dim(), v));
+                TRY(dwim_attention(dev, att, q, kc, vc, pos, c.heads, c.head_dim, c.kv_heads));
+                TRY(dwim_sigmoid_mul(dev, att, gate));
+                TRY(dwim_matmul_add(dev, x, l.o, att, xb));
             }
-            TRY(dwim_rmsnorm(dev, q, l.q_norm, eps));
-            TRY(dwim_rmsnorm(dev, k, l.k_norm, eps));
-            TRY(dwim_rope(dev, q, rope, pos, c.heads, c.head_dim, c.rot_dim));
-            TRY(dwim_rope(dev, k, rope, pos, c.kv_heads, c.head_dim, c.rot_dim));
-            TRY(dwim_store(dev, seq.k_cache[l.cache], pos * kv_dim(), k));
-            TRY(dwim_store(dev, seq.v_cache[l.cache], pos * kv_dim(), v));
-            TRY(dwim_attention(dev, att, q, seq.k_cache[l.cache], seq.v_cache[l.cache], pos, c.heads, c.head_dim,
-                               c.kv_heads));
-            TRY(dwim_sigmoid_mul(dev, att, gate));
-            TRY(dwim_matmul_add(dev, x, l.o, att, xb));
         } else {
             TRY(dwim_resize(dev, q, n * k_dim()));
             TRY(dwim_resize(dev, k, n * k_dim()));
             TRY(dwim_resize(dev, v, n * v_dim()));
             TRY(dwim_resize(dev, att, n * v_dim()));
+            auto &pair = seq.conv_state[l.slot];
+            dwim_buf *state = seq.parity ? pair[0] : pair[1];
+            dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
             if (fused) {
                 const dwim_weight *ws[2] = {l.qkv, l.z};
                 dwim_buf *outs[2] = {qkv, z};
                 TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
+                TRY(dwim_matmul(dev, ab, l.ab, xh));
+                DWIM_HIP(launch_conv_l2(dev->stream, q->data, k->data, v->data, state_out->data, qkv->data,
+                                        state->data, l.conv->data, n, k_dim(), k_dim(), v_dim(), c.state_dim, eps));
+                TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, seq.ssm_state[l.slot], c.k_heads, c.v_heads,
+                                   c.state_dim));
+                DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps,
+                                           one ? 0 : -1));
+                if (one) TRY(add_planes(l.out));
+                else TRY(dwim_matmul_add(dev, x, l.out, z, xb));
             } else {
                 TRY(dwim_matmul(dev, qkv, l.qkv, xh));
                 TRY(dwim_matmul(dev, z, l.z, xh));
+                TRY(dwim_matmul(dev, ab, l.ab, xh));
+                TRY(dwim_conv(dev, q, k, v, state_out, qkv, state, l.conv));
+                TRY(dwim_l2norm(dev, q, c.state_dim, eps));
+                TRY(dwim_l2norm(dev, k, c.state_dim, eps));
+                TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, seq.ssm_state[l.slot], c.k_heads, c.v_heads,
+                                   c.state_dim));
+                TRY(dwim_rmsnorm(dev, att, l.norm, eps));
+                TRY(dwim_silu_mul(dev, z, att));
+                TRY(dwim_matmul_add(dev, x, l.out, z, xb));
             }
-            TRY(dwim_matmul(dev, ab, l.ab, xh));
-            auto &pair = seq.conv_state[l.slot];
-            dwim_buf *state = seq.parity ? pair[0] : pair[1];
-            dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
-            TRY(dwim_conv(dev, q, k, v, state_out, qkv, state, l.conv));
-            TRY(dwim_l2norm(dev, q, c.state_dim, eps));
-            TRY(dwim_l2norm(dev, k, c.state_dim, eps));
-            TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, seq.ssm_state[l.slot], c.k_heads, c.v_heads,
-                               c.state_dim));
-            TRY(dwim_rmsnorm(dev, att, l.norm, eps));
-            TRY(dwim_silu_mul(dev, z, att));
-            TRY(dwim_matmul_add(dev, x, l.out, z, xb));
+        }
+        if (one) {
+            // norm → planes → gate/up pair → planes of its result → x += down · them
+            DWIM_HIP(launch_planes(dev, x->data, c.hidden, l.mlp_norm->data, eps, nullptr, 0));
+            const dwim_weight *ws[2] = {l.gate, l.up};
+            float *outs[2] = {up->data, nullptr};
+            DWIM_HIP(launch_mv_q4k_mfma(dev, ws, outs, nullptr, 2, 1, 0));
+            DWIM_HIP(launch_planes(dev, up->data, c.intermediate, nullptr, eps, nullptr, 0));
+            return add_planes(l.down);
         }
         if (fused) {
             DWIM_HIP(launch_swiglu_q4k(dev, l.gate, l.up, up->data, x->data, n, l.mlp_norm->data, eps));

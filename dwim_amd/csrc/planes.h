@@ -1,0 +1,89 @@
+// One token's activations as the int8 matrix cores take them (the
+// "planes"): per group of 32 activations, s = max|x| / 8355000 and
+// X = rint(x / s) split into balanced base-256 digits X = 65536·X2 + 256·X1 +
+// X0 (each in [-128, 127]), written as three int8 rows [3][cols]; beside them,
+// per pair of groups, their two f32 sums and their two scales.  A device holds
+// two such areas, so that a kernel can read one and write the other.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace planes {
+
+constexpr size_t kMaxCols = 80 * 256;
+constexpr int kMax = 8355711;          // 127·(65536 + 256 + 1): every digit within int8
+constexpr float kScale = 8355000.0f;   // max|x| maps here, rounding well inside kMax
+constexpr size_t kStatOff = 3 * kMaxCols;                       // bytes
+constexpr size_t kZerosOff = kStatOff + 8 * (kMaxCols / 32);    // 64 zero bytes
+constexpr size_t kAreaBytes = kZerosOff + 256;
+
+struct View {
+    int8_t *q;      // [3][cols]
+    float *stat;    // [cols/64][4]: sum(2k), sum(2k+1), scale(2k), scale(2k+1)
+    size_t cols;
+};
+
+__host__ __device__ inline View view(void *area, size_t cols) {
+    int8_t *p = (int8_t *)area;
+    return View{p, (float *)(p + kStatOff), cols};
+}
+
+__device__ __forceinline__ void digits(float x, float inv, int &d0, int &d1, int &d2) {
+    const int X = min(max((int)rintf(x * inv), -kMax), kMax);
+    d0 = ((X + 128) & 255) - 128;
+    const int X1 = (X - d0) >> 8;
+    d1 = ((X1 + 128) & 255) - 128;
+    d2 = (X1 - d1) >> 8;
+}
+
+__device__ __forceinline__ void put_stat(const View &v, size_t group, float sum, float m) {
+    v.stat[(group / 2) * 4 + group % 2] = sum;
+    v.stat[(group / 2) * 4 + 2 + group % 2] = m / kScale;
+}
+
+// Activation i = 32·group + lane of a group that 32 consecutive lanes (a
+// 32-aligned run of the wave) hold one each.
+__device__ __forceinline__ void write32(const View &v, size_t i, float x) {
+    float m = fabsf(x), s = x;
+#pragma unroll
+    for (int k = 16; k > 0; k >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, k, 64));
+        s += __shfl_xor(s, k, 64);
+    }
+    const float inv = m > 0.0f ? kScale / m : 0.0f;
+    int d0, d1, d2;
+    digits(x, inv, d0, d1, d2);
+    v.q[i] = (int8_t)d0;
+    v.q[v.cols + i] = (int8_t)d1;
+    v.q[2 * v.cols + i] = (int8_t)d2;
+    if ((i & 31) == 0) put_stat(v, i / 32, s, m);
+}
+
+// Activations 4j..4j+3 of a group that 8 consecutive (8-aligned) lanes hold
+// four each.
+__device__ __forceinline__ void write8x4(const View &v, size_t j, float4 x) {
+    float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+    float s = (x.x + x.y) + (x.z + x.w);
+#pragma unroll
+    for (int k = 4; k > 0; k >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, k, 64));
+        s += __shfl_xor(s, k, 64);
+    }
+    const float inv = m > 0.0f ? kScale / m : 0.0f;
+    const float e[4] = {x.x, x.y, x.z, x.w};
+    uint32_t p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int d0, d1, d2;
+        digits(e[k], inv, d0, d1, d2);
+        p0 |= (uint32_t)(d0 & 255) << (8 * k);
+        p1 |= (uint32_t)(d1 & 255) << (8 * k);
+        p2 |= (uint32_t)(d2 & 255) << (8 * k);
+    }
+    ((uint32_t *)v.q)[j] = p0;
+    ((uint32_t *)(v.q + v.cols))[j] = p1;
+    ((uint32_t *)(v.q + 2 * v.cols))[j] = p2;
+    if ((j & 7) == 0) put_stat(v, j / 8, s, m);
+}
+
+}  // namespace planes

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "dwim_hip.h"
+#include "planes.h"
 
 struct dwim_dev {
     int index = 0;
@@ -97,15 +98,18 @@ hipError_t launch_matvec_q4k_multi(dwim_dev *dev, const dwim_weight *const *ws, 
 // out = silu(gate·x) · (up·x) for Q4_K gate and up, x optionally RMS-normalized
 hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                              const float *x, size_t n, const float *norm, float eps);
-// One token on the int8 matrix cores: launch_planes writes x's planes (RMS-
-// normalized by `norm` when given, the normalized x also to xn_out when
-// given) into the device's scratch; launch_mv_q4k_mfma then runs up to four
-// matrices over them (outs[j] += or = W_j·x by adds[j]), or gate and up as a
-// SwiGLU pair (swiglu = 1, count = 2, the result in outs[0]).
+// One token on the int8 matrix cores (planes.h): launch_planes writes x's
+// planes (RMS-normalized by `norm` when given, the normalized x also to
+// xn_out when given) into plane area `area` (0 or 1) of the device;
+// launch_mv_q4k_mfma then runs up to four matrices over that area
+// (outs[j] += or = W_j·x by adds[j]), or gate and up as a SwiGLU pair
+// (swiglu = 1, count = 2, the result in outs[0]).
 size_t planes_scratch_bytes();
-hipError_t launch_planes(dwim_dev *dev, const float *x, size_t cols, const float *norm, float eps, float *xn_out);
+planes::View planes_area(dwim_dev *dev, int area, size_t cols);
+hipError_t launch_planes(dwim_dev *dev, const float *x, size_t cols, const float *norm, float eps, float *xn_out,
+                         int area);
 hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
-                              int count, int swiglu);
+                              int count, int swiglu, int area);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
@@ -119,11 +123,30 @@ hipError_t launch_delta_net(hipStream_t s, float *out, const float *q, const flo
                             size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim);
 hipError_t launch_embed(hipStream_t s, float *out, const dwim_weight *w, const uint32_t *tokens,
                         size_t n);
-hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols,
-                         uint32_t *out);
+// first index of each row's maximum, into the first `rows` words of scratch
+// (argmax_scratch_words(rows) words)
+size_t argmax_scratch_words(size_t rows);
+hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols, uint32_t *scratch);
 hipError_t launch_synthetic_q4_k(hipStream_t s, uint8_t *tiled, size_t rows, size_t cols,
                                  uint64_t seed, float c);
 hipError_t launch_synthetic_q6_k(hipStream_t s, uint8_t *ql, uint8_t *qh, int8_t *sc,
                                  uint16_t *d, size_t rows, size_t cols, uint64_t seed, float c);
 hipError_t launch_synthetic_bf16(hipStream_t s, uint16_t *q, size_t rows, size_t cols,
                                  uint64_t seed, float c);
+
+// ---- fused launches of the model host (k_fused.hip, k_attention.hip) ----
+hipError_t launch_conv_l2(hipStream_t s, float *q, float *k, float *v, float *state_out, const float *x,
+                          const float *state, const float *w, size_t n, size_t qd, size_t kd, size_t vd, size_t dim,
+                          float eps);
+// z = silu(z) · rmsnorm(att, w) per dim-row of the n·total values; area >= 0
+// (one token): the result's planes into that plane area too
+hipError_t launch_gated_norm(dwim_dev *dev, float *z, const float *att, const float *w, size_t n, size_t total,
+                             size_t dim, float eps, int area);
+hipError_t launch_qk_prep(hipStream_t s, float *q, float *k, const float *v, const float *q_norm,
+                          const float *k_norm, const float *table, size_t n, size_t pos, size_t heads,
+                          size_t kv_heads, size_t head_dim, size_t rot, float eps, dwim_cache *kc, dwim_cache *vc);
+// attention, then out *= sigmoid(gate) when gate is given, and (one token,
+// area >= 0) out's planes into that plane area
+hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
+                                  const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
+                                  size_t n_kv_heads, const float *gate, int area);

@@ -377,7 +377,7 @@ extern "C" int dwim_matmul_add(dwim_dev *dev, dwim_buf *x, const dwim_weight *w,
 extern "C" int dwim_prepare(dwim_dev *dev, const dwim_buf *x) {
     DWIM_CHECK(x->len > 0 && x->len % 256 == 0 && x->len <= 80 * 256,
                "prepare: one token of whole 256-blocks, at most 20480");
-    LAUNCH(launch_planes(dev, x->data, x->len, nullptr, 0.0f, nullptr));
+    LAUNCH(launch_planes(dev, x->data, x->len, nullptr, 0.0f, nullptr, 0));
     dev->prepared = x->len;
     return 0;
 }
@@ -388,7 +388,7 @@ extern "C" int dwim_matmul_prepared(dwim_dev *dev, dwim_buf *out, const dwim_wei
     DWIM_CHECK(out->len == w->rows, "matmul_prepared: out must hold one row of results");
     const int add = 0;
     float *o = out->data;
-    LAUNCH(launch_mv_q4k_mfma(dev, &w, &o, &add, 1, 0));
+    LAUNCH(launch_mv_q4k_mfma(dev, &w, &o, &add, 1, 0, 0));
     return 0;
 }
 
@@ -533,7 +533,7 @@ extern "C" int dwim_argmax(dwim_dev *dev, const dwim_buf *logits, size_t rows, u
         if (dev->argmax_buf) hipFree(dev->argmax_buf);
         dev->argmax_buf = nullptr;
         dev->argmax_cap = 0;
-        DWIM_HIP(hipMalloc(&dev->argmax_buf, rows * 4));
+        DWIM_HIP(hipMalloc(&dev->argmax_buf, argmax_scratch_words(rows) * 4));
         dev->argmax_cap = rows;
     }
     LAUNCH(launch_argmax(dev->stream, logits->data, rows, logits->len / rows, dev->argmax_buf));

@@ -441,3 +441,10 @@ def test_argmax_takes_the_first_maximum(gpu):
     want = [O.argmax(logits[r * cols:(r + 1) * cols]) for r in range(rows)]
     assert list(got) == want
     assert got[1] == 7 and got[3] == cols - 1
+    # ties in different parts of a long row, and rows shorter than a part
+    logits = np.full(cols, -1.0, np.float32)
+    logits[[200_000, 100_000, 150_001]] = 3.0
+    assert gpu.argmax(gpu.buffer(logits))[0] == 100_000
+    for n in (1, 63, 1000, 1025):
+        x = rng.floats(n)
+        assert gpu.argmax(gpu.buffer(x))[0] == O.argmax(x)
