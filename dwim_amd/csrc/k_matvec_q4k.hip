@@ -304,7 +304,11 @@ Args base_args(size_t cols) {
 
 }  // namespace
 
+// Batches of at least kGemmTokens go through the f16 matrix-core GEMM.
+constexpr size_t kGemmTokens = 16;
+
 hipError_t launch_matvec_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
+    if (n >= kGemmTokens) return launch_gemm_q4k(dev, w, out, x, n, add);
     if (n == 1) {
         hipError_t e = launch_planes(dev, x, w->cols, nullptr, 0.0f, nullptr, 0);
         if (e != hipSuccess) return e;
@@ -327,6 +331,21 @@ hipError_t launch_matvec_q4k_multi(dwim_dev *dev, const dwim_weight *const *ws, 
         if (e != hipSuccess) return e;
         return launch_mv_q4k_mfma(dev, ws, outs, nullptr, count, 0, 0);
     }
+    if (n >= kGemmTokens) {
+        const float *in = x;
+        if (norm) {
+            float *xn = xn_out ? xn_out : dev_work(dev, n * ws[0]->cols);
+            if (!xn) return hipErrorOutOfMemory;
+            hipError_t e = launch_rmsnorm(dev->stream, xn, x, norm, n, ws[0]->cols, eps);
+            if (e != hipSuccess) return e;
+            in = xn;
+        }
+        for (int j = 0; j < count; j++) {
+            hipError_t e = launch_gemm_q4k(dev, ws[j], outs[j], in, n, 0);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     Args a = base_args(ws[0]->cols);
     for (int j = 0; j < count; j++) a.job[j] = Job{(const uint8_t *)ws[j]->q, ws[j]->rows, outs[j], 0};
     a.njobs = count;
@@ -346,6 +365,23 @@ hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_
         const dwim_weight *ws[2] = {gate, up};
         float *outs[2] = {out, nullptr};
         return launch_mv_q4k_mfma(dev, ws, outs, nullptr, 2, 1, 0);
+    }
+    if (n >= kGemmTokens) {
+        // x normalized, gate·x into out, up·x into the work scratch, then silu(out)·up
+        const size_t cols = gate->cols, rows = gate->rows;
+        float *work = dev_work(dev, n * rows + (norm ? n * cols : 0));
+        if (!work) return hipErrorOutOfMemory;
+        const float *in = x;
+        if (norm) {
+            float *xn = work + n * rows;
+            hipError_t e = launch_rmsnorm(dev->stream, xn, x, norm, n, cols, eps);
+            if (e != hipSuccess) return e;
+            in = xn;
+        }
+        hipError_t e = launch_gemm_q4k(dev, gate, out, in, n, 0);
+        if (e == hipSuccess) e = launch_gemm_q4k(dev, up, work, in, n, 0);
+        if (e == hipSuccess) e = launch_silu_mul(dev->stream, out, work, n * rows);
+        return e;
     }
     Args a = base_args(gate->cols);
     a.job[0] = Job{(const uint8_t *)gate->q, gate->rows, out, 0};

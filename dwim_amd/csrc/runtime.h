@@ -26,6 +26,10 @@ struct dwim_dev {
     size_t tokens_cap = 0;
     void *planes = nullptr;  // one token's int8 activation planes (planes_scratch_bytes())
     size_t prepared = 0;     // width of the planes dwim_prepare wrote (0: none, or replaced)
+    void *split = nullptr;   // the f16 hi/lo parts of a batch's activations (k_gemm_q4k)
+    size_t split_cap = 0;    // bytes
+    float *work = nullptr;   // normalized activations / a product's second result
+    size_t work_cap = 0;     // floats
     // The open handle and every live buffer, weight and cache hold a
     // reference: the device (its stream) outlives whatever was made on it,
     // whichever order a binding frees them in.
@@ -150,3 +154,10 @@ hipError_t launch_qk_prep(hipStream_t s, float *q, float *k, const float *v, con
 hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                                   const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
                                   size_t n_kv_heads, const float *gate, int area);
+
+// ---- batches of tokens (k_gemm_q4k.hip) ----
+// out (+)= w · x for n tokens on the f16 matrix cores (x's hi/lo parts are
+// written to the device's split scratch first)
+hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n, int add);
+// the device's work scratch, grown to at least `floats`
+float *dev_work(dwim_dev *dev, size_t floats);

@@ -60,6 +60,17 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
     return 0;
 }
 
+float *dev_work(dwim_dev *dev, size_t floats) {
+    if (dev->work_cap < floats) {
+        if (dev->work) hipFree(dev->work);
+        dev->work = nullptr;
+        dev->work_cap = 0;
+        if (hipMalloc(&dev->work, floats * sizeof(float)) != hipSuccess) return nullptr;
+        dev->work_cap = floats;
+    }
+    return dev->work;
+}
+
 void dwim_dev_release(dwim_dev *dev) {
     if (--dev->refs > 0) return;
     hipSetDevice(dev->index);
@@ -68,6 +79,8 @@ void dwim_dev_release(dwim_dev *dev) {
     if (dev->argmax_buf) hipFree(dev->argmax_buf);
     if (dev->tokens) hipFree(dev->tokens);
     if (dev->planes) hipFree(dev->planes);
+    if (dev->split) hipFree(dev->split);
+    if (dev->work) hipFree(dev->work);
     hipStreamDestroy(dev->stream);
     delete dev;
 }
