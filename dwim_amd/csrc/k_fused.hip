@@ -61,6 +61,48 @@ __global__ void __launch_bounds__(256) k_conv_l2(float *__restrict__ q, float *_
     state_out[2 * ch + c] = s2;
 }
 
+// The same for a batch: a block of `dim` threads per (`dim` channels, token),
+// every token at once (the window reads the previous tokens' inputs, or the
+// carried state before the first).
+__global__ void __launch_bounds__(256) k_conv_l2_batch(float *__restrict__ q, float *__restrict__ k,
+                                                       float *__restrict__ v, float *__restrict__ state_out,
+                                                       const float *__restrict__ x, const float *__restrict__ state,
+                                                       const float *__restrict__ w, size_t n, size_t qd, size_t kd,
+                                                       size_t vd, float eps) {
+    __shared__ float red[4];
+    const size_t ch = qd + kd + vd;
+    const size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+    // input t' of the window: x[t'] for t' >= 0, else the state's row 3 + t'
+    float in[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const long tp = (long)t + j - 3;
+        in[j] = tp >= 0 ? x[(size_t)tp * ch + c] : state[(size_t)(3 + tp) * ch + c];
+    }
+    float acc = 0.0f;
+    acc += w[c * 4] * in[0];
+    acc += w[c * 4 + 1] * in[1];
+    acc += w[c * 4 + 2] * in[2];
+    acc += w[c * 4 + 3] * in[3];
+    float y = acc * sigmoidf_(acc);
+    float *dst;
+    size_t stride, col;
+    bool norm = true;
+    if (c < qd) { dst = q; stride = qd; col = c; }
+    else if (c < qd + kd) { dst = k; stride = kd; col = c - qd; }
+    else { dst = v; stride = vd; col = c - qd - kd; norm = false; }
+    if (norm) {  // uniform over the block
+        const float ss = block_sum(y * y, red);
+        y = y * (1.0f / sqrtf(ss + eps));
+    }
+    dst[t * stride + col] = y;
+    if (t == n - 1) {
+        // the last three inputs carry over
+#pragma unroll
+        for (int j = 0; j < 3; j++) state_out[(size_t)j * ch + c] = in[j + 1];
+    }
+}
+
 // z = silu(z) · (att · (1/rms(att) · w)) per `dim`-row (rmsnorm, gpu/cpu.rs:
 // 157-166, then silu_mul, :238-242), four values a thread; with one token,
 // the result's planes too.
@@ -151,8 +193,12 @@ hipError_t launch_conv_l2(hipStream_t s, float *q, float *k, float *v, float *st
                           const float *state, const float *w, size_t n, size_t qd, size_t kd, size_t vd, size_t dim,
                           float eps) {
     if (dim % 64 || dim > 256 || qd % dim || kd % dim || vd % dim) return hipErrorInvalidValue;
-    k_conv_l2<<<(unsigned)((qd + kd + vd) / dim), (unsigned)dim, 0, s>>>(q, k, v, state_out, x, state, w, n, qd, kd,
-                                                                         vd, eps);
+    if (n == 1)
+        k_conv_l2<<<(unsigned)((qd + kd + vd) / dim), (unsigned)dim, 0, s>>>(q, k, v, state_out, x, state, w, n, qd,
+                                                                             kd, vd, eps);
+    else
+        k_conv_l2_batch<<<dim3((unsigned)((qd + kd + vd) / dim), (unsigned)n), (unsigned)dim, 0, s>>>(
+            q, k, v, state_out, x, state, w, n, qd, kd, vd, eps);
     return hipGetLastError();
 }
 

@@ -256,6 +256,49 @@ hipError_t launch_fmt(hipStream_t s, const Weights &w, const float *x, float *ou
 
 }  // namespace
 
+// Batches through a bf16 matrix of few rows (at most 128, as DeltaNet's
+// gate projection has): a block per 8 tokens, the rows' k-slice transposed in
+// LDS so that the threads of a token read consecutive rows, f32 sums in k
+// order as the reference's dot product keeps them per lane (gpu/cpu.rs:370-384
+// sums 8 lanes; the tolerance covers the order).
+constexpr int kSkTok = 8, kSkK = 64;
+
+__global__ void __launch_bounds__(256) k_skinny_bf16(const uint16_t *__restrict__ w, const float *__restrict__ x,
+                                                     float *__restrict__ out, size_t rows, size_t cols, size_t n,
+                                                     int add) {
+    __shared__ float wt[kSkK][129];  // [k][row], padded
+    __shared__ float xs[kSkTok][kSkK];
+    const int tid = threadIdx.x, tt = tid >> 5, rg = tid & 31;  // token tt, rows rg + 32i
+    const size_t t0 = (size_t)blockIdx.x * kSkTok;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (size_t k0 = 0; k0 < cols; k0 += kSkK) {
+        for (int i = tid; i < kSkK * 128; i += 256) {
+            const int r = i / kSkK, k = i % kSkK;
+            wt[k][r] = r < (int)rows ? dq::bf16_to_f32(w[r * cols + k0 + k]) : 0.0f;
+        }
+        for (int i = tid; i < kSkTok * kSkK; i += 256) {
+            const int t = i / kSkK, k = i % kSkK;
+            xs[t][k] = t0 + t < n ? x[(t0 + t) * cols + k0 + k] : 0.0f;
+        }
+        __syncthreads();
+        for (int k = 0; k < kSkK; k++) {
+            const float xv = xs[tt][k];
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] += wt[k][rg + 32 * i] * xv;
+        }
+        __syncthreads();
+    }
+    if (t0 + tt >= n) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const size_t r = rg + 32 * i;
+        if (r < rows) {
+            float *o = out + (t0 + tt) * rows + r;
+            *o = add ? *o + acc[i] : acc[i];
+        }
+    }
+}
+
 hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const float *x, size_t n, int add) {
     hipStream_t s = dev->stream;
     Weights w{wt->q, wt->s, wt->s2, wt->s3, wt->rows, wt->cols};
@@ -264,7 +307,13 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
     case DWIM_Q6_K: return launch_fmt<DWIM_Q6_K>(s, w, x, out, n, add);
     case DWIM_Q4_0: return launch_fmt<DWIM_Q4_0>(s, w, x, out, n, add);
     case DWIM_Q8_0: return launch_fmt<DWIM_Q8_0>(s, w, x, out, n, add);
-    default: return launch_fmt<DWIM_BF16>(s, w, x, out, n, add);
+    default:
+        if (n >= 16 && wt->rows <= 128 && wt->cols % kSkK == 0) {
+            k_skinny_bf16<<<(unsigned)((n + kSkTok - 1) / kSkTok), 256, 0, s>>>((const uint16_t *)wt->q, x, out,
+                                                                               wt->rows, wt->cols, n, add);
+            return hipGetLastError();
+        }
+        return launch_fmt<DWIM_BF16>(s, w, x, out, n, add);
     }
 }
 

@@ -94,6 +94,18 @@ def test_matmul_matches_cpu(gpu):
         close(gpu.read(out), want, 1e-4)
 
 
+def test_bf16_batches_through_few_rows_match_cpu(gpu):
+    # DeltaNet's gate projection shape (96 x 5120) and ragged batches
+    rng = O.Rng(5)
+    for rows, cols, n in [(96, 5120, 40), (128, 1024, 17), (3, 64, 300)]:
+        w = rng.bf16(rows, cols)
+        x = rng.floats(n * cols)
+        want = O.matmul(w, x)
+        out = gpu.alloc(n * rows)
+        gpu.matmul(out, gpu.upload(to_tensor(w)), gpu.buffer(x))
+        close(gpu.read(out), want, 1e-4)
+
+
 BLOCK_SHAPES = [(1, 32, 1), (200, 5120, 1), (70_000, 32, 2), (77, 1056, 3), (200, 5120, 8), (64, 160, 9),
                 (64, 128, 16), (100, 256, 47), (1030, 1152, 33), (300, 1152, 130), (2500, 5120, 64)]
 
