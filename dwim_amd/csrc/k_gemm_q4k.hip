@@ -23,6 +23,7 @@
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 namespace {
 
@@ -57,13 +58,20 @@ struct GemmArgs {
     int add;
 };
 
+// The global loads of one step (a quant group of a block): this thread's 16
+// quant bytes of its row and, at a block's first group, the row's header; and
+// 32 halves of each part of its token's activations.
+struct StepLoad {
+    uint4 q, hdr, xh[4], xl[4];
+};
+
 __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     extern __shared__ _Float16 lds[];
     _Float16 *ah = lds, *al = ah + kRows * kPad, *bh = al + kRows * kPad, *bl = bh + kToks * kPad;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave >> 1, wc = wave & 1;  // the wave's 64-row, 64-token quarter
     const size_t row0 = (size_t)blockIdx.x * kRows, tok0 = (size_t)blockIdx.y * kToks;
-    const size_t nb = a.cols / 256, tiles = q4kt::tiles(a.rows);
+    const size_t nb = a.cols / 256, tiles = q4kt::tiles(a.rows), steps = 4 * nb;
 
     // the weights this thread dequantizes: row lr of the tile, quant bytes 16·lh..16·lh+15
     const int lr = tid >> 1, lh = tid & 1;
@@ -73,84 +81,125 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     const int lt = tid >> 1, lx = tid & 1;
     const bool xlive = tok0 + lt < a.n;
 
+    auto fetch = [&](size_t s, StepLoad &L) {
+        const size_t b = s / 4, g = s % 4;
+        if (wlive) {
+            const uint8_t *u = a.w + q4kt::unit(wtile, b, nb);
+            L.q = *(const uint4 *)(u + q4kt::qs_off(g, (row0 + lr) % 16) + 16 * lh);
+            if (g == 0) L.hdr = *(const uint4 *)(u + q4kt::meta_off((row0 + lr) % 16));
+        } else {
+            L.q = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);  // (stored 0 weights)
+            L.hdr = make_uint4(0, 0, 0, 0);
+        }
+        const size_t off = (tok0 + (xlive ? lt : 0)) * a.cols + b * 256 + g * kStep + 32 * lx;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            L.xh[k] = ((const uint4 *)(a.xh + off))[k];
+            L.xl[k] = ((const uint4 *)(a.xl + off))[k];
+        }
+        if (!xlive)
+#pragma unroll
+            for (int k = 0; k < 4; k++) L.xh[k] = L.xl[k] = make_uint4(0, 0, 0, 0);
+    };
+
     float4v acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (size_t b = 0; b < nb; b++) {
-        // this row's block header: d, dmin and the 6-bit scales and mins
-        uint8_t hdr[16];
-        if (wlive) {
-            const uint4 h = *(const uint4 *)(a.w + q4kt::unit(wtile, b, nb) + q4kt::meta_off((row0 + lr) % 16));
-            __builtin_memcpy(hdr, &h, 16);
-        } else {
-            for (int i = 0; i < 16; i++) hdr[i] = 0;
+    StepLoad cur, nxt;
+    fetch(0, cur);
+    uint8_t hdr[16];
+    float d = 0.0f, dmin = 0.0f;
+    for (size_t s = 0; s < steps; s++) {
+        const int g = (int)(s % 4);
+        if (g == 0) {
+            // this row's block header: d, dmin and the 6-bit scales and mins
+            __builtin_memcpy(hdr, &cur.hdr, 16);
+            d = dq::from_f16((uint16_t)(hdr[0] | hdr[1] << 8));
+            dmin = dq::from_f16((uint16_t)(hdr[2] | hdr[3] << 8));
         }
-        const float d = dq::from_f16((uint16_t)(hdr[0] | hdr[1] << 8)), dmin = dq::from_f16((uint16_t)(hdr[2] | hdr[3] << 8));
-        for (int g = 0; g < 4; g++) {
-            // stage the weights: sub-blocks 2g (low nibbles) and 2g+1 (high nibbles)
-            {
-                float sc0, mn0, sc1, mn1;
-                scale_min(hdr + 4, 2 * g, sc0, mn0);
-                scale_min(hdr + 4, 2 * g + 1, sc1, mn1);
-                const float d0 = d * sc0, m0 = dmin * mn0, d1 = d * sc1, m1 = dmin * mn1;
-                uint4 q = make_uint4(0, 0, 0, 0);
-                if (wlive) q = *(const uint4 *)(a.w + q4kt::unit(wtile, b, nb) + q4kt::qs_off(g, (row0 + lr) % 16) + 16 * lh);
-                const uint32_t words[4] = {q.x, q.y, q.z, q.w};
-                _Float16 *dh = ah + lr * kPad + 16 * lh, *dl = al + lr * kPad + 16 * lh;
+        // stage the weights: sub-blocks 2g (low nibbles) and 2g+1 (high nibbles)
+        {
+            float sc0, mn0, sc1, mn1;
+            scale_min(hdr + 4, 2 * g, sc0, mn0);
+            scale_min(hdr + 4, 2 * g + 1, sc1, mn1);
+            const float d0 = d * sc0, m0 = dmin * mn0, d1 = d * sc1, m1 = dmin * mn1;
+            const uint32_t words[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+            // 16 low-nibble weights (sub-block 2g), 16 high (2g+1): hi and lo
+            // halves packed in pairs, written 8 halves at a time
+            uint32_t hh0[8], hl0[8], hh1[8], hl1[8];
 #pragma unroll
-                for (int k = 0; k < 16; k++) {
-                    const uint32_t byte = q4kt::stored((uint8_t)(words[k / 4] >> (8 * (k % 4))));
-                    const float w0 = d0 * (float)(byte & 0xf) - m0, w1 = d1 * (float)(byte >> 4) - m1;
-                    const _Float16 h0 = (_Float16)w0, h1 = (_Float16)w1;
-                    dh[k] = h0;
-                    dl[k] = (_Float16)(w0 - (float)h0);
-                    dh[32 + k] = h1;
-                    dl[32 + k] = (_Float16)(w1 - (float)h1);
+            for (int k = 0; k < 4; k++) {
+                const uint32_t lo = words[k] & 0x0f0f0f0fu, hi = ((words[k] ^ 0x80808080u) >> 4) & 0x0f0f0f0fu;
+                float w0[4], w1[4];
+                w0[0] = d0 * (float)(lo & 0xffu) - m0;
+                w0[1] = d0 * (float)((lo >> 8) & 0xffu) - m0;
+                w0[2] = d0 * (float)((lo >> 16) & 0xffu) - m0;
+                w0[3] = d0 * (float)(lo >> 24) - m0;
+                w1[0] = d1 * (float)(hi & 0xffu) - m1;
+                w1[1] = d1 * (float)((hi >> 8) & 0xffu) - m1;
+                w1[2] = d1 * (float)((hi >> 16) & 0xffu) - m1;
+                w1[3] = d1 * (float)(hi >> 24) - m1;
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const half2v h0 = half2v{(_Float16)w0[2 * e], (_Float16)w0[2 * e + 1]};
+                    const half2v h1 = half2v{(_Float16)w1[2 * e], (_Float16)w1[2 * e + 1]};
+                    const half2v l0 = half2v{(_Float16)(w0[2 * e] - (float)h0[0]), (_Float16)(w0[2 * e + 1] - (float)h0[1])};
+                    const half2v l1 = half2v{(_Float16)(w1[2 * e] - (float)h1[0]), (_Float16)(w1[2 * e + 1] - (float)h1[1])};
+                    hh0[2 * k + e] = __builtin_bit_cast(uint32_t, h0);
+                    hl0[2 * k + e] = __builtin_bit_cast(uint32_t, l0);
+                    hh1[2 * k + e] = __builtin_bit_cast(uint32_t, h1);
+                    hl1[2 * k + e] = __builtin_bit_cast(uint32_t, l1);
                 }
             }
-            // stage the activations: 32 halves of each part
-            {
-                const size_t off = (tok0 + lt) * a.cols + b * 256 + g * kStep + 32 * lx;
-                uint4 xh4[4], xl4[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    xh4[k] = xlive ? ((const uint4 *)(a.xh + off))[k] : make_uint4(0, 0, 0, 0);
-                    xl4[k] = xlive ? ((const uint4 *)(a.xl + off))[k] : make_uint4(0, 0, 0, 0);
-                }
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    *(uint4 *)(bh + lt * kPad + 32 * lx + 8 * k) = xh4[k];
-                    *(uint4 *)(bl + lt * kPad + 32 * lx + 8 * k) = xl4[k];
-                }
-            }
-            __syncthreads();
-#pragma unroll
-            for (int kk = 0; kk < 2; kk++) {
-                const int ko = kk * 32 + 8 * (lane >> 4);
-                half8 fah[4], fal[4], fbh[4], fbl[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int r = wr * 64 + i * 16 + (lane & 15);
-                    fah[i] = *(const half8 *)(ah + r * kPad + ko);
-                    fal[i] = *(const half8 *)(al + r * kPad + ko);
-                    const int t = wc * 64 + i * 16 + (lane & 15);
-                    fbh[i] = *(const half8 *)(bh + t * kPad + ko);
-                    fbl[i] = *(const half8 *)(bl + t * kPad + ko);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fah[i], fbh[j], acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fah[i], fbl[j], acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fal[i], fbh[j], acc[i][j], 0, 0, 0);
-                    }
-            }
-            __syncthreads();
+            uint32_t *dh = (uint32_t *)(ah + lr * kPad + 16 * lh), *dl = (uint32_t *)(al + lr * kPad + 16 * lh);
+            *(uint4 *)dh = make_uint4(hh0[0], hh0[1], hh0[2], hh0[3]);
+            *(uint4 *)(dh + 4) = make_uint4(hh0[4], hh0[5], hh0[6], hh0[7]);
+            *(uint4 *)(dh + 16) = make_uint4(hh1[0], hh1[1], hh1[2], hh1[3]);
+            *(uint4 *)(dh + 20) = make_uint4(hh1[4], hh1[5], hh1[6], hh1[7]);
+            *(uint4 *)dl = make_uint4(hl0[0], hl0[1], hl0[2], hl0[3]);
+            *(uint4 *)(dl + 4) = make_uint4(hl0[4], hl0[5], hl0[6], hl0[7]);
+            *(uint4 *)(dl + 16) = make_uint4(hl1[0], hl1[1], hl1[2], hl1[3]);
+            *(uint4 *)(dl + 20) = make_uint4(hl1[4], hl1[5], hl1[6], hl1[7]);
         }
+        // stage the activations: 32 halves of each part
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            *(uint4 *)(bh + lt * kPad + 32 * lx + 8 * k) = cur.xh[k];
+            *(uint4 *)(bl + lt * kPad + 32 * lx + 8 * k) = cur.xl[k];
+        }
+        __syncthreads();
+        // the next step's loads fly while this step's products run
+        if (s + 1 < steps) {
+            fetch(s + 1, nxt);
+            if ((s + 1) % 4 != 0) nxt.hdr = cur.hdr;
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            const int ko = kk * 32 + 8 * (lane >> 4);
+            half8 fah[4], fal[4], fbh[4], fbl[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = wr * 64 + i * 16 + (lane & 15);
+                fah[i] = *(const half8 *)(ah + r * kPad + ko);
+                fal[i] = *(const half8 *)(al + r * kPad + ko);
+                const int t = wc * 64 + i * 16 + (lane & 15);
+                fbh[i] = *(const half8 *)(bh + t * kPad + ko);
+                fbl[i] = *(const half8 *)(bl + t * kPad + ko);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fah[i], fbh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fah[i], fbl[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fal[i], fbh[j], acc[i][j], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+        cur = nxt;
     }
     // C tile (i, j): lane holds rows 16i + 4(lane/16) + e of token 16j + lane%16
 #pragma unroll
