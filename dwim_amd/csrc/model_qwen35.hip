@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <array>
+#include <map>
 #include <memory>
 #include <string>
 #include <vector>
@@ -27,6 +28,7 @@ namespace {
     } while (0)
 
 constexpr size_t kConvKernel = 4;
+constexpr size_t kMaxDrafts = 8;  // MAX_DRAFTS (qwen35/mod.rs:26)
 
 // FNV-1a of a tensor's name, the key of its value stream
 uint64_t fnv1a(const std::string &s) {
@@ -58,7 +60,9 @@ struct Draft {
     Layer layer;
 };
 
+// Sequence (qwen35/mod.rs:1351-1374): a sequence's own state
 struct Sequence {
+    size_t id = 0;
     std::vector<dwim_cache *> k_cache, v_cache;
     std::vector<std::array<dwim_buf *, 2>> conv_state;
     bool parity = false;
@@ -66,6 +70,9 @@ struct Sequence {
     size_t max_len = 0;
     dwim_buf *hidden = nullptr;
     bool carry = false;
+    // a batch being verified: its tokens and the position of the first
+    std::vector<uint32_t> verified;
+    size_t verified_at = 0;
 };
 
 }  // namespace
@@ -87,6 +94,15 @@ struct dwim_model {
              *v = nullptr, *att = nullptr, *qkv = nullptr, *z = nullptr, *ab = nullptr;
     dwim_buf *up = nullptr, *gate_ffn = nullptr, *logits = nullptr, *rope = nullptr, *drafted = nullptr;
     Sequence seq;
+    std::map<size_t, Sequence> parked;  // the sequences not running
+    // verifying: the linear layers' states run through the batch, and their
+    // inputs, apart from the real ones (with a drafter only)
+    std::vector<dwim_buf *> ssm_scratch, qkv_saved, ab_saved;
+    // the mark: linear layers' states and the carried hidden state
+    std::vector<dwim_buf *> mark_conv, mark_ssm;
+    dwim_buf *mark_hidden = nullptr;
+    bool mark_carry = false;
+    long marked = -1;  // the id of the sequence marked, or -1
     size_t caches = 0, slots = 0;
     // everything allocated, freed with the model
     std::vector<dwim_buf *> bufs;
@@ -173,7 +189,8 @@ struct dwim_model {
 
     int zeroed(size_t len, dwim_buf **out) { return buf(len, out); }  // dwim_alloc zeroes
 
-    int new_sequence(Sequence &s, size_t max_len) {
+    int new_sequence(Sequence &s, size_t id, size_t max_len) {
+        s.id = id;
         s.max_len = max_len;
         for (size_t i = 0; i < caches; i++) {
             dwim_cache *kc, *vc;
@@ -241,8 +258,9 @@ struct dwim_model {
         return 0;
     }
 
-    // Pass::layer (qwen35/mod.rs:541-655), the verify-free path
-    int layer(const Layer &l, size_t n, size_t pos) {
+    // Pass::layer (qwen35/mod.rs:541-655).  Verifying, the linear layers
+    // save their inputs and run a copy of their recurrent state (:606-632).
+    int layer(const Layer &l, size_t n, size_t pos, bool verify = false) {
         const float eps = c.eps;
         const bool fused = fusable(l), one = fused && n == 1;
         TRY(dwim_resize(dev, xh, n * c.hidden));
@@ -287,15 +305,16 @@ struct dwim_model {
             auto &pair = seq.conv_state[l.slot];
             dwim_buf *state = seq.parity ? pair[0] : pair[1];
             dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
+            dwim_buf *ssm = verify ? ssm_scratch[l.slot] : seq.ssm_state[l.slot];
             if (fused) {
                 const dwim_weight *ws[2] = {l.qkv, l.z};
                 dwim_buf *outs[2] = {qkv, z};
                 TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
                 TRY(dwim_matmul(dev, ab, l.ab, xh));
+                if (verify) TRY(save_inputs(l.slot, n));
                 DWIM_HIP(launch_conv_l2(dev->stream, q->data, k->data, v->data, state_out->data, qkv->data,
                                         state->data, l.conv->data, n, k_dim(), k_dim(), v_dim(), c.state_dim, eps));
-                TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, seq.ssm_state[l.slot], c.k_heads, c.v_heads,
-                                   c.state_dim));
+                TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads, c.state_dim));
                 DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps,
                                            one ? 0 : -1));
                 if (one) TRY(add_planes(l.out));
@@ -304,11 +323,11 @@ struct dwim_model {
                 TRY(dwim_matmul(dev, qkv, l.qkv, xh));
                 TRY(dwim_matmul(dev, z, l.z, xh));
                 TRY(dwim_matmul(dev, ab, l.ab, xh));
+                if (verify) TRY(save_inputs(l.slot, n));
                 TRY(dwim_conv(dev, q, k, v, state_out, qkv, state, l.conv));
                 TRY(dwim_l2norm(dev, q, c.state_dim, eps));
                 TRY(dwim_l2norm(dev, k, c.state_dim, eps));
-                TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, seq.ssm_state[l.slot], c.k_heads, c.v_heads,
-                                   c.state_dim));
+                TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads, c.state_dim));
                 TRY(dwim_rmsnorm(dev, att, l.norm, eps));
                 TRY(dwim_silu_mul(dev, z, att));
                 TRY(dwim_matmul_add(dev, x, l.out, z, xb));
@@ -331,6 +350,13 @@ struct dwim_model {
         }
         TRY(dwim_matmul_add(dev, x, l.down, up, xb));
         return 0;
+    }
+
+    // the verified batch's inputs of linear layer `slot`, and its state
+    int save_inputs(size_t slot, size_t n) {
+        TRY(dwim_copy(dev, qkv_saved[slot], 0, qkv, 0, n * (2 * k_dim() + v_dim())));
+        TRY(dwim_copy(dev, ab_saved[slot], 0, ab, 0, n * 2 * c.v_heads));
+        return dwim_copy(dev, ssm_scratch[slot], 0, seq.ssm_state[slot], 0, ssm_width());
     }
 
     // Pass::drafter (qwen35/mod.rs:663-698), fed rows of seq.hidden from `first`
@@ -367,14 +393,16 @@ struct dwim_model {
         return dwim_read(dev, xb, &one, 1);
     }
 
-    // forward_batch (qwen35/mod.rs:425-496) for verify = false.  With
-    // `logits_out` the logits after the last token are read back; with
-    // `greedy` the first index of their maximum is taken on the device.
-    int forward_batch(const uint32_t *tokens, size_t n, size_t pos, bool wanted, float *logits_out, uint32_t *greedy) {
+    // forward_batch (qwen35/mod.rs:425-496).  With `logits_out` the logits
+    // after the last token are read back, or verifying, after every token;
+    // with `greedy` the first index of each row's maximum is taken on the
+    // device.
+    int forward_batch(const uint32_t *tokens, size_t n, size_t pos, bool verify, bool wanted, float *logits_out,
+                      uint32_t *greedy) {
         TRY(batch(n));
         TRY(dwim_embed(dev, x, embd, tokens, n));
-        for (const Layer &l : layers) TRY(layer(l, n, pos));
-        seq.parity = !seq.parity;
+        for (const Layer &l : layers) TRY(layer(l, n, pos, verify));
+        if (!verify) seq.parity = !seq.parity;
         const size_t h = c.hidden;
         if (!has_draft) {
             if (!wanted) return finish();
@@ -388,6 +416,13 @@ struct dwim_model {
         }
         TRY(normalize(xh, x, norm, n));
         TRY(dwim_copy(dev, seq.hidden, h, xh, 0, n * h));
+        if (verify) {
+            seq.verified.assign(tokens, tokens + n);
+            seq.verified_at = pos;
+            TRY(dwim_resize(dev, logits, n * c.vocab));
+            TRY(dwim_matmul(dev, logits, head, xh));
+            return read_logits(logits_out, greedy, n);
+        }
         if (wanted) {
             TRY(dwim_resize(dev, xb, h));
             TRY(dwim_copy(dev, xb, 0, xh, (n - 1) * h, h));
@@ -401,9 +436,9 @@ struct dwim_model {
         return finish();
     }
 
-    int read_logits(float *logits_out, uint32_t *greedy) {
-        if (greedy) TRY(dwim_argmax(dev, logits, 1, greedy));
-        if (logits_out) TRY(dwim_read(dev, logits, logits_out, c.vocab));
+    int read_logits(float *logits_out, uint32_t *greedy, size_t rows = 1) {
+        if (greedy) TRY(dwim_argmax(dev, logits, rows, greedy));
+        if (logits_out) TRY(dwim_read(dev, logits, logits_out, rows * c.vocab));
         if (!greedy && !logits_out) return finish();
         return 0;
     }
@@ -416,9 +451,134 @@ struct dwim_model {
         for (size_t i = 0; i < batches; i++) {
             const size_t m = std::min(most, n - i * most);
             const bool last = i + 1 == batches;
-            TRY(forward_batch(tokens + i * most, m, pos + i * most, last, last ? logits_out : nullptr,
+            TRY(forward_batch(tokens + i * most, m, pos + i * most, false, last, last ? logits_out : nullptr,
                               last ? greedy : nullptr));
         }
+        return 0;
+    }
+
+    // LanguageModel::draft (qwen35/mod.rs:1045-1071): the drafter at the
+    // position before `token`, fed the hidden state carried over, then on
+    // its own output, `k` times; each draft the head's greedy pick, taken on
+    // the device.  Returns how many were drafted.
+    size_t draft_tokens(uint32_t token, size_t pos, size_t k, uint32_t *drafts, int *status) {
+        *status = 0;
+        if (!has_draft) return 0;
+        k = std::min(k, kMaxDrafts);
+        k = std::min(k, seq.max_len > pos + 1 ? seq.max_len - (pos + 1) : (size_t)0);
+        if (!seq.carry || !seq.verified.empty() || pos == 0 || k == 0) return 0;
+        uint32_t next = token;
+        for (size_t i = 0; i < k; i++) {
+            if (drafter(1, pos - 1 + i, 0, i > 0, &next) || dwim_copy(dev, drafted, 0, xh, 0, c.hidden) ||
+                dwim_resize(dev, logits, c.vocab) || dwim_matmul(dev, logits, head, xh) ||
+                dwim_argmax(dev, logits, 1, &next)) {
+                *status = 1;
+                return i;
+            }
+            drafts[i] = next;
+        }
+        return k;
+    }
+
+    // LanguageModel::verify (qwen35/mod.rs:1073-1091)
+    int verify(const uint32_t *tokens, size_t n, size_t pos, float *logits_out, uint32_t *greedy) {
+        if (!has_draft) return dwim_fail("the model does not draft");
+        if (!seq.verified.empty() || !seq.carry) return dwim_fail("a batch is being verified, or none was run before");
+        if (n == 0 || n > kMaxDrafts + 1)
+            return dwim_fail("a batch of " + std::to_string(n) + " tokens is not one to verify");
+        if (pos + n > seq.max_len) return dwim_fail("tokens past the end of the cache");
+        return forward_batch(tokens, n, pos, true, true, logits_out, greedy);
+    }
+
+    // LanguageModel::rewind (qwen35/mod.rs:1099-1169): commits the first
+    // `keep` tokens of the batch being verified.  All kept, the states the
+    // batch ran through become the real ones; fewer, the real ones run
+    // through the tokens kept from the inputs saved.  Then the drafter
+    // catches up on the tokens kept.
+    int rewind(size_t keep) {
+        const size_t n = seq.verified.size();
+        if (n == 0 || keep == 0 || keep > n)
+            return dwim_fail("keeping " + std::to_string(keep) + " tokens of a batch of " + std::to_string(n) +
+                             " being verified");
+        const std::vector<uint32_t> tokens = std::move(seq.verified);
+        seq.verified.clear();
+        if (keep == n) {
+            for (size_t slot = 0; slot < slots; slot++) std::swap(seq.ssm_state[slot], ssm_scratch[slot]);
+        } else {
+            TRY(batch(keep));
+            TRY(dwim_resize(dev, q, keep * k_dim()));
+            TRY(dwim_resize(dev, k, keep * k_dim()));
+            TRY(dwim_resize(dev, v, keep * v_dim()));
+            TRY(dwim_resize(dev, att, keep * v_dim()));
+            for (const Layer &l : layers) {
+                if (l.attention) continue;
+                TRY(dwim_copy(dev, qkv, 0, qkv_saved[l.slot], 0, keep * (2 * k_dim() + v_dim())));
+                TRY(dwim_copy(dev, ab, 0, ab_saved[l.slot], 0, keep * 2 * c.v_heads));
+                auto &pair = seq.conv_state[l.slot];
+                dwim_buf *state = seq.parity ? pair[0] : pair[1];
+                dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
+                TRY(dwim_conv(dev, q, k, v, state_out, qkv, state, l.conv));
+                TRY(dwim_l2norm(dev, q, c.state_dim, c.eps));
+                TRY(dwim_l2norm(dev, k, c.state_dim, c.eps));
+                TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, seq.ssm_state[l.slot], c.k_heads, c.v_heads,
+                                   c.state_dim));
+            }
+        }
+        seq.parity = !seq.parity;
+        TRY(drafter(keep, seq.verified_at - 1, 0, false, tokens.data()));
+        TRY(carry_over(keep));
+        return finish();
+    }
+
+    // LanguageModel::mark (qwen35/mod.rs:1176-1203): the linear layers'
+    // states and the carried hidden state, copied aside on the device
+    int mark() {
+        if (!seq.verified.empty()) return dwim_fail("a batch is being verified");
+        for (size_t slot = 0; slot < slots; slot++) {
+            TRY(dwim_copy(dev, mark_conv[slot], 0, seq.conv_state[slot][seq.parity ? 0 : 1], 0, conv_width()));
+            TRY(dwim_copy(dev, mark_ssm[slot], 0, seq.ssm_state[slot], 0, ssm_width()));
+        }
+        if (seq.carry) TRY(dwim_copy(dev, mark_hidden, 0, seq.hidden, 0, c.hidden));
+        mark_carry = seq.carry;
+        marked = (long)seq.id;
+        return 0;
+    }
+
+    // LanguageModel::rewind_to_mark (qwen35/mod.rs:1207-1228)
+    int rewind_to_mark() {
+        if (marked != (long)seq.id) return dwim_fail("no mark to rewind to");
+        if (!seq.verified.empty()) return dwim_fail("a batch is being verified");
+        for (size_t slot = 0; slot < slots; slot++) {
+            TRY(dwim_copy(dev, seq.conv_state[slot][0], 0, mark_conv[slot], 0, conv_width()));
+            TRY(dwim_copy(dev, seq.ssm_state[slot], 0, mark_ssm[slot], 0, ssm_width()));
+        }
+        seq.parity = true;
+        if (mark_carry) TRY(dwim_copy(dev, seq.hidden, 0, mark_hidden, 0, c.hidden));
+        seq.carry = mark_carry;
+        return 0;
+    }
+
+    // LanguageModel::add_sequence (qwen35/mod.rs:1258-1272)
+    int add_sequence(size_t *id) {
+        const size_t next = parked.size() + 1;
+        Sequence s;
+        TRY(new_sequence(s, next, seq.max_len));
+        parked.emplace(next, std::move(s));
+        *id = next;
+        return dwim_sync(dev);
+    }
+
+    // LanguageModel::select_sequence (qwen35/mod.rs:1275-1290): nothing copied
+    int select_sequence(size_t id) {
+        if (seq.id == id) return 0;
+        if (!seq.verified.empty()) return dwim_fail("a batch is being verified");
+        auto it = parked.find(id);
+        if (it == parked.end()) return dwim_fail("no sequence " + std::to_string(id));
+        Sequence next = std::move(it->second);
+        parked.erase(it);
+        const size_t old = seq.id;
+        parked.emplace(old, std::move(seq));
+        seq = std::move(next);
         return 0;
     }
 
@@ -431,6 +591,8 @@ struct dwim_model {
         }
         seq.parity = false;
         seq.carry = false;
+        seq.verified.clear();
+        if (marked == (long)seq.id) marked = -1;
         return 0;
     }
 
@@ -501,12 +663,29 @@ extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg
     for (int i = 0; i < 11; i++)
         if (m->buf(m->most * m->widths[i], b[i])) return 1;
     if (m->buf(m->most * c.intermediate, &m->up) || m->buf(m->most * c.intermediate, &m->gate_ffn) ||
-        m->buf((c.drafter ? 9 : 1) * c.vocab, &m->logits) || m->buf(c.hidden, &m->drafted))
+        m->buf((c.drafter ? kMaxDrafts + 1 : 1) * c.vocab, &m->logits) || m->buf(c.hidden, &m->drafted))
         return 1;
     std::vector<float> table;
     rope_table(table, max_len, c.rot_dim, c.rope_theta);
     if (m->buf(table.size(), &m->rope) || dwim_write(dev, m->rope, table.data(), table.size())) return 1;
-    if (m->new_sequence(m->seq, max_len)) return 1;
+    for (size_t i = 0; i < m->slots; i++) {
+        dwim_buf *mc, *ms;
+        if (m->buf(m->conv_width(), &mc) || m->buf(m->ssm_width(), &ms)) return 1;
+        m->mark_conv.push_back(mc);
+        m->mark_ssm.push_back(ms);
+        if (c.drafter) {
+            // verify batches hold at most MAX_DRAFTS + 1 tokens
+            dwim_buf *sc, *qs, *as;
+            if (m->buf(m->ssm_width(), &sc) || m->buf((kMaxDrafts + 1) * (2 * k_dim + v_dim), &qs) ||
+                m->buf((kMaxDrafts + 1) * 2 * c.v_heads, &as))
+                return 1;
+            m->ssm_scratch.push_back(sc);
+            m->qkv_saved.push_back(qs);
+            m->ab_saved.push_back(as);
+        }
+    }
+    if (m->buf(c.hidden, &m->mark_hidden)) return 1;
+    if (m->new_sequence(m->seq, 0, max_len)) return 1;
     if (dwim_sync(dev)) return 1;
     *out = m.release();
     return 0;
@@ -525,3 +704,24 @@ extern "C" int dwim_model_forward_greedy(dwim_model *m, const uint32_t *tokens, 
 }
 
 extern "C" int dwim_model_reset(dwim_model *m) { return m->reset(); }
+
+extern "C" int dwim_model_draft(dwim_model *m, uint32_t token, size_t pos, size_t k, uint32_t *drafts, size_t *count) {
+    int status = 0;
+    *count = m->draft_tokens(token, pos, k, drafts, &status);
+    return status;
+}
+
+extern "C" int dwim_model_verify(dwim_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits,
+                                 uint32_t *greedy) {
+    return m->verify(tokens, n, pos, logits, greedy);
+}
+
+extern "C" int dwim_model_rewind(dwim_model *m, size_t keep) { return m->rewind(keep); }
+
+extern "C" int dwim_model_mark(dwim_model *m) { return m->mark(); }
+
+extern "C" int dwim_model_rewind_to_mark(dwim_model *m) { return m->rewind_to_mark(); }
+
+extern "C" int dwim_model_add_sequence(dwim_model *m, size_t *id) { return m->add_sequence(id); }
+
+extern "C" int dwim_model_select_sequence(dwim_model *m, size_t id) { return m->select_sequence(id); }

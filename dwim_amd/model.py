@@ -66,11 +66,26 @@ def _declare(L):
     L.dwim_model_forward_greedy.argtypes = [vp, u32p, sz, sz, u32p]
     L.dwim_model_reset.restype = ctypes.c_int
     L.dwim_model_reset.argtypes = [vp]
+    L.dwim_model_draft.restype = ctypes.c_int
+    L.dwim_model_draft.argtypes = [vp, ctypes.c_uint32, sz, sz, u32p, ctypes.POINTER(sz)]
+    L.dwim_model_verify.restype = ctypes.c_int
+    L.dwim_model_verify.argtypes = [vp, u32p, sz, sz, f32p, u32p]
+    L.dwim_model_rewind.restype = ctypes.c_int
+    L.dwim_model_rewind.argtypes = [vp, sz]
+    for name in ("dwim_model_mark", "dwim_model_rewind_to_mark"):
+        getattr(L, name).restype = ctypes.c_int
+        getattr(L, name).argtypes = [vp]
+    L.dwim_model_add_sequence.restype = ctypes.c_int
+    L.dwim_model_add_sequence.argtypes = [vp, ctypes.POINTER(sz)]
+    L.dwim_model_select_sequence.restype = ctypes.c_int
+    L.dwim_model_select_sequence.argtypes = [vp, sz]
     _sigs_done = True
 
 
 MODEL_SIGNATURES = ["dwim_model_synthetic", "dwim_model_free", "dwim_model_batch", "dwim_model_forward",
-                    "dwim_model_forward_greedy", "dwim_model_reset"]
+                    "dwim_model_forward_greedy", "dwim_model_reset", "dwim_model_draft", "dwim_model_verify",
+                    "dwim_model_rewind", "dwim_model_mark", "dwim_model_rewind_to_mark", "dwim_model_add_sequence",
+                    "dwim_model_select_sequence"]
 
 
 class Model:
@@ -105,6 +120,44 @@ class Model:
 
     def reset(self):
         D._check(self.L.dwim_model_reset(self.h))
+
+    def draft(self, token: int, pos: int, k: int) -> list[int]:
+        """LanguageModel::draft (qwen35/mod.rs:1045-1071)."""
+        out = np.zeros(max(k, 1), np.uint32)
+        n = ctypes.c_size_t()
+        D._check(self.L.dwim_model_draft(self.h, token, pos, k, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                         ctypes.byref(n)))
+        return [int(t) for t in out[:n.value]]
+
+    def verify(self, tokens, pos: int, want_logits: bool = True):
+        """LanguageModel::verify (qwen35/mod.rs:1073-1091): the logits after
+        every token ([n][vocab]) and each row's greedy pick."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        rows = np.empty((t.size, self.cfg.vocab), np.float32) if want_logits else None
+        greedy = np.zeros(t.size, np.uint32)
+        D._check(self.L.dwim_model_verify(
+            self.h, t.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), t.size, pos,
+            None if rows is None else rows.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+            greedy.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))))
+        return rows, [int(g) for g in greedy]
+
+    def rewind(self, keep: int):
+        D._check(self.L.dwim_model_rewind(self.h, keep))
+
+    def mark(self) -> bool:
+        D._check(self.L.dwim_model_mark(self.h))
+        return True
+
+    def rewind_to_mark(self):
+        D._check(self.L.dwim_model_rewind_to_mark(self.h))
+
+    def add_sequence(self) -> int:
+        i = ctypes.c_size_t()
+        D._check(self.L.dwim_model_add_sequence(self.h, ctypes.byref(i)))
+        return i.value
+
+    def select_sequence(self, seq: int):
+        D._check(self.L.dwim_model_select_sequence(self.h, seq))
 
     def close(self):
         if getattr(self, "h", None):

@@ -204,6 +204,32 @@ int dwim_model_forward_greedy(dwim_model *m, const uint32_t *tokens, size_t n, s
                               uint32_t *next);
 /* LanguageModel::reset (qwen35/mod.rs:1230-1246). */
 int dwim_model_reset(dwim_model *m);
+/* LanguageModel::draft (qwen35/mod.rs:1045-1071): up to k (at most 8, and as
+ * many as the cache has room to verify) tokens the drafter predicts after
+ * `token` at `pos`, each the head's first maximum; *count is how many (0
+ * without a drafter, before any batch, or while one is being verified).
+ * `drafts` holds k tokens. */
+int dwim_model_draft(dwim_model *m, uint32_t token, size_t pos, size_t k, uint32_t *drafts,
+                     size_t *count);
+/* LanguageModel::verify (qwen35/mod.rs:1073-1091): runs 1..=9 tokens from
+ * `pos` without committing the linear layers' states; writes the logits after
+ * every token (n·vocab floats) to `logits` and/or each row's first maximum
+ * (n tokens) to `greedy`, either of which may be NULL. */
+int dwim_model_verify(dwim_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits,
+                      uint32_t *greedy);
+/* LanguageModel::rewind (qwen35/mod.rs:1099-1169): commits the first `keep`
+ * (1..=n) tokens of the batch being verified. */
+int dwim_model_rewind(dwim_model *m, size_t keep);
+/* LanguageModel::mark / rewind_to_mark (qwen35/mod.rs:1176-1228): copies the
+ * running sequence's linear-layer states aside on the device, and back; the
+ * one mark belongs to the sequence that made it (error from another). */
+int dwim_model_mark(dwim_model *m);
+int dwim_model_rewind_to_mark(dwim_model *m);
+/* LanguageModel::add_sequence / select_sequence (qwen35/mod.rs:1258-1290):
+ * another sequence, as before any token, of the first one's length; and a
+ * switch of the running sequence (nothing copied; error while verifying). */
+int dwim_model_add_sequence(dwim_model *m, size_t *id);
+int dwim_model_select_sequence(dwim_model *m, size_t id);
 
 /* Host-side quantizers, the product's own (gpu/quant.rs restated for the host
  * loader, plus the K formats).  `x` holds `cols` weights. */

@@ -465,6 +465,14 @@ def _declare_model(L):
     L.or_model_draft.argtypes = [vp, ctypes.c_uint32, _sz, _sz, u32p]
     L.or_model_reset.restype = None
     L.or_model_reset.argtypes = [vp]
+    L.or_model_verify.restype = None
+    L.or_model_verify.argtypes = [vp, u32p, _sz, _sz, _f32p]
+    L.or_model_rewind.restype = None
+    L.or_model_rewind.argtypes = [vp, _sz]
+    L.or_model_mark.restype = None
+    L.or_model_mark.argtypes = [vp]
+    L.or_model_rewind_to_mark.restype = ctypes.c_int
+    L.or_model_rewind_to_mark.argtypes = [vp]
     L.or_synthetic_values.restype = None
     L.or_synthetic_values.argtypes = [ctypes.c_uint64, ctypes.c_uint64, _sz, ctypes.c_float, _f32p]
     L._model_declared = True
@@ -500,6 +508,24 @@ class Model:
         out = np.zeros(max(k, 1), np.uint32)
         n = self.L.or_model_draft(self.h, token, pos, k, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
         return list(out[:n])
+
+    def verify(self, tokens, pos):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        assert 0 < t.size <= 9
+        out = np.empty((t.size, self.vocab), np.float32)
+        self.L.or_model_verify(self.h, t.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), t.size, pos,
+                               _p(out, _f32p))
+        return out
+
+    def rewind(self, keep):
+        self.L.or_model_rewind(self.h, keep)
+
+    def mark(self):
+        self.L.or_model_mark(self.h)
+
+    def rewind_to_mark(self):
+        if self.L.or_model_rewind_to_mark(self.h):
+            raise RuntimeError("no mark to rewind to, or a batch is being verified")
 
     def reset(self):
         self.L.or_model_reset(self.h)

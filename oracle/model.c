@@ -8,7 +8,8 @@
  * Restated from qwen35/mod.rs: forward_batch :425-496 (verify = false),
  * Pass::layer :541-655, Pass::drafter :663-698, State::carry_over
  * :1466-1473, rope_table :1504-1515, LanguageModel::forward :1021-1038,
- * draft :1045-1071, reset :1230-1246.
+ * draft :1045-1071, verify :1073-1091, rewind :1099-1169, mark and
+ * rewind_to_mark :1176-1228, reset :1230-1246.
  */
 #include <math.h>
 #include <stdio.h>
@@ -88,6 +89,14 @@ struct or_model {
     int parity;
     float *hidden;
     int carry;
+    /* a batch being verified: its tokens, where it started, and the linear
+     * layers' inputs and states run through it apart from the real ones */
+    uint32_t verified[OR_MAX_DRAFTS + 1];
+    size_t n_verified, verified_at;
+    float **ssm_scratch, **qkv_saved, **ab_saved;
+    /* the mark */
+    float **mark_conv, **mark_ssm, *mark_hidden;
+    int marked, mark_carry;
 };
 
 static float *vec(struct or_model *m, const char *name, size_t len, float sigma, float offset) {
@@ -258,7 +267,7 @@ or_model *or_model_synthetic(const or_qwen35_config *cfg, uint64_t seed, int bod
     m->ab = calloc(most * 2 * c->v_heads, 4);
     m->up = calloc(most * c->intermediate, 4);
     m->gate_ffn = calloc(most * c->intermediate, 4);
-    m->logits = calloc(c->vocab, 4);
+    m->logits = calloc((OR_MAX_DRAFTS + 1) * c->vocab, 4);
     m->drafted = calloc(H, 4);
     m->rope = malloc(max_len * c->rot_dim * 4);
     or_rope_table(m->rope, max_len, c->rot_dim, c->rope_theta);
@@ -278,6 +287,14 @@ or_model *or_model_synthetic(const or_qwen35_config *cfg, uint64_t seed, int bod
     }
     m->ssm_state = calloc(m->slots, sizeof(float *));
     for (size_t i = 0; i < m->slots; i++) m->ssm_state[i] = calloc(ssm_width(m), 4);
+    float ***per_slot[] = {&m->ssm_scratch, &m->qkv_saved, &m->ab_saved, &m->mark_conv, &m->mark_ssm};
+    size_t widths[] = {ssm_width(m), (OR_MAX_DRAFTS + 1) * (2 * kd + vd), (OR_MAX_DRAFTS + 1) * 2 * c->v_heads,
+                       conv_width(m), ssm_width(m)};
+    for (int j = 0; j < 5; j++) {
+        *per_slot[j] = calloc(m->slots, sizeof(float *));
+        for (size_t i = 0; i < m->slots; i++) (*per_slot[j])[i] = calloc(widths[j], 4);
+    }
+    m->mark_hidden = calloc(H, 4);
     m->hidden = calloc((most + 1) * H, 4);
 #undef MAX
     return m;
@@ -307,6 +324,12 @@ void or_model_free(or_model *m) {
     }
     for (size_t i = 0; i < m->slots; i++) free(m->ssm_state[i]);
     free(m->ssm_state);
+    float **per_slot[] = {m->ssm_scratch, m->qkv_saved, m->ab_saved, m->mark_conv, m->mark_ssm};
+    for (int j = 0; j < 5; j++) {
+        for (size_t i = 0; i < m->slots; i++) free(per_slot[j][i]);
+        free(per_slot[j]);
+    }
+    free(m->mark_hidden);
     free(m);
 }
 
@@ -344,7 +367,7 @@ static void matmul_add(float *x, const or_weight *w, const float *in, size_t n, 
     or_add(x, scratch, n * w->rows);
 }
 
-static void layer(struct or_model *m, const layer_t *l, size_t n, size_t pos) {
+static void layer(struct or_model *m, const layer_t *l, size_t n, size_t pos, int verify) {
     const or_qwen35_config *c = &m->c;
     float eps = c->eps;
     size_t H = c->hidden;
@@ -370,12 +393,18 @@ static void layer(struct or_model *m, const layer_t *l, size_t n, size_t pos) {
         or_matmul(m->qkv, &l->qkv.w, m->xh, n);
         or_matmul(m->z, &l->z.w, m->xh, n);
         or_matmul(m->ab, &l->ab.w, m->xh, n);
+        if (verify) {
+            memcpy(m->qkv_saved[l->slot], m->qkv, n * (2 * kd + vd) * 4);
+            memcpy(m->ab_saved[l->slot], m->ab, n * 2 * c->v_heads * 4);
+            memcpy(m->ssm_scratch[l->slot], m->ssm_state[l->slot], ssm_width(m) * 4);
+        }
         float *state = m->parity ? m->conv_state[0][l->slot] : m->conv_state[1][l->slot];
         float *state_out = m->parity ? m->conv_state[1][l->slot] : m->conv_state[0][l->slot];
         or_conv(m->q, kd, m->k, kd, m->v, vd, state_out, m->qkv, n, state, l->conv);
         or_l2norm(m->q, n * kd, c->state_dim, eps);
         or_l2norm(m->k, n * kd, c->state_dim, eps);
-        or_delta_net(m->att, m->q, m->k, m->v, m->ab, l->decay, m->ssm_state[l->slot], n, c->k_heads, c->v_heads,
+        or_delta_net(m->att, m->q, m->k, m->v, m->ab, l->decay,
+                     verify ? m->ssm_scratch[l->slot] : m->ssm_state[l->slot], n, c->k_heads, c->v_heads,
                      c->state_dim);
         or_rmsnorm(m->att, n * vd, l->norm, c->state_dim, eps);
         or_silu_mul(m->z, m->att, n * vd);
@@ -401,7 +430,7 @@ static void drafter(struct or_model *m, size_t rows, size_t pos, size_t first, i
     or_matmul(m->x, &m->eproj.w, m->xb, rows);
     or_matmul(m->xb, &m->hproj.w, m->xh, rows);
     or_add(m->x, m->xb, rows * H);
-    layer(m, &m->dlayer, rows, pos);
+    layer(m, &m->dlayer, rows, pos, 0);
     normalize(m, m->xh, m->x, m->dnorm, rows);
 }
 
@@ -412,13 +441,13 @@ static void carry_over(struct or_model *m, size_t n) {
     m->carry = 1;
 }
 
-/* returns 1 when logits were computed */
-static int forward_batch(struct or_model *m, const uint32_t *tokens, size_t n, size_t pos, int wanted) {
+/* returns 1 when logits were computed; verifying, the logits of every token */
+static int forward_batch(struct or_model *m, const uint32_t *tokens, size_t n, size_t pos, int verify, int wanted) {
     const or_qwen35_config *c = &m->c;
     size_t H = c->hidden;
     embed(m, m->x, tokens, n);
-    for (size_t i = 0; i < c->layers; i++) layer(m, &m->layers[i], n, pos);
-    m->parity = !m->parity;
+    for (size_t i = 0; i < c->layers; i++) layer(m, &m->layers[i], n, pos, verify);
+    if (!verify) m->parity = !m->parity;
     if (!m->has_draft) {
         if (!wanted) return 0;
         memcpy(m->xb, m->x + (n - 1) * H, H * 4);
@@ -428,6 +457,13 @@ static int forward_batch(struct or_model *m, const uint32_t *tokens, size_t n, s
     }
     normalize(m, m->xh, m->x, m->norm, n);
     memcpy(m->hidden + H, m->xh, n * H * 4);
+    if (verify) {
+        memcpy(m->verified, tokens, n * sizeof *tokens);
+        m->n_verified = n;
+        m->verified_at = pos;
+        or_matmul(m->logits, &m->head.w, m->xh, n);
+        return 1;
+    }
     if (wanted) {
         memcpy(m->xb, m->xh + (n - 1) * H, H * 4);
         or_matmul(m->logits, &m->head.w, m->xb, 1);
@@ -442,15 +478,15 @@ void or_model_forward(or_model *m, const uint32_t *tokens, size_t n, size_t pos,
     size_t batches = (n + m->most - 1) / m->most;
     for (size_t i = 0; i < batches; i++) {
         size_t k = n - i * m->most < m->most ? n - i * m->most : m->most;
-        forward_batch(m, tokens + i * m->most, k, pos + i * m->most, i + 1 == batches);
+        forward_batch(m, tokens + i * m->most, k, pos + i * m->most, 0, i + 1 == batches);
     }
     if (logits) memcpy(logits, m->logits, m->c.vocab * 4);
 }
 
 /* LanguageModel::draft (qwen35/mod.rs:1045-1071) */
 size_t or_model_draft(or_model *m, uint32_t token, size_t pos, size_t k, uint32_t *drafts) {
-    if (!m->has_draft || !m->carry || pos == 0) return 0;
-    if (k > 8) k = 8;
+    if (!m->has_draft || !m->carry || m->n_verified || pos == 0) return 0;
+    if (k > OR_MAX_DRAFTS) k = OR_MAX_DRAFTS;
     if (pos + 1 + k > m->max_len) k = m->max_len > pos + 1 ? m->max_len - pos - 1 : 0;
     uint32_t next = token;
     for (size_t i = 0; i < k; i++) {
@@ -463,6 +499,70 @@ size_t or_model_draft(or_model *m, uint32_t token, size_t pos, size_t k, uint32_
     return k;
 }
 
+/* LanguageModel::verify (qwen35/mod.rs:1073-1091): logits [n][vocab] */
+void or_model_verify(or_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits) {
+    forward_batch(m, tokens, n, pos, 1, 1);
+    memcpy(logits, m->logits, n * m->c.vocab * 4);
+}
+
+/* LanguageModel::rewind (qwen35/mod.rs:1099-1169) */
+void or_model_rewind(or_model *m, size_t keep) {
+    const or_qwen35_config *c = &m->c;
+    size_t n = m->n_verified, kd = k_dim(m), vd = v_dim(m);
+    uint32_t tokens[OR_MAX_DRAFTS + 1];
+    memcpy(tokens, m->verified, n * sizeof *tokens);
+    m->n_verified = 0;
+    if (keep == n) {
+        for (size_t i = 0; i < m->slots; i++) {
+            float *t = m->ssm_state[i];
+            m->ssm_state[i] = m->ssm_scratch[i];
+            m->ssm_scratch[i] = t;
+        }
+    } else {
+        for (size_t li = 0; li < c->layers; li++) {
+            const layer_t *l = &m->layers[li];
+            if (l->attention) continue;
+            memcpy(m->qkv, m->qkv_saved[l->slot], keep * (2 * kd + vd) * 4);
+            memcpy(m->ab, m->ab_saved[l->slot], keep * 2 * c->v_heads * 4);
+            float *state = m->parity ? m->conv_state[0][l->slot] : m->conv_state[1][l->slot];
+            float *state_out = m->parity ? m->conv_state[1][l->slot] : m->conv_state[0][l->slot];
+            or_conv(m->q, kd, m->k, kd, m->v, vd, state_out, m->qkv, keep, state, l->conv);
+            or_l2norm(m->q, keep * kd, c->state_dim, c->eps);
+            or_l2norm(m->k, keep * kd, c->state_dim, c->eps);
+            or_delta_net(m->att, m->q, m->k, m->v, m->ab, l->decay, m->ssm_state[l->slot], keep, c->k_heads,
+                         c->v_heads, c->state_dim);
+        }
+    }
+    m->parity = !m->parity;
+    if (m->has_draft) {
+        drafter(m, keep, m->verified_at - 1, 0, 0, tokens);
+        carry_over(m, keep);
+    }
+}
+
+/* LanguageModel::mark and rewind_to_mark (qwen35/mod.rs:1176-1228) */
+void or_model_mark(or_model *m) {
+    for (size_t i = 0; i < m->slots; i++) {
+        memcpy(m->mark_conv[i], m->conv_state[m->parity ? 0 : 1][i], conv_width(m) * 4);
+        memcpy(m->mark_ssm[i], m->ssm_state[i], ssm_width(m) * 4);
+    }
+    if (m->carry) memcpy(m->mark_hidden, m->hidden, m->c.hidden * 4);
+    m->mark_carry = m->carry;
+    m->marked = 1;
+}
+
+int or_model_rewind_to_mark(or_model *m) {
+    if (!m->marked || m->n_verified) return 1;
+    for (size_t i = 0; i < m->slots; i++) {
+        memcpy(m->conv_state[0][i], m->mark_conv[i], conv_width(m) * 4);
+        memcpy(m->ssm_state[i], m->mark_ssm[i], ssm_width(m) * 4);
+    }
+    m->parity = 1;
+    if (m->mark_carry) memcpy(m->hidden, m->mark_hidden, m->c.hidden * 4);
+    m->carry = m->mark_carry;
+    return 0;
+}
+
 void or_model_reset(or_model *m) {
     for (size_t i = 0; i < m->slots; i++) {
         memset(m->conv_state[0][i], 0, conv_width(m) * 4);
@@ -471,4 +571,6 @@ void or_model_reset(or_model *m) {
     }
     m->parity = 0;
     m->carry = 0;
+    m->n_verified = 0;
+    m->marked = 0;
 }

@@ -112,12 +112,17 @@ typedef struct {
     int drafter;
 } or_qwen35_config;
 typedef struct or_model or_model;
+#define OR_MAX_DRAFTS 8  /* qwen35 MAX_DRAFTS (inference/qwen35/mod.rs:26) */
 void or_synthetic_values(uint64_t seed, uint64_t first, size_t n, float sigma, float *out);
 or_model *or_model_synthetic(const or_qwen35_config *cfg, uint64_t seed, int body_fmt, int head_fmt,
                              size_t max_len, size_t batch);
 void or_model_free(or_model *m);
 void or_model_forward(or_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits);
 size_t or_model_draft(or_model *m, uint32_t token, size_t pos, size_t k, uint32_t *drafts);
+void or_model_verify(or_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits);
+void or_model_rewind(or_model *m, size_t keep);
+void or_model_mark(or_model *m);
+int or_model_rewind_to_mark(or_model *m);
 void or_model_reset(or_model *m);
 
 #ifdef __cplusplus

@@ -85,3 +85,242 @@ def test_greedy_tokens_match_the_oracle():
         lo = o.forward([tok_o], pos)
         tok_o = int(np.argmax(lo))
     assert close_calls <= 2
+
+
+# ---- drafting, verifying and rewinding (qwen35/mod.rs:1045-1290)
+
+PREFIX, BATCH = [3, 17, 42, 7, 9], [11, 2, 30, 5]
+REST = [(i * 5 % 43) for i in range(40)]
+
+
+def _verify_and_rewind(spec, plain, keep, tol):
+    """qwen35/mod.rs:1868-1906: a verified batch's rows are the logits after
+    each of its tokens; rewound to `keep` tokens, the model goes on as if it
+    had run those alone, and drafts the same."""
+    spec.forward(PREFIX, 0)
+    plain.forward(PREFIX, 0)
+    rows = spec.verify(BATCH, 5)
+    if isinstance(rows, tuple):
+        rows = rows[0]
+    assert rows.shape == (len(BATCH), spec.cfg.vocab if hasattr(spec.cfg, "vocab") else spec.vocab)
+    for i, token in enumerate(BATCH[:keep]):
+        _close(rows[i], plain.forward([token], 5 + i), tol, f"row {i}")
+    spec.rewind(keep)
+    at = 5 + keep
+    _close(spec.forward([23], at), plain.forward([23], at), tol, "after the rewind")
+    assert spec.draft(8, at + 1, 3) == plain.draft(8, at + 1, 3)
+
+
+@pytest.mark.parametrize("keep", [1, 2, 3, 4])
+def test_oracle_verifying_and_rewinding_runs_the_tokens_kept(keep):
+    cfg = _tiny().as_dict()
+    _verify_and_rewind(O.Model(cfg, SEED), O.Model(cfg, SEED), keep, 1e-4)
+
+
+def test_oracle_drafts_are_the_drafters_picks():
+    # qwen35/mod.rs:1936-1960
+    cfg = _tiny().as_dict()
+    m = O.Model(cfg, SEED)
+    assert m.draft(3, 0, 4) == []
+    m.forward(PREFIX, 0)
+    drafts = m.draft(11, 5, 4)
+    assert len(drafts) == 4 and all(t < cfg["vocab"] for t in drafts)
+    assert m.draft(11, 5, 4) == drafts
+    assert len(m.draft(11, 5, 100)) == 8
+    small = O.Model(cfg, SEED, max_len=8)
+    small.forward(PREFIX, 0)
+    assert len(small.draft(11, 5, 4)) == 2
+
+
+def _rewinding(m):
+    """qwen35/mod.rs:1772-1791: straight through, with a detour, and with the
+    detour taken from a mark rewound to."""
+    m.forward(PREFIX, 0)
+    straight = (m.forward(REST, 5), m.draft(8, 45, 3))
+    m.reset()
+    m.forward(PREFIX, 0)
+    m.forward([11, 2, 30], 5)
+    m.forward([8], 8)
+    detoured = (m.forward(REST, 9), m.draft(8, 49, 3))
+    m.reset()
+    m.forward(PREFIX, 0)
+    m.mark()
+    m.forward([11, 2, 30], 5)
+    m.forward([8], 8)
+    m.rewind_to_mark()
+    rewound = (m.forward(REST, 5), m.draft(8, 45, 3))
+    return straight, detoured, rewound
+
+
+def test_oracle_rewinds_to_a_mark():
+    # qwen35/mod.rs:1793-1824
+    cfg = _tiny().as_dict()
+    straight, detoured, rewound = _rewinding(O.Model(cfg, SEED))
+    assert not np.array_equal(straight[0], detoured[0])
+    assert np.array_equal(straight[0], rewound[0])
+    assert straight[1] == rewound[1]
+    m = O.Model(cfg, SEED)
+    with pytest.raises(RuntimeError):
+        m.rewind_to_mark()
+    m.forward([3, 17], 0)
+    m.mark()
+    m.reset()
+    with pytest.raises(RuntimeError):
+        m.rewind_to_mark()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("keep", [1, 3, 4])
+def test_verifying_and_rewinding_agrees_with_cpu(keep):
+    # qwen35/mod.rs:1919-1934 (2e-2: the batch runs through other kernels
+    # than the single tokens it is compared with)
+    cfg = _tiny()
+    gpu = D.Hip(0)
+    _verify_and_rewind(M.Model(gpu, cfg, SEED, max_len=64), M.Model(gpu, cfg, SEED, max_len=64), keep, 2e-2)
+    # and against the oracle's own verify
+    g = M.Model(gpu, cfg, SEED, max_len=64)
+    o = O.Model(cfg.as_dict(), SEED)
+    g.forward(PREFIX, 0)
+    o.forward(PREFIX, 0)
+    rows, greedy = g.verify(BATCH, 5)
+    want = o.verify(BATCH, 5)
+    for i in range(len(BATCH)):
+        _close(rows[i], want[i], 2e-2, f"row {i} against the oracle")
+    assert greedy == [int(np.argmax(r)) for r in rows]
+    g.rewind(keep)
+    o.rewind(keep)
+    at = 5 + keep
+    _close(g.forward([23], at), o.forward([23], at), 2e-2, "after the rewind, against the oracle")
+    assert g.draft(8, at + 1, 3) == o.draft(8, at + 1, 3)
+
+
+@pytest.mark.gpu
+def test_drafts_match_the_oracle():
+    cfg = _tiny()
+    gpu = D.Hip(0)
+    g = M.Model(gpu, cfg, SEED, max_len=64)
+    o = O.Model(cfg.as_dict(), SEED)
+    assert g.draft(3, 0, 4) == []
+    g.forward(PREFIX, 0)
+    o.forward(PREFIX, 0)
+    drafts = g.draft(11, 5, 4)
+    assert drafts == o.draft(11, 5, 4)
+    assert g.draft(11, 5, 4) == drafts
+    assert len(g.draft(11, 5, 100)) == 8
+    small = M.Model(gpu, cfg, SEED, max_len=8)
+    small.forward(PREFIX, 0)
+    assert len(small.draft(11, 5, 4)) == 2
+
+
+@pytest.mark.gpu
+def test_rewinds_to_a_mark():
+    cfg = _tiny()
+    gpu = D.Hip(0)
+    straight, detoured, rewound = _rewinding(M.Model(gpu, cfg, SEED, max_len=64))
+    assert not np.array_equal(straight[0], detoured[0])
+    _close(rewound[0], straight[0], 2e-3, "rewound on the GPU")
+    assert straight[1] == rewound[1]
+    o_straight, _, _ = _rewinding(O.Model(cfg.as_dict(), SEED))
+    _close(straight[0], o_straight[0], 1e-2, "against the oracle")
+    m = M.Model(gpu, cfg, SEED, max_len=64)
+    with pytest.raises(RuntimeError):
+        m.rewind_to_mark()
+    m.forward([3, 17], 0)
+    m.mark()
+    m.reset()
+    with pytest.raises(RuntimeError):
+        m.rewind_to_mark()
+
+
+@pytest.mark.gpu
+def test_sequences_keep_their_own_state():
+    # qwen35/mod.rs:1962-2051: two sequences interleaved batch by batch on
+    # one model, with a verified draft in one and a mark rewound to in the
+    # other, against each run alone on a model of its own (the oracle).
+    cfg = _tiny()
+    gpu = D.Hip(0)
+    o = O.Model(cfg.as_dict(), SEED)
+    o.forward(PREFIX, 0)
+    first = (o.forward(REST, 5), o.draft(8, 45, 3))
+    o.reset()
+    o.forward([1, 2, 3, 4], 0)
+    second = (o.forward([5, 6], 4), o.draft(7, 6, 3))
+
+    m = M.Model(gpu, cfg, SEED, max_len=64)
+    other = m.add_sequence()
+    assert other == 1
+    m.forward(PREFIX, 0)
+    m.select_sequence(other)
+    m.forward([1, 2, 3], 0)
+    m.select_sequence(0)
+    m.mark()
+    m.forward([11, 2, 30], 5)
+    m.select_sequence(other)
+    with pytest.raises(RuntimeError):
+        m.rewind_to_mark()  # the mark is the first sequence's
+    drafts = m.draft(4, 3, 2)
+    assert len(drafts) == 2
+    m.verify([4] + drafts, 3)
+    with pytest.raises(RuntimeError):
+        m.select_sequence(0)  # not while a batch is being verified
+    m.rewind(1)
+    m.select_sequence(0)
+    m.rewind_to_mark()
+    got_first = (m.forward(REST, 5), m.draft(8, 45, 3))
+    m.select_sequence(other)
+    got_second = (m.forward([5, 6], 4), m.draft(7, 6, 3))
+    _close(got_first[0], first[0], 1e-2, "the first sequence")
+    _close(got_second[0], second[0], 2e-3, "the second sequence")
+    assert got_first[1] == first[1]
+    assert got_second[1] == second[1]
+    with pytest.raises(RuntimeError):
+        m.select_sequence(7)
+
+
+def _greedy(m, prompt, decode):
+    out, tok = [], m.forward_greedy(prompt, 0)
+    while len(out) < decode:
+        out.append(tok)
+        tok = m.forward_greedy([tok], len(prompt) + len(out) - 1)
+    return out
+
+
+def _speculative(m, prompt, decode, k=4):
+    """The greedy speculative loop of qwen35/mod.rs:2103-2141 (Local::step,
+    inference/local.rs:320-368, with a greedy sampler)."""
+    toks = list(prompt)
+    token = m.forward_greedy(toks, 0)
+    out, accepted = [], 0
+    while len(out) < decode:
+        out.append(token)
+        pos = len(toks)
+        drafts = m.draft(token, pos, k)
+        if not drafts:
+            toks.append(token)
+            token = m.forward_greedy([token], pos)
+            continue
+        batch = [token] + drafts
+        _, picks = m.verify(batch, pos, want_logits=False)
+        keep = 1
+        for i, d in enumerate(drafts):
+            if picks[i] != d or len(out) >= decode:
+                break
+            out.append(d)
+            keep += 1
+            accepted += 1
+        m.rewind(keep)
+        toks.extend(batch[:keep])
+        token = picks[keep - 1]
+    return out[:decode], accepted
+
+
+@pytest.mark.gpu
+def test_speculative_decode_is_greedy_decode():
+    # qwen35/mod.rs:2100-2149: token for token the same as plain greedy
+    cfg = _tiny()
+    gpu = D.Hip(0)
+    prompt = [5, 9, 33, 1, 60, 12, 7, 2]
+    plain = _greedy(M.Model(gpu, cfg, SEED + 2, max_len=64), prompt, 30)
+    spec, accepted = _speculative(M.Model(gpu, cfg, SEED + 2, max_len=64), prompt, 30)
+    print(f"speculative: {accepted} drafts accepted")
+    assert spec == plain
