@@ -21,8 +21,9 @@
 // per row and sub-block by the lanes that decode the headers.
 //
 // Per weight that is a quarter of a VALU op to unpack, and the MFMA; the f32
-// path costs over two.  A wave takes up to K blocks of a tile, every weight
-// load issued first; its plane loads are issued per half-block, as it goes.
+// path costs over two.  A wave takes up to K blocks of a tile and issues
+// every load before any compute: the planes of its blocks (parked in LDS,
+// where the B operands are read from), then the weights.
 //
 // Modes: several matrices sharing x in one launch (workgroups find their
 // matrix from their index), x += W·in (gpu/mod.rs:259), and gate and up paired
@@ -38,225 +39,320 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int kMaxWaves = 16;
+// One token's planes from f32 activations.  A workgroup of 256 writes 1024
+// activations (eight lanes a group of 32, four each); with a norm, every
+// workgroup first sums the squares of the whole vector itself, in the same
+// order, so that all of them scale by the same bits.
+constexpr int kPlanesThreads = 256;
 
-DEV float block_sum1024(float v, float *red) {
-    v = group_sum<64>(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float s = 0.0f;
-    for (int i = 0; i < waves; i++) s += red[i];
-    return s;
-}
-
-// One token's planes from f32 activations, in one workgroup; eight lanes take
-// a group of 32, four activations each.
-__global__ void __launch_bounds__(1024) k_planes(const float *__restrict__ x, const float *norm, float eps,
-                                                 float *xn_out, planes::View out) {
-    __shared__ float red[16];
-    const size_t n4 = out.cols / 4;
+__global__ void __launch_bounds__(kPlanesThreads) k_planes(const float *__restrict__ x, const float *norm, float eps,
+                                                           float *xn_out, planes::View out) {
+    __shared__ float red[kPlanesThreads / 64];
+    const unsigned n4 = (unsigned)(out.cols / 4);
     float scale = 1.0f;
     if (norm) {
         float ss = 0.0f;
-        for (size_t i = threadIdx.x; i < n4; i += blockDim.x) {
+        for (unsigned i = threadIdx.x; i < n4; i += kPlanesThreads) {
             const float4 v = ((const float4 *)x)[i];
             ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
         }
-        ss = block_sum1024(ss, red);
+        ss = block_sum<kPlanesThreads>(ss, red);
         scale = 1.0f / sqrtf(ss / (float)out.cols + eps);
     }
     // cols / 4 is a whole number of waves, so every group of 8 lanes is whole
-    for (size_t i = threadIdx.x; i < n4; i += blockDim.x) {
-        float4 v = ((const float4 *)x)[i];
-        if (norm) {
-            const float4 w = ((const float4 *)norm)[i];
-            v.x = v.x * (scale * w.x);
-            v.y = v.y * (scale * w.y);
-            v.z = v.z * (scale * w.z);
-            v.w = v.w * (scale * w.w);
-            if (xn_out) ((float4 *)xn_out)[i] = v;
-        }
-        planes::write8x4(out, i, v);
+    const unsigned i = blockIdx.x * kPlanesThreads + threadIdx.x;
+    if (i >= n4) return;
+    float4 v = ((const float4 *)x)[i];
+    if (norm) {
+        const float4 w = ((const float4 *)norm)[i];
+        v.x = v.x * (scale * w.x);
+        v.y = v.y * (scale * w.y);
+        v.z = v.z * (scale * w.z);
+        v.w = v.w * (scale * w.w);
+        if (xn_out) ((float4 *)xn_out)[i] = v;
     }
+    planes::write8x4(out, i, v);
 }
 
-DEV void scale_min(uint32_t y, uint32_t z, uint32_t w, int j, float &sc, float &mn) {
-    // the 6-bit scale and min of sub-block j (ggml get_scale_min_k4); y, z, w
-    // hold scale bytes 0-3, 4-7, 8-11
-    const int sh = 8 * (j & 3);
-    const uint32_t a = (y >> sh) & 0xffu, bz = (z >> sh) & 0xffu, c = (w >> sh) & 0xffu;
-    if (j < 4) {
-        sc = (float)(a & 63u);
-        mn = (float)(bz & 63u);
-    } else {
-        sc = (float)((c & 0xfu) | ((a >> 6) << 4));
-        mn = (float)((c >> 4) | ((bz >> 6) << 4));
-    }
+// The d·sc and dmin·m of sub-blocks 2k and 2k + 1 (k = 0..3) from the
+// block header words w1, w2, w3 (scale bytes 0-3, 4-7, 8-11), both at once
+// in the two bytes of a 16-bit lane, as ggml's get_scale_min_k4 defines them:
+// sub-block j < 4 keeps 6 bits of scale byte j and of byte j + 4; j >= 4 takes
+// the low / high nibble of byte j + 4 and the top two bits of byte j - 4 / j.
+DEV void scales_pair(uint32_t w1, uint32_t w2, uint32_t w3, int k, float &sc0, float &sc1, float &mn0, float &mn1) {
+    const int sh = 16 * (k & 1);
+    const uint32_t A = (w1 >> sh) & 0xffffu, B = (w2 >> sh) & 0xffffu, C = (w3 >> sh) & 0xffffu;
+    const uint32_t sc = k < 2 ? A & 0x3f3fu : (C & 0x0f0fu) | ((A >> 2) & 0x3030u);
+    const uint32_t mn = k < 2 ? B & 0x3f3fu : ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
+    sc0 = (float)(sc & 0xffu);
+    sc1 = (float)(sc >> 8);
+    mn0 = (float)(mn & 0xffu);
+    mn1 = (float)(mn >> 8);
 }
 
-struct Job {
-    const uint8_t *w;
-    size_t rows;
-    float *out;
-    int add;
-};
+DEV float f16_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// lane j of each quad of lanes, to all four
+template <int J>
+DEV uint32_t quad_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, J * 0x55, 0xf, 0xf, false);
+}
+
+constexpr int kMaxJobs = 4;
+constexpr int kMaxParts = 4;
+// s_waitcnt immediate (gfx9 encoding) waiting for every vector memory
+// operation: vmcnt 0, expcnt and lgkmcnt at their maxima (no wait)
+constexpr int kWaitVm0 = 0x0f70;
 
 struct Args {
-    Job job[4];
-    unsigned first_tile[5];
-    int njobs;
-    int swiglu;  // job 0's out = silu(job 0 · x) · (job 1 · x)
-    size_t nb;
-    int waves;   // per matrix and tile
-    planes::View in;
-    const int8_t *zeros;  // 64 zero bytes: the B operand of lanes with no column
+    const uint8_t *w[kMaxJobs];
+    float *out[kMaxJobs];
+    unsigned rows[kMaxJobs];
+    unsigned first[kMaxJobs];      // first workgroup of each matrix; all ones past the last
+    unsigned tile0[kMaxJobs];      // the matrix's first tile in the launch's tile numbering
+    unsigned add_mask;             // bit j: out[j] += W_j·x, else out[j] = W_j·x
+    unsigned nb;                   // 256-blocks per row
+    unsigned S;                    // waves per matrix in a workgroup
+    unsigned P;                    // workgroups (parts) per tile
+    int swiglu;                    // out[0] = silu(W_0·x) · (W_1·x), waves S..2S-1 taking W_1
+    const int8_t *xq;              // the planes, [3][cols]
+    const float4 *xstat;           // [cols/64]: sums and scales of a pair of groups
+    float *partials;               // P > 1: [tile][part][2][16]
+    unsigned *counters;            // P > 1: [tile], zero between launches
+};
+
+// Per wave LDS, in 16-byte chunks: the planes of its K blocks (chunk
+// 48i + 16p + c holds activations 16c..16c+15 of digit p of block i), the
+// group statistics (chunk 4i + k: sums and scales of groups 2k, 2k + 1 of
+// block i), two zero chunks and the decoded scales ([sub-block][row] floats).
+template <int K>
+struct Lds {
+    static constexpr int kPlaneChunks = (K * 48 + 63) / 64 * 64;
+    static constexpr int kStat = kPlaneChunks;
+    static constexpr int kZero = kStat + 64;
+    static constexpr int kHdr = kZero + 2;
+    static constexpr int kChunks = kHdr + 8 * 16 / 4;
 };
 
 template <int K>
 __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
-    __shared__ float hdr[kMaxWaves][8][16];  // [wave][sub-block][row]: d·sc·s (high nibbles /16)
-    __shared__ float red[kMaxWaves][16];
+    using L = Lds<K>;
+    extern __shared__ uint4 lds_all[];
+    __shared__ float red[16][16];
     const int lane = threadIdx.x & 63, wave_all = threadIdx.x >> 6, kq = lane >> 4, c = lane & 15;
-    const int S = a.waves;
-    int j = 0;
-    while (j + 1 < a.njobs && blockIdx.x >= a.first_tile[j + 1]) j++;
-    const size_t tile = blockIdx.x - a.first_tile[j];
-    const int pairj = a.swiglu && wave_all >= S ? 1 : 0;  // a swiglu workgroup's up half
-    const int wave = wave_all - pairj * S;
-    const Job job = a.job[j + pairj];
-    const size_t nb = a.nb, cols = nb * 256;
-    const int b0 = (int)((size_t)wave * nb / S), b1 = (int)((size_t)(wave + 1) * nb / S);
-    // B: lane (k-group kq, column c) carries digit c % 3 of sub-block 2·kq + h when c / 3 == kq
-    const bool active = c < 12 && c / 3 == kq;
-    const int8_t *xp = active ? a.in.q + (size_t)(c % 3) * cols + 64 * kq : a.zeros;
-    const size_t xstride = active ? 256 : 0;
-    const float4 *xstat = (const float4 *)a.in.stat;
+    // every argument is read up front and selected without branches, so that
+    // the scalar loads of the kernel arguments issue together; a launch's
+    // unused first[] entries are all ones
+    const unsigned S = a.S, P = a.P, nb = a.nb, bx = blockIdx.x;
+    const unsigned f1 = a.first[1], f2 = a.first[2], f3 = a.first[3];
+    const int j = (int)(bx >= f1) + (int)(bx >= f2) + (int)(bx >= f3);
+    const unsigned wg = bx - (j == 0 ? 0u : j == 1 ? f1 : j == 2 ? f2 : f3);
+    const unsigned tile = wg / P, part = wg - tile * P;
+    const int pairj = a.swiglu != 0 && (unsigned)wave_all >= S;  // a swiglu workgroup's W_1 waves
+    const unsigned wave = (unsigned)wave_all - (pairj ? S : 0u);
+    const int jw = j + pairj;
+    const uint8_t *wbase = jw == 0 ? a.w[0] : jw == 1 ? a.w[1] : jw == 2 ? a.w[2] : a.w[3];
+    // this wave's blocks [b0, b1) of the tile: range part·S + wave of P·S
+    const unsigned R = P * S, r = part * S + wave;
+    const unsigned b0 = r * nb / R, b1 = (r + 1) * nb / R;
+    const int nblk = (int)(b1 - b0);
+    const uint8_t *wt = wbase + ((size_t)tile * nb + b0) * q4kt::kUnit;
+    uint4 *my = lds_all + wave_all * L::kChunks;
+    float *hdr = (float *)(my + L::kHdr);
 
+    // every load of the wave is issued before any compute: the planes and
+    // statistics of its blocks first, then the weights
+    constexpr int kPlaneLoads = L::kPlaneChunks / 64;
+    uint4 xc[kPlaneLoads];
+    const unsigned cols = nb * 256;
+#pragma unroll
+    for (int u = 0; u < kPlaneLoads; u++) {
+        // chunks past the wave's blocks reload chunk 0 (no branch around a load)
+        const int ci0 = lane + 64 * u;
+        const int ci = ci0 < nblk * 48 ? ci0 : 0;
+        const unsigned i = (unsigned)ci / 48u, p = ((unsigned)ci % 48u) / 16u, part16 = (unsigned)ci % 16u;
+        xc[u] = *(const uint4 *)(a.xq + p * cols + (b0 + i) * 256u + 16u * part16);
+    }
+    const float4 st = a.xstat[b0 * 4u + (lane < nblk * 4 ? (unsigned)lane : 0u)];
+    uint4 wq[K][2];
+    uint32_t hw[K];
+#pragma unroll
+    for (int i = 0; i < K; i++) {
+        const unsigned off = (unsigned)(i < nblk ? i : 0) * (unsigned)q4kt::kUnit;
+        wq[i][0] = *(const uint4 *)(wt + off + q4kt::qs_off(kq, c));
+        wq[i][1] = *(const uint4 *)(wt + off + q4kt::qs_off(kq, c) + 16);
+        hw[i] = *(const uint32_t *)(wt + off + 4 * lane);
+    }
+    // every chunk is stored, the spare ones too: a store under a branch would
+    // let the compiler sink its load behind the weights
+#pragma unroll
+    for (int u = 0; u < kPlaneLoads; u++) my[lane + 64 * u] = xc[u];
+    ((float4 *)(my + L::kStat))[lane] = st;
+    if (lane < 2) my[L::kZero + lane] = make_uint4(0, 0, 0, 0);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+
+    // B: lane (k-group kq, column c) carries digit c % 3 of sub-block 2·kq + h
+    // when c / 3 == kq, else the zero chunks
+    const bool active = c < 12 && c / 3 == kq;
+    const int bsel = active ? 16 * (c % 3) + 4 * kq : 0;
+    const int sbcol = 2 * (c < 12 ? c / 3 : 0);
+    const int k4 = lane & 3, R4 = lane >> 2;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float macc = 0.0f;
-    {
-        uint4 wq[K][2];
-        uint32_t hw[K];
-        float4 xs[K];
 #pragma unroll
-        for (int i = 0; i < K; i++) {
-            const int b = b0 + i < b1 ? b0 + i : b0;
-            const uint8_t *u = job.w + q4kt::unit(tile, b, nb);
-            wq[i][0] = *(const uint4 *)(u + q4kt::qs_off(kq, c));
-            wq[i][1] = *(const uint4 *)(u + q4kt::qs_off(kq, c) + 16);
-            hw[i] = *(const uint32_t *)(u + 4 * lane);
-            xs[i] = xstat[(size_t)b * 4 + (lane & 3)];
+    for (int i = 0; i < K; i++) {
+        if (i >= nblk) break;
+        {
+            // lane l decodes row l/4's sub-blocks 2(l%4), 2(l%4)+1 from the
+            // header words its quad holds
+            const uint32_t w0 = quad_bcast<0>(hw[i]), w1 = quad_bcast<1>(hw[i]), w2 = quad_bcast<2>(hw[i]),
+                           w3 = quad_bcast<3>(hw[i]);
+            const float d = f16_bits(w0 & 0xffffu), dmin = f16_bits(w0 >> 16);
+            float sc0, sc1, mn0, mn1;
+            scales_pair(w1, w2, w3, k4, sc0, sc1, mn0, mn1);
+            const float4 s4 = ((const float4 *)(my + L::kStat))[4 * i + k4];
+            const float D0 = d * sc0, D1 = d * sc1;
+            // the low nibble is q; the high one arrives as 16·(q − 8), so its
+            // scale is d·sc/16 and 8·d·sc joins the min term
+            macc += (dmin * mn0) * s4.x + (dmin * mn1 - 8.0f * D1) * s4.y;
+            hdr[(2 * k4) * 16 + R4] = D0 * s4.z;
+            hdr[(2 * k4 + 1) * 16 + R4] = (D1 * 0.0625f) * s4.w;
         }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 #pragma unroll
-        for (int i = 0; i < K; i++) {
-            if (b0 + i >= b1) break;
+        for (int h = 0; h < 2; h++) {
+            const uint4 *xv = my + (active ? 48 * i + 2 * h + bsel : L::kZero);
+            const uint4 xq0 = xv[0], xq1 = xv[1];
+            const uint32_t mask = h ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+            v4i C = {0, 0, 0, 0};
             {
-                // lane l decodes row l/4's sub-blocks 2(l%4) and 2(l%4)+1 from
-                // the header words its quad holds
-                const int base = lane & ~3, k = lane & 3, R = lane >> 2;
-                const uint32_t w0 = __shfl(hw[i], base, 64), w1 = __shfl(hw[i], base + 1, 64),
-                               w2 = __shfl(hw[i], base + 2, 64), w3 = __shfl(hw[i], base + 3, 64);
-                const float d = dq::from_f16((uint16_t)(w0 & 0xffffu)), dmin = dq::from_f16((uint16_t)(w0 >> 16));
-                float sc0, mn0, sc1, mn1;
-                scale_min(w1, w2, w3, 2 * k, sc0, mn0);
-                scale_min(w1, w2, w3, 2 * k + 1, sc1, mn1);
-                const float D0 = d * sc0, D1 = d * sc1;
-                macc += (dmin * mn0) * xs[i].x + (dmin * mn1 - 8.0f * D1) * xs[i].y;
-                // the two sub-blocks' activation scales join d·sc
-                hdr[wave_all][2 * k][R] = D0 * xs[i].z;
-                hdr[wave_all][2 * k + 1][R] = (D1 * 0.0625f) * xs[i].w;
+                const uint4 q = wq[i][0];
+                const v4i av = {(int)(q.x & mask), (int)(q.y & mask), (int)(q.z & mask), (int)(q.w & mask)};
+                const v4i bv = {(int)xq0.x, (int)xq0.y, (int)xq0.z, (int)xq0.w};
+                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, C, 0, 0, 0);
             }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint4 *xv = (const uint4 *)(xp + (size_t)(b0 + i) * xstride) + 2 * h;
-                const uint4 xq[2] = {xv[0], xv[1]};
-                const uint32_t mask = h ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-                v4i C = {0, 0, 0, 0};
-#pragma unroll
-                for (int m = 0; m < 2; m++) {
-                    const uint4 q = wq[i][m];
-                    v4i av, bv;
-                    av[0] = (int)(q.x & mask);
-                    av[1] = (int)(q.y & mask);
-                    av[2] = (int)(q.z & mask);
-                    av[3] = (int)(q.w & mask);
-                    bv[0] = (int)xq[m].x;
-                    bv[1] = (int)xq[m].y;
-                    bv[2] = (int)xq[m].z;
-                    bv[3] = (int)xq[m].w;
-                    C = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, C, 0, 0, 0);
-                }
-                const int sb = 2 * (c < 12 ? c / 3 : 0) + h;
-                const float4 D = *(const float4 *)&hdr[wave_all][sb][4 * kq];
-                acc[0] += D.x * (float)C[0];
-                acc[1] += D.y * (float)C[1];
-                acc[2] += D.z * (float)C[2];
-                acc[3] += D.w * (float)C[3];
+            {
+                const uint4 q = wq[i][1];
+                const v4i av = {(int)(q.x & mask), (int)(q.y & mask), (int)(q.z & mask), (int)(q.w & mask)};
+                const v4i bv = {(int)xq1.x, (int)xq1.y, (int)xq1.z, (int)xq1.w};
+                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, C, 0, 0, 0);
             }
-            __builtin_amdgcn_wave_barrier();
+            const float4 D = *(const float4 *)&hdr[(sbcol + h) * 16 + 4 * kq];
+            acc[0] += D.x * (float)C[0];
+            acc[1] += D.y * (float)C[1];
+            acc[2] += D.z * (float)C[2];
+            acc[3] += D.w * (float)C[3];
         }
+        __builtin_amdgcn_wave_barrier();
     }
     // the columns meet, weighted by their digit: lanes 16kq..16kq+15 hold
     // rows 4kq..4kq+3; the min terms of row R sit in lanes 4R..4R+3
     const float f = c < 12 ? (c % 3 == 0 ? 1.0f : c % 3 == 1 ? 256.0f : 65536.0f) : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float v = acc[i] * f;
-        v += __shfl_xor(v, 1, 64);
-        v += __shfl_xor(v, 2, 64);
-        v += __shfl_xor(v, 4, 64);
-        v += __shfl_xor(v, 8, 64);
-        acc[i] = v;
-    }
-    macc += __shfl_xor(macc, 1, 64);
-    macc += __shfl_xor(macc, 2, 64);
-    if (c == 0)
-        for (int i = 0; i < 4; i++) red[wave_all][4 * kq + i] = acc[i];
+    for (int i = 0; i < 4; i++) acc[i] = group_sum<16>(acc[i] * f);
+    macc = group_sum<4>(macc);
+    const float mrow = __shfl(macc, 16 * kq + 4 * (c & 3), 64);
+    if (c < 4) red[wave_all][4 * kq + c] = (c == 0 ? acc[0] : c == 1 ? acc[1] : c == 2 ? acc[2] : acc[3]) - mrow;
     __syncthreads();
-    if ((lane & 3) == 0) red[wave_all][lane >> 2] -= macc;
-    __syncthreads();
-    const Job out_job = a.job[j];
-    const size_t row = tile * 16 + lane;
-    if (wave_all == 0 && lane < 16 && row < out_job.rows) {
-        float v = 0.0f;
-        for (int w = 0; w < S; w++) v += red[w][lane];
-        if (a.swiglu) {
-            float u = 0.0f;
-            for (int w = S; w < 2 * S; w++) u += red[w][lane];
-            v = v * sigmoidf_(v) * u;  // silu(gate) · up (gpu/cpu.rs:238-242)
+    if (wave_all != 0 || lane >= 16) return;
+
+    float v = 0.0f, u = 0.0f;
+    for (unsigned w = 0; w < S; w++) v += red[w][lane];
+    if (a.swiglu)
+        for (unsigned w = S; w < 2 * S; w++) u += red[w][lane];
+    const unsigned gtile = (j == 0 ? a.tile0[0] : j == 1 ? a.tile0[1] : j == 2 ? a.tile0[2] : a.tile0[3]) + tile;
+    if (P > 1) {
+        // the parts of a tile meet in the last workgroup to finish, which sums
+        // them in part order (the same bits whichever finishes last) and
+        // clears the tile's counter for the next launch.  The partial sums go
+        // out as device-coherent stores (written through to the point where
+        // every XCD sees them) and are complete before the counter moves; the
+        // last workgroup reads them device-coherently.  No cache maintenance:
+        // a device-scope fence would write back and invalidate the whole L2
+        // of every workgroup's XCD.
+        float *pp = a.partials + ((size_t)gtile * kMaxParts + part) * 32;
+        __hip_atomic_store(pp + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + 16 + lane, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        unsigned old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(&a.counters[gtile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __shfl(old, 0, 64);
+        if (old != P - 1) return;
+        v = 0.0f;
+        u = 0.0f;
+        const float *tp = a.partials + (size_t)gtile * kMaxParts * 32;
+        for (unsigned q = 0; q < P; q++) {
+            v += __hip_atomic_load(tp + q * 32 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            u += __hip_atomic_load(tp + q * 32 + 16 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        float *o = out_job.out + row;
-        *o = out_job.add ? *o + v : v;
+        if (lane == 0) __hip_atomic_store(&a.counters[gtile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    const unsigned row = tile * 16 + (unsigned)lane;
+    const unsigned rows = j == 0 ? a.rows[0] : j == 1 ? a.rows[1] : j == 2 ? a.rows[2] : a.rows[3];
+    if (row >= rows) return;
+    if (a.swiglu) v = v * sigmoidf_(v) * u;  // silu(gate) · up (gpu/cpu.rs:238-242)
+    float *o = (j == 0 ? a.out[0] : j == 1 ? a.out[1] : j == 2 ? a.out[2] : a.out[3]) + row;
+    *o = (a.add_mask >> j) & 1u ? *o + v : v;
 }
 
-hipError_t run(dwim_dev *dev, Args a) {
-    const size_t nb = a.nb;
-    // blocks per wave (measured on MI355X: 5 for rows of 20 blocks, 3 for 24,
-    // 5-6 for 68), enough waves to cover the row, at most 16 a workgroup
-    const int per = a.swiglu ? 8 : 16;
-    int K = (nb <= 24 && nb % 3 == 0) ? 3 : 5;
-    while ((int)((nb + K - 1) / K) > per) K++;
-    if (K > 6) return hipErrorInvalidValue;
-    a.waves = (int)((nb + K - 1) / K);
-    unsigned total = 0;
-    const unsigned threads = (unsigned)(64 * a.waves * (a.swiglu ? 2 : 1));
-    if (a.swiglu) a.njobs = 1;  // workgroups index gate's tiles; up's are read beside them
-    for (int j = 0; j < a.njobs; j++) {
-        a.first_tile[j] = total;
-        total += (unsigned)q4kt::tiles(a.job[j].rows);
-    }
-    a.first_tile[a.njobs] = total;
-    hipStream_t s = dev->stream;
-    if (K == 3) k_mv_q4k_mfma<3><<<total, threads, 0, s>>>(a);
-    else if (K == 4) k_mv_q4k_mfma<4><<<total, threads, 0, s>>>(a);
-    else if (K == 5) k_mv_q4k_mfma<5><<<total, threads, 0, s>>>(a);
-    else k_mv_q4k_mfma<6><<<total, threads, 0, s>>>(a);
+// Blocks per wave, waves per matrix in a workgroup and workgroups per tile
+// (measured on MI355X): 5 blocks a wave when the launch has 512 tiles or
+// more, else 3 (more, lighter waves for the smaller matrices); a tile's waves
+// split over P workgroups only as far as keeps a workgroup to 8 waves per
+// matrix, since the meeting of the parts costs about a microsecond.
+struct Plan {
+    int K;
+    unsigned S, P;
+};
+
+Plan plan(unsigned nb, unsigned tiles) {
+    Plan p{tiles >= 512 ? 5 : 3, 0, 1};
+    if ((unsigned)p.K > nb) p.K = (int)nb;
+    const unsigned ranges = (nb + p.K - 1) / p.K;
+    while ((ranges + p.P - 1) / p.P > 8 && p.P < (unsigned)kMaxParts) p.P++;
+    p.S = (ranges + p.P - 1) / p.P;
+    return p;
+}
+
+template <int K>
+hipError_t go(dwim_dev *dev, const Args &a, unsigned grid, unsigned waves) {
+    const size_t lds = (size_t)waves * Lds<K>::kChunks * 16;
+    k_mv_q4k_mfma<K><<<grid, waves * 64, lds, dev->stream>>>(a);
     return hipGetLastError();
+}
+
+hipError_t run(dwim_dev *dev, Args a, unsigned njobs, const size_t *rows) {
+    unsigned tiles = 0;
+    for (unsigned j = 0; j < njobs; j++) tiles += (unsigned)q4kt::tiles(rows[j]);
+    const Plan pl = plan(a.nb, tiles);
+    a.S = pl.S;
+    a.P = pl.P;
+    if (a.P > 1 && tiles > dev->mv_tiles_cap) a.P = 1, a.S = (a.nb + pl.K - 1) / pl.K;
+    const unsigned waves = a.S * (a.swiglu ? 2 : 1);
+    if (waves > 16) return hipErrorInvalidValue;
+    unsigned total = 0, t0 = 0;
+    for (unsigned j = 0; j < kMaxJobs; j++) {
+        a.first[j] = j < njobs ? total : 0xffffffffu;
+        a.tile0[j] = t0;
+        if (j < njobs) {
+            const unsigned t = (unsigned)q4kt::tiles(rows[j]);
+            total += t * a.P;
+            t0 += t;
+        }
+    }
+    a.first[0] = 0;
+    a.partials = dev->mv_partials;
+    a.counters = dev->mv_counters;
+    switch (pl.K) {
+        case 1: return go<1>(dev, a, total, waves);
+        case 2: return go<2>(dev, a, total, waves);
+        case 3: return go<3>(dev, a, total, waves);
+        case 4: return go<4>(dev, a, total, waves);
+        case 5: return go<5>(dev, a, total, waves);
+        default: return go<6>(dev, a, total, waves);
+    }
 }
 
 }  // namespace
@@ -271,25 +367,32 @@ hipError_t launch_planes(dwim_dev *dev, const float *x, size_t cols, const float
                          int area) {
     if (cols > planes::kMaxCols || cols % 256) return hipErrorInvalidValue;
     dev->prepared = 0;
-    k_planes<<<1, 1024, 0, dev->stream>>>(x, norm, eps, xn_out, planes_area(dev, area, cols));
+    const unsigned blocks = (unsigned)((cols / 4 + kPlanesThreads - 1) / kPlanesThreads);
+    k_planes<<<blocks, kPlanesThreads, 0, dev->stream>>>(x, norm, eps, xn_out, planes_area(dev, area, cols));
     return hipGetLastError();
 }
 
 hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                               int count, int swiglu, int area) {
-    if (count < 1 || count > 4 || (swiglu && count != 2)) return hipErrorInvalidValue;
+    if (count < 1 || count > kMaxJobs || (swiglu && count != 2)) return hipErrorInvalidValue;
     const size_t cols = ws[0]->cols;
     if (cols > planes::kMaxCols || cols % 256) return hipErrorInvalidValue;
     Args a{};
-    a.nb = cols / 256;
-    a.in = planes_area(dev, area, cols);
-    a.zeros = (const int8_t *)dev->planes + area * planes::kAreaBytes + planes::kZerosOff;
+    a.nb = (unsigned)(cols / 256);
+    const planes::View in = planes_area(dev, area, cols);
+    a.xq = in.q;
+    a.xstat = (const float4 *)in.stat;
+    size_t rows[kMaxJobs];
     for (int j = 0; j < count; j++) {
-        if (ws[j]->cols != cols || ws[j]->fmt != DWIM_Q4_K) return hipErrorInvalidValue;
-        a.job[j] = Job{(const uint8_t *)ws[j]->q, ws[j]->rows, outs[j], adds ? adds[j] : 0};
+        if (ws[j]->cols != cols || ws[j]->fmt != DWIM_Q4_K || ws[j]->rows >= (1u << 31)) return hipErrorInvalidValue;
+        a.w[j] = (const uint8_t *)ws[j]->q;
+        a.out[j] = outs[j];
+        a.rows[j] = (unsigned)ws[j]->rows;
+        rows[j] = ws[j]->rows;
+        if (adds && adds[j]) a.add_mask |= 1u << j;
     }
     if (swiglu && ws[0]->rows != ws[1]->rows) return hipErrorInvalidValue;
-    a.njobs = count;
     a.swiglu = swiglu;
-    return run(dev, a);
+    // a swiglu workgroup takes gate's tile and reads up's beside it
+    return run(dev, a, swiglu ? 1 : (unsigned)count, rows);
 }

@@ -30,6 +30,12 @@ struct dwim_dev {
     size_t split_cap = 0;    // bytes
     float *work = nullptr;   // normalized activations / a product's second result
     size_t work_cap = 0;     // floats
+    // Split one-token Q4_K products (k_mv_q4k_mfma.hip): the partial sums of
+    // up to mv_tiles_cap 16-row tiles (4 parts × 32 floats each) and a counter
+    // per tile, zero between launches.
+    float *mv_partials = nullptr;
+    unsigned *mv_counters = nullptr;
+    unsigned mv_tiles_cap = 0;
     // The open handle and every live buffer, weight and cache hold a
     // reference: the device (its stream) outlives whatever was made on it,
     // whichever order a binding frees them in.
@@ -37,6 +43,8 @@ struct dwim_dev {
 };
 
 void dwim_dev_release(dwim_dev *dev);
+// frees everything a device holds, whatever its reference count
+void dwim_dev_release_resources(dwim_dev *dev);
 
 struct dwim_buf {
     dwim_dev *dev;

@@ -56,6 +56,15 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
         delete dev;
         return dwim_fail("allocating the activation planes failed");
     }
+    // the split matrix products' partial sums and counters
+    dev->mv_tiles_cap = 4096;
+    if (hipMalloc(&dev->mv_partials, (size_t)dev->mv_tiles_cap * 4 * 32 * sizeof(float)) != hipSuccess ||
+        hipMalloc(&dev->mv_counters, (size_t)dev->mv_tiles_cap * sizeof(unsigned)) != hipSuccess ||
+        hipMemset(dev->mv_counters, 0, (size_t)dev->mv_tiles_cap * sizeof(unsigned)) != hipSuccess) {
+        dev->refs = 0;
+        dwim_dev_release_resources(dev);
+        return dwim_fail("allocating the split-product scratch failed");
+    }
     *out = dev;
     return 0;
 }
@@ -71,10 +80,11 @@ float *dev_work(dwim_dev *dev, size_t floats) {
     return dev->work;
 }
 
-void dwim_dev_release(dwim_dev *dev) {
-    if (--dev->refs > 0) return;
+void dwim_dev_release_resources(dwim_dev *dev) {
     hipSetDevice(dev->index);
     hipStreamSynchronize(dev->stream);
+    if (dev->mv_partials) hipFree(dev->mv_partials);
+    if (dev->mv_counters) hipFree(dev->mv_counters);
     if (dev->partials) hipFree(dev->partials);
     if (dev->argmax_buf) hipFree(dev->argmax_buf);
     if (dev->tokens) hipFree(dev->tokens);
@@ -83,6 +93,11 @@ void dwim_dev_release(dwim_dev *dev) {
     if (dev->work) hipFree(dev->work);
     hipStreamDestroy(dev->stream);
     delete dev;
+}
+
+void dwim_dev_release(dwim_dev *dev) {
+    if (--dev->refs > 0) return;
+    dwim_dev_release_resources(dev);
 }
 
 extern "C" void dwim_close(dwim_dev *dev) {
