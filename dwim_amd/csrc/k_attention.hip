@@ -243,7 +243,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ o
         float o = a / L;
         if (gate) o *= sigmoidf_(gate[i]);
         out[i] = o;
-        if (pv.q) planes::write32(pv, i, o);  // D is whole groups of 32 lanes
+        if (pv.q) planes::write16(pv, i, o);  // D is whole groups of 16 lanes
     }
 }
 

@@ -26,8 +26,17 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
                                                         const float *__restrict__ k, const float *__restrict__ v,
                                                         const float *__restrict__ gates,
                                                         const float *__restrict__ decay, float *__restrict__ state,
-                                                        size_t n, int n_k_heads, int n_v_heads) {
+                                                        size_t n, int n_k_heads, int n_v_heads, Rms rms) {
     __shared__ float tile[kD][kCols + 1];
+    __shared__ float red[kThreads / 64];
+    // the gates' RMS scale, when the gate projection took x·w unscaled
+    float gs = 1.0f;
+    if (rms.ss) {
+        float t = 0.0f;
+        for (unsigned g = threadIdx.x; g < rms.groups; g += kThreads) t += rms.ss[g];
+        t = block_sum<kThreads>(t, red);
+        gs = 1.0f / sqrtf(t / rms.cols + rms.eps);
+    }
     const int h = blockIdx.y, c0 = blockIdx.x * kCols;
     const int kh = h / (n_v_heads / n_k_heads);
     const int c = threadIdx.x / kParts, p = threadIdx.x % kParts;
@@ -53,8 +62,8 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
             qq[i] = q4.x; qq[i + 1] = q4.y; qq[i + 2] = q4.z; qq[i + 3] = q4.w;
         }
         const float vj = v[(t * n_v_heads + h) * kD + c0 + c];
-        const float alpha = gates[t * 2 * n_v_heads + h];
-        const float beta = sigmoidf_(gates[t * 2 * n_v_heads + n_v_heads + h]);
+        const float alpha = gs * gates[t * 2 * n_v_heads + h];
+        const float beta = sigmoidf_(gs * gates[t * 2 * n_v_heads + n_v_heads + h]);
         const float g = expf(a * softplusf_(alpha + dt));
         float kv = 0.0f;
 #pragma unroll
@@ -85,8 +94,9 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
 
 hipError_t launch_delta_net(hipStream_t s, float *out, const float *q, const float *k, const float *v,
                             const float *gates, const float *decay, float *state, size_t n, size_t n_k_heads,
-                            size_t n_v_heads, size_t head_dim) {
+                            size_t n_v_heads, size_t head_dim, const Rms *rms) {
     dim3 grid(kD / kCols, (unsigned)n_v_heads);
-    k_delta_net<<<grid, kThreads, 0, s>>>(out, q, k, v, gates, decay, state, n, (int)n_k_heads, (int)n_v_heads);
+    k_delta_net<<<grid, kThreads, 0, s>>>(out, q, k, v, gates, decay, state, n, (int)n_k_heads, (int)n_v_heads,
+                                          rms ? *rms : Rms{});
     return hipGetLastError();
 }

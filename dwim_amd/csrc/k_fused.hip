@@ -122,7 +122,7 @@ __global__ void __launch_bounds__(256) k_gated_norm(float *__restrict__ z, const
     g.z = g.z * sigmoidf_(g.z) * (a.z * (scale * nw.z));
     g.w = g.w * sigmoidf_(g.w) * (a.w * (scale * nw.w));
     ((float4 *)z)[i] = g;
-    if (out.q) planes::write8x4(out, i, g);
+    if (out.q) planes::write4x4(out, i, g);
 }
 
 // The attention projections' epilogue for token t, one block of head_dim

@@ -40,17 +40,20 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 namespace {
 
 // One token's planes from f32 activations.  A workgroup of 256 writes 1024
-// activations (eight lanes a group of 32, four each); with a norm, every
-// workgroup first sums the squares of the whole vector itself, in the same
-// order, so that all of them scale by the same bits.
+// activations (four lanes a group of 16, four each).  With a norm, either
+// (handover = 0) x is RMS-normalized first, every workgroup summing the
+// squares of the whole vector itself in the same order so that all of them
+// scale by the same bits; or (handover = 1) the planes are of x·norm with
+// each group's Σx², for a product that applies the RMS scale itself.
+// xn_out, when given, receives what the planes hold, in f32.
 constexpr int kPlanesThreads = 256;
 
 __global__ void __launch_bounds__(kPlanesThreads) k_planes(const float *__restrict__ x, const float *norm, float eps,
-                                                           float *xn_out, planes::View out) {
+                                                           int handover, float *xn_out, planes::View out) {
     __shared__ float red[kPlanesThreads / 64];
     const unsigned n4 = (unsigned)(out.cols / 4);
     float scale = 1.0f;
-    if (norm) {
+    if (norm && !handover) {
         float ss = 0.0f;
         for (unsigned i = threadIdx.x; i < n4; i += kPlanesThreads) {
             const float4 v = ((const float4 *)x)[i];
@@ -59,11 +62,17 @@ __global__ void __launch_bounds__(kPlanesThreads) k_planes(const float *__restri
         ss = block_sum<kPlanesThreads>(ss, red);
         scale = 1.0f / sqrtf(ss / (float)out.cols + eps);
     }
-    // cols / 4 is a whole number of waves, so every group of 8 lanes is whole
+    // cols / 4 is a whole number of waves, so every group of 4 lanes is whole
     const unsigned i = blockIdx.x * kPlanesThreads + threadIdx.x;
     if (i >= n4) return;
     float4 v = ((const float4 *)x)[i];
     if (norm) {
+        if (handover) {
+            float sq = (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+            sq += __shfl_xor(sq, 1, 64);
+            sq += __shfl_xor(sq, 2, 64);
+            if ((i & 3) == 0) out.ss[i / 4] = sq;
+        }
         const float4 w = ((const float4 *)norm)[i];
         v.x = v.x * (scale * w.x);
         v.y = v.y * (scale * w.y);
@@ -71,7 +80,7 @@ __global__ void __launch_bounds__(kPlanesThreads) k_planes(const float *__restri
         v.w = v.w * (scale * w.w);
         if (xn_out) ((float4 *)xn_out)[i] = v;
     }
-    planes::write8x4(out, i, v);
+    planes::write4x4(out, i, v);
 }
 
 // The d·sc and dmin·m of sub-blocks 2k and 2k + 1 (k = 0..3) from the
@@ -103,6 +112,9 @@ constexpr int kMaxParts = 4;
 // s_waitcnt immediate (gfx9 encoding) waiting for every vector memory
 // operation: vmcnt 0, expcnt and lgkmcnt at their maxima (no wait)
 constexpr int kWaitVm0 = 0x0f70;
+// RMS partial sums a lane loads up front: 6 · 64 groups of 16 cover 6144
+// columns (the rest, if any, are loaded at the end)
+constexpr int kRmsLoads = 6;
 
 struct Args {
     const uint8_t *w[kMaxJobs];
@@ -116,22 +128,34 @@ struct Args {
     unsigned P;                    // workgroups (parts) per tile
     int swiglu;                    // out[0] = silu(W_0·x) · (W_1·x), waves S..2S-1 taking W_1
     const int8_t *xq;              // the planes, [3][cols]
-    const float4 *xstat;           // [cols/64]: sums and scales of a pair of groups
+    const float4 *xstat;           // [cols/64][2]: four groups' scales, then their sums
+    const float *rms_ss;           // given: the planes are x·w, results scale by 1/sqrt(Σ ss / cols + eps)
+    float eps;
+    // given (matrix 0 only): the planes of out[0] (after the add or the
+    // SwiGLU) into `emit`; with emit_norm, of out[0]·emit_norm with each
+    // group's Σ out[0]² (and out[0]·emit_norm in f32 into emit_xw if given)
+    planes::View emit;
+    const float *emit_norm;
+    float *emit_xw;
     float *partials;               // P > 1: [tile][part][2][16]
     unsigned *counters;            // P > 1: [tile], zero between launches
 };
 
 // Per wave LDS, in 16-byte chunks: the planes of its K blocks (chunk
 // 48i + 16p + c holds activations 16c..16c+15 of digit p of block i), the
-// group statistics (chunk 4i + k: sums and scales of groups 2k, 2k + 1 of
-// block i), two zero chunks and the decoded scales ([sub-block][row] floats).
+// group statistics (chunks 8i + 2k and 8i + 2k + 1: scales and sums of groups
+// 4k..4k+3 of block i), two zero chunks and the decoded scales ([group][row]
+// floats).
+// The plane loads come in whole waves of 64 chunks; the spare ones past
+// K·48 are stored into the statistics area, which is written after them.
 template <int K>
 struct Lds {
-    static constexpr int kPlaneChunks = (K * 48 + 63) / 64 * 64;
-    static constexpr int kStat = kPlaneChunks;
+    static constexpr int kPlaneLoads = (K * 48 + 63) / 64;
+    static constexpr int kStat = K * 48;
     static constexpr int kZero = kStat + 64;
     static constexpr int kHdr = kZero + 2;
-    static constexpr int kChunks = kHdr + 8 * 16 / 4;
+    static constexpr int kChunks = kHdr + 16 * 16 / 4;
+    static_assert(kPlaneLoads * 64 <= kZero, "spare plane chunks must land in the statistics area");
 };
 
 template <int K>
@@ -162,7 +186,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
 
     // every load of the wave is issued before any compute: the planes and
     // statistics of its blocks first, then the weights
-    constexpr int kPlaneLoads = L::kPlaneChunks / 64;
+    constexpr int kPlaneLoads = L::kPlaneLoads;
     uint4 xc[kPlaneLoads];
     const unsigned cols = nb * 256;
 #pragma unroll
@@ -173,7 +197,24 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
         const unsigned i = (unsigned)ci / 48u, p = ((unsigned)ci % 48u) / 16u, part16 = (unsigned)ci % 16u;
         xc[u] = *(const uint4 *)(a.xq + p * cols + (b0 + i) * 256u + 16u * part16);
     }
-    const float4 st = a.xstat[b0 * 4u + (lane < nblk * 4 ? (unsigned)lane : 0u)];
+    const float4 st = a.xstat[b0 * 8u + (lane < nblk * 8 ? (unsigned)lane : 0u)];
+    // the RMS partial sums (up to kRmsLoads per lane) are loaded here too,
+    // by every wave and without a branch, and added up at the end
+    const unsigned ng = cols / (unsigned)planes::kGroup;
+    const float *ssrc = a.rms_ss ? a.rms_ss : (const float *)a.xstat;
+    float ssv[kRmsLoads];
+#pragma unroll
+    for (int t = 0; t < kRmsLoads; t++) {
+        const unsigned g = (unsigned)lane + 64u * t;
+        ssv[t] = ssrc[g < ng ? g : 0u];
+    }
+    // and the tile's old outputs (x of x += W·in) and next norm weights
+    const unsigned orow = tile * 16 + (unsigned)(lane & 15);
+    const unsigned orows = j == 0 ? a.rows[0] : j == 1 ? a.rows[1] : j == 2 ? a.rows[2] : a.rows[3];
+    float *const obase = j == 0 ? a.out[0] : j == 1 ? a.out[1] : j == 2 ? a.out[2] : a.out[3];
+    const unsigned orow_c = orow < orows ? orow : 0u;
+    const float old_out = (a.add_mask >> j) & 1u ? obase[orow_c] : 0.0f;
+    const float next_w = a.emit_norm ? a.emit_norm[orow_c] : 0.0f;
     uint4 wq[K][2];
     uint32_t hw[K];
 #pragma unroll
@@ -183,8 +224,9 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
         wq[i][1] = *(const uint4 *)(wt + off + q4kt::qs_off(kq, c) + 16);
         hw[i] = *(const uint32_t *)(wt + off + 4 * lane);
     }
-    // every chunk is stored, the spare ones too: a store under a branch would
-    // let the compiler sink its load behind the weights
+    // every chunk is stored, the spare ones too (a store under a branch would
+    // let the compiler sink its load behind the weights); the statistics
+    // then overwrite the spares
 #pragma unroll
     for (int u = 0; u < kPlaneLoads; u++) my[lane + 64 * u] = xc[u];
     ((float4 *)(my + L::kStat))[lane] = st;
@@ -196,7 +238,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     // when c / 3 == kq, else the zero chunks
     const bool active = c < 12 && c / 3 == kq;
     const int bsel = active ? 16 * (c % 3) + 4 * kq : 0;
-    const int sbcol = 2 * (c < 12 ? c / 3 : 0);
+    const int gcol = 4 * (c < 12 ? c / 3 : 0);  // the column's first group of 16
     const int k4 = lane & 3, R4 = lane >> 2;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float macc = 0.0f;
@@ -204,46 +246,45 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     for (int i = 0; i < K; i++) {
         if (i >= nblk) break;
         {
-            // lane l decodes row l/4's sub-blocks 2(l%4), 2(l%4)+1 from the
-            // header words its quad holds
+            // lane l decodes row l/4's sub-blocks 2(l%4), 2(l%4)+1 (groups
+            // 4(l%4)..4(l%4)+3) from the header words its quad holds
             const uint32_t w0 = quad_bcast<0>(hw[i]), w1 = quad_bcast<1>(hw[i]), w2 = quad_bcast<2>(hw[i]),
                            w3 = quad_bcast<3>(hw[i]);
             const float d = f16_bits(w0 & 0xffffu), dmin = f16_bits(w0 >> 16);
             float sc0, sc1, mn0, mn1;
             scales_pair(w1, w2, w3, k4, sc0, sc1, mn0, mn1);
-            const float4 s4 = ((const float4 *)(my + L::kStat))[4 * i + k4];
+            const float4 xs = ((const float4 *)(my + L::kStat))[8 * i + 2 * k4];
+            const float4 xm = ((const float4 *)(my + L::kStat))[8 * i + 2 * k4 + 1];
             const float D0 = d * sc0, D1 = d * sc1;
             // the low nibble is q; the high one arrives as 16·(q − 8), so its
             // scale is d·sc/16 and 8·d·sc joins the min term
-            macc += (dmin * mn0) * s4.x + (dmin * mn1 - 8.0f * D1) * s4.y;
-            hdr[(2 * k4) * 16 + R4] = D0 * s4.z;
-            hdr[(2 * k4 + 1) * 16 + R4] = (D1 * 0.0625f) * s4.w;
+            macc += (dmin * mn0) * (xm.x + xm.y) + (dmin * mn1 - 8.0f * D1) * (xm.z + xm.w);
+            const float D1h = D1 * 0.0625f;
+            hdr[(4 * k4) * 16 + R4] = D0 * xs.x;
+            hdr[(4 * k4 + 1) * 16 + R4] = D0 * xs.y;
+            hdr[(4 * k4 + 2) * 16 + R4] = D1h * xs.z;
+            hdr[(4 * k4 + 3) * 16 + R4] = D1h * xs.w;
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 #pragma unroll
         for (int h = 0; h < 2; h++) {
+            // the two MFMAs of a half cover its two groups of 16, each summed
+            // apart to take its own activation scale
             const uint4 *xv = my + (active ? 48 * i + 2 * h + bsel : L::kZero);
-            const uint4 xq0 = xv[0], xq1 = xv[1];
             const uint32_t mask = h ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-            v4i C = {0, 0, 0, 0};
-            {
-                const uint4 q = wq[i][0];
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const uint4 q = wq[i][m], xq = xv[m];
                 const v4i av = {(int)(q.x & mask), (int)(q.y & mask), (int)(q.z & mask), (int)(q.w & mask)};
-                const v4i bv = {(int)xq0.x, (int)xq0.y, (int)xq0.z, (int)xq0.w};
-                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, C, 0, 0, 0);
+                const v4i bv = {(int)xq.x, (int)xq.y, (int)xq.z, (int)xq.w};
+                const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const float4 D = *(const float4 *)&hdr[(gcol + 2 * h + m) * 16 + 4 * kq];
+                acc[0] += D.x * (float)C[0];
+                acc[1] += D.y * (float)C[1];
+                acc[2] += D.z * (float)C[2];
+                acc[3] += D.w * (float)C[3];
             }
-            {
-                const uint4 q = wq[i][1];
-                const v4i av = {(int)(q.x & mask), (int)(q.y & mask), (int)(q.z & mask), (int)(q.w & mask)};
-                const v4i bv = {(int)xq1.x, (int)xq1.y, (int)xq1.z, (int)xq1.w};
-                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, C, 0, 0, 0);
-            }
-            const float4 D = *(const float4 *)&hdr[(sbcol + h) * 16 + 4 * kq];
-            acc[0] += D.x * (float)C[0];
-            acc[1] += D.y * (float)C[1];
-            acc[2] += D.z * (float)C[2];
-            acc[3] += D.w * (float)C[3];
         }
         __builtin_amdgcn_wave_barrier();
     }
@@ -256,12 +297,15 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     const float mrow = __shfl(macc, 16 * kq + 4 * (c & 3), 64);
     if (c < 4) red[wave_all][4 * kq + c] = (c == 0 ? acc[0] : c == 1 ? acc[1] : c == 2 ? acc[2] : acc[3]) - mrow;
     __syncthreads();
-    if (wave_all != 0 || lane >= 16) return;
+    if (wave_all != 0) return;
 
+    // wave 0 finishes the tile; lanes 0..15 hold its rows
+    const bool mine = lane < 16;
+    const int rl = lane & 15;
     float v = 0.0f, u = 0.0f;
-    for (unsigned w = 0; w < S; w++) v += red[w][lane];
+    for (unsigned w = 0; w < S; w++) v += red[w][rl];
     if (a.swiglu)
-        for (unsigned w = S; w < 2 * S; w++) u += red[w][lane];
+        for (unsigned w = S; w < 2 * S; w++) u += red[w][rl];
     const unsigned gtile = (j == 0 ? a.tile0[0] : j == 1 ? a.tile0[1] : j == 2 ? a.tile0[2] : a.tile0[3]) + tile;
     if (P > 1) {
         // the parts of a tile meet in the last workgroup to finish, which sums
@@ -273,8 +317,10 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
         // a device-scope fence would write back and invalidate the whole L2
         // of every workgroup's XCD.
         float *pp = a.partials + ((size_t)gtile * kMaxParts + part) * 32;
-        __hip_atomic_store(pp + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(pp + 16 + lane, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (mine) {
+            __hip_atomic_store(pp + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + 16 + lane, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
         unsigned old = 0;
         if (lane == 0) old = __hip_atomic_fetch_add(&a.counters[gtile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -284,17 +330,43 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
         u = 0.0f;
         const float *tp = a.partials + (size_t)gtile * kMaxParts * 32;
         for (unsigned q = 0; q < P; q++) {
-            v += __hip_atomic_load(tp + q * 32 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            u += __hip_atomic_load(tp + q * 32 + 16 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v += __hip_atomic_load(tp + q * 32 + rl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            u += __hip_atomic_load(tp + q * 32 + 16 + rl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         if (lane == 0) __hip_atomic_store(&a.counters[gtile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const unsigned row = tile * 16 + (unsigned)lane;
-    const unsigned rows = j == 0 ? a.rows[0] : j == 1 ? a.rows[1] : j == 2 ? a.rows[2] : a.rows[3];
-    if (row >= rows) return;
+    if (a.rms_ss) {
+        // the RMS norm of the producer's x, from its per-group sums of squares
+        // (in group order, so every workgroup scales by the same bits)
+        float t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kRmsLoads; k++)
+            if ((unsigned)lane + 64u * k < ng) t += ssv[k];
+        for (unsigned g = (unsigned)lane + 64u * kRmsLoads; g < ng; g += 64) t += a.rms_ss[g];
+        t = group_sum<64>(t);
+        const float sc = 1.0f / sqrtf(t / (float)cols + a.eps);
+        v *= sc;
+        u *= sc;
+    }
+    if (!mine) return;
     if (a.swiglu) v = v * sigmoidf_(v) * u;  // silu(gate) · up (gpu/cpu.rs:238-242)
-    float *o = (j == 0 ? a.out[0] : j == 1 ? a.out[1] : j == 2 ? a.out[2] : a.out[3]) + row;
-    *o = (a.add_mask >> j) & 1u ? *o + v : v;
+    const unsigned row = orow;
+    const bool valid = row < orows;
+    if (valid) {
+        v += old_out;
+        obase[row] = v;
+    }
+    if (a.emit.q && j == 0) {
+        // this tile's rows are one group of 16 of the next product's input
+        float e = valid ? v : 0.0f;
+        if (a.emit_norm) {
+            const float sq = group_sum<16>(e * e);
+            if (lane == 0) a.emit.ss[tile] = sq;
+            e = valid ? e * next_w : 0.0f;
+            if (a.emit_xw && valid) a.emit_xw[row] = e;
+        }
+        planes::write16(a.emit, row, e);
+    }
 }
 
 // Blocks per wave, waves per matrix in a workgroup and workgroups per tile
@@ -364,16 +436,16 @@ planes::View planes_area(dwim_dev *dev, int area, size_t cols) {
 }
 
 hipError_t launch_planes(dwim_dev *dev, const float *x, size_t cols, const float *norm, float eps, float *xn_out,
-                         int area) {
+                         int area, int handover) {
     if (cols > planes::kMaxCols || cols % 256) return hipErrorInvalidValue;
     dev->prepared = 0;
     const unsigned blocks = (unsigned)((cols / 4 + kPlanesThreads - 1) / kPlanesThreads);
-    k_planes<<<blocks, kPlanesThreads, 0, dev->stream>>>(x, norm, eps, xn_out, planes_area(dev, area, cols));
+    k_planes<<<blocks, kPlanesThreads, 0, dev->stream>>>(x, norm, eps, handover, xn_out, planes_area(dev, area, cols));
     return hipGetLastError();
 }
 
 hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
-                              int count, int swiglu, int area) {
+                              int count, int swiglu, int area, const MvExtra *extra) {
     if (count < 1 || count > kMaxJobs || (swiglu && count != 2)) return hipErrorInvalidValue;
     const size_t cols = ws[0]->cols;
     if (cols > planes::kMaxCols || cols % 256) return hipErrorInvalidValue;
@@ -393,6 +465,21 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
     }
     if (swiglu && ws[0]->rows != ws[1]->rows) return hipErrorInvalidValue;
     a.swiglu = swiglu;
+    if (extra) {
+        if (extra->rms) {
+            a.rms_ss = in.ss;
+            a.eps = extra->eps;
+        }
+        if (extra->emit_area >= 0) {
+            // the next product's input: whole 256-blocks, in the other area
+            if (extra->emit_area == area || ws[0]->rows % 256 || ws[0]->rows > planes::kMaxCols) return hipErrorInvalidValue;
+            if (!swiglu && count != 1) return hipErrorInvalidValue;
+            a.emit = planes_area(dev, extra->emit_area, ws[0]->rows);
+            a.emit_norm = extra->emit_norm;
+            a.emit_xw = extra->emit_xw;
+            dev->prepared = 0;
+        }
+    }
     // a swiglu workgroup takes gate's tile and reads up's beside it
     return run(dev, a, swiglu ? 1 : (unsigned)count, rows);
 }

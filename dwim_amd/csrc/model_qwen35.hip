@@ -250,19 +250,107 @@ struct dwim_model {
                                          xn_out ? xn_out->data : nullptr));
         return 0;
     }
-    // x += w · (the activations in plane area 0), one token
-    int add_planes(const dwim_weight *w) {
+    // One token through the int8 matrix cores, the activations of each
+    // product handed over as planes: a layer's input arrives in area 0 as the
+    // planes of x·attn_norm with Σx² per group (written by the previous
+    // layer's last product when `handed`, else by launch_planes here); the
+    // mixer's output goes to area 1; the residual product x += o·att writes
+    // the planes of x·mlp_norm into area 0; the SwiGLU pair writes its
+    // result's planes into area 1; and the down product's x += down·h hands
+    // the next layer its input in area 0.  The RMS norms become scales the
+    // consuming products apply to their results.
+    bool handed = false;
+
+    Rms rms0() const {
+        const planes::View in = planes_area(dev, 0, c.hidden);
+        return Rms{in.ss, (unsigned)(c.hidden / planes::kGroup), (float)c.hidden, c.eps};
+    }
+    // x += w · (area `area`), handing the planes of x·norm (and x·norm in f32
+    // to xw when given) on to area `to`
+    int add_handover(const dwim_weight *w, int area, int to, const dwim_buf *norm, dwim_buf *xw) {
         float *o = x->data;
         const int add = 1;
-        DWIM_HIP(launch_mv_q4k_mfma(dev, &w, &o, &add, 1, 0, 0));
+        MvExtra e;
+        e.emit_area = to;
+        e.emit_norm = norm ? norm->data : nullptr;
+        e.emit_xw = xw ? xw->data : nullptr;
+        DWIM_HIP(launch_mv_q4k_mfma(dev, &w, &o, &add, 1, 0, area, norm ? &e : nullptr));
+        return 0;
+    }
+    // products of the layer input (area 0, RMS-scaled)
+    int from_input(const dwim_weight *const *ws, dwim_buf *const *outs, int count) {
+        float *o[4];
+        for (int i = 0; i < count; i++) o[i] = outs[i]->data;
+        MvExtra e;
+        e.rms = 1;
+        e.eps = c.eps;
+        DWIM_HIP(launch_mv_q4k_mfma(dev, ws, o, nullptr, count, 0, 0, &e));
+        return 0;
+    }
+
+    // The one-token layer on the handover path (Pass::layer, qwen35/mod.rs:
+    // 541-655, in the same order); `next` is the following layer's input
+    // norm, to hand its input over, or null.
+    int layer_one(const Layer &l, size_t pos, const dwim_buf *next) {
+        const float eps = c.eps;
+        TRY(dwim_resize(dev, xh, c.hidden));
+        // the DeltaNet gate projection takes x·attn_norm in f32 (xh)
+        if (!handed)
+            DWIM_HIP(launch_planes(dev, x->data, c.hidden, l.attn_norm->data, eps, l.attention ? nullptr : xh->data, 0, 1));
+        handed = false;
+        if (l.attention) {
+            TRY(dwim_resize(dev, q, q_dim()));
+            TRY(dwim_resize(dev, gate, q_dim()));
+            TRY(dwim_resize(dev, k, kv_dim()));
+            TRY(dwim_resize(dev, v, kv_dim()));
+            TRY(dwim_resize(dev, att, q_dim()));
+            dwim_cache *kc = seq.k_cache[l.cache], *vc = seq.v_cache[l.cache];
+            const dwim_weight *ws[4] = {l.q, l.qgate, l.k, l.v};
+            dwim_buf *outs[4] = {q, gate, k, v};
+            TRY(from_input(ws, outs, 4));
+            DWIM_HIP(launch_qk_prep(dev->stream, q->data, k->data, v->data, l.q_norm->data, l.k_norm->data,
+                                    rope->data, 1, pos, c.heads, c.kv_heads, c.head_dim, c.rot_dim, eps, kc, vc));
+            DWIM_HIP(launch_attention_gated(dev, att->data, q->data, kc, vc, 1, pos, c.heads, c.head_dim, c.kv_heads,
+                                            gate->data, 1));
+            TRY(add_handover(l.o, 1, 0, l.mlp_norm, nullptr));
+        } else {
+            TRY(dwim_resize(dev, q, k_dim()));
+            TRY(dwim_resize(dev, k, k_dim()));
+            TRY(dwim_resize(dev, v, v_dim()));
+            TRY(dwim_resize(dev, att, v_dim()));
+            auto &pair = seq.conv_state[l.slot];
+            dwim_buf *state = seq.parity ? pair[0] : pair[1];
+            dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
+            const dwim_weight *ws[2] = {l.qkv, l.z};
+            dwim_buf *outs[2] = {qkv, z};
+            TRY(from_input(ws, outs, 2));
+            // the gate projection, conv, delta rule and gated norm in one
+            // launch, the gate logits from x·attn_norm (xh) RMS-scaled
+            DWIM_HIP(launch_gdn(dev, qkv->data, state->data, state_out->data, l.conv->data, l.ab, xh->data, rms0(),
+                                l.decay->data, seq.ssm_state[l.slot]->data, z->data, l.norm->data, eps, c.k_heads,
+                                c.v_heads, c.state_dim, 1));
+            TRY(add_handover(l.out, 1, 0, l.mlp_norm, nullptr));
+        }
+        // the FFN: gate/up pair from area 0 (RMS-scaled), its planes to area 1
+        const dwim_weight *ws[2] = {l.gate, l.up};
+        float *outs[2] = {up->data, nullptr};
+        MvExtra e;
+        e.rms = 1;
+        e.eps = eps;
+        e.emit_area = 1;
+        DWIM_HIP(launch_mv_q4k_mfma(dev, ws, outs, nullptr, 2, 1, 0, &e));
+        TRY(add_handover(l.down, 1, 0, next, next ? xh : nullptr));
+        handed = next != nullptr;
         return 0;
     }
 
     // Pass::layer (qwen35/mod.rs:541-655).  Verifying, the linear layers
     // save their inputs and run a copy of their recurrent state (:606-632).
-    int layer(const Layer &l, size_t n, size_t pos, bool verify = false) {
+    int layer(const Layer &l, size_t n, size_t pos, bool verify = false, const dwim_buf *next = nullptr) {
         const float eps = c.eps;
         const bool fused = fusable(l), one = fused && n == 1;
+        if (one && !verify) return layer_one(l, pos, next);
+        handed = false;
         TRY(dwim_resize(dev, xh, n * c.hidden));
         if (!fused) TRY(normalize(xh, x, l.attn_norm, n));
         if (l.attention) {
@@ -279,9 +367,8 @@ struct dwim_model {
                 DWIM_HIP(launch_qk_prep(dev->stream, q->data, k->data, v->data, l.q_norm->data, l.k_norm->data,
                                         rope->data, n, pos, c.heads, c.kv_heads, c.head_dim, c.rot_dim, eps, kc, vc));
                 DWIM_HIP(launch_attention_gated(dev, att->data, q->data, kc, vc, n, pos, c.heads, c.head_dim,
-                                                c.kv_heads, gate->data, one ? 0 : -1));
-                if (one) TRY(add_planes(l.o));
-                else TRY(dwim_matmul_add(dev, x, l.o, att, xb));
+                                                c.kv_heads, gate->data, -1));
+                TRY(dwim_matmul_add(dev, x, l.o, att, xb));
             } else {
                 TRY(dwim_matmul(dev, q, l.q, xh));
                 TRY(dwim_matmul(dev, gate, l.qgate, xh));
@@ -315,10 +402,8 @@ struct dwim_model {
                 DWIM_HIP(launch_conv_l2(dev->stream, q->data, k->data, v->data, state_out->data, qkv->data,
                                         state->data, l.conv->data, n, k_dim(), k_dim(), v_dim(), c.state_dim, eps));
                 TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads, c.state_dim));
-                DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps,
-                                           one ? 0 : -1));
-                if (one) TRY(add_planes(l.out));
-                else TRY(dwim_matmul_add(dev, x, l.out, z, xb));
+                DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps, -1));
+                TRY(dwim_matmul_add(dev, x, l.out, z, xb));
             } else {
                 TRY(dwim_matmul(dev, qkv, l.qkv, xh));
                 TRY(dwim_matmul(dev, z, l.z, xh));
@@ -332,15 +417,6 @@ struct dwim_model {
                 TRY(dwim_silu_mul(dev, z, att));
                 TRY(dwim_matmul_add(dev, x, l.out, z, xb));
             }
-        }
-        if (one) {
-            // norm → planes → gate/up pair → planes of its result → x += down · them
-            DWIM_HIP(launch_planes(dev, x->data, c.hidden, l.mlp_norm->data, eps, nullptr, 0));
-            const dwim_weight *ws[2] = {l.gate, l.up};
-            float *outs[2] = {up->data, nullptr};
-            DWIM_HIP(launch_mv_q4k_mfma(dev, ws, outs, nullptr, 2, 1, 0));
-            DWIM_HIP(launch_planes(dev, up->data, c.intermediate, nullptr, eps, nullptr, 0));
-            return add_planes(l.down);
         }
         if (fused) {
             DWIM_HIP(launch_swiglu_q4k(dev, l.gate, l.up, up->data, x->data, n, l.mlp_norm->data, eps));
@@ -373,6 +449,7 @@ struct dwim_model {
         TRY(dwim_matmul(dev, x, draft.embed_proj, xb));
         TRY(dwim_matmul(dev, xb, draft.hidden_proj, xh));
         TRY(dwim_add(dev, x, xb));
+        handed = false;
         TRY(layer(draft.layer, rows, pos));
         return normalize(xh, x, draft.norm, rows);
     }
@@ -401,7 +478,9 @@ struct dwim_model {
                       uint32_t *greedy) {
         TRY(batch(n));
         TRY(dwim_embed(dev, x, embd, tokens, n));
-        for (const Layer &l : layers) TRY(layer(l, n, pos, verify));
+        handed = false;
+        for (size_t i = 0; i < layers.size(); i++)
+            TRY(layer(layers[i], n, pos, verify, i + 1 < layers.size() ? layers[i + 1].attn_norm : nullptr));
         if (!verify) seq.parity = !seq.parity;
         const size_t h = c.hidden;
         if (!has_draft) {

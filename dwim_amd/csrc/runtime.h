@@ -116,12 +116,27 @@ hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_
 // launch_mv_q4k_mfma then runs up to four matrices over that area
 // (outs[j] += or = W_j·x by adds[j]), or gate and up as a SwiGLU pair
 // (swiglu = 1, count = 2, the result in outs[0]).
+// handover = 1 with a norm: the planes of x·norm and each group's Σx²
+// (planes.h), for a product launched with MvExtra::rms.
 size_t planes_scratch_bytes();
 planes::View planes_area(dwim_dev *dev, int area, size_t cols);
 hipError_t launch_planes(dwim_dev *dev, const float *x, size_t cols, const float *norm, float eps, float *xn_out,
-                         int area);
+                         int area, int handover = 0);
+// Optional parts of a one-token product: rms, the input planes are x·w with
+// Σx² per group and every result is scaled by 1/sqrt(Σx²/cols + eps);
+// emit_area >= 0 (one matrix or a SwiGLU pair, rows whole 256-blocks), the
+// planes of outs[0] (after the add or the SwiGLU) go to that area, of
+// outs[0]·emit_norm with Σ outs[0]² per group when emit_norm is given (and
+// outs[0]·emit_norm in f32 to emit_xw when that is given).
+struct MvExtra {
+    int rms = 0;
+    float eps = 0.0f;
+    int emit_area = -1;
+    const float *emit_norm = nullptr;
+    float *emit_xw = nullptr;
+};
 hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
-                              int count, int swiglu, int area);
+                              int count, int swiglu, int area, const MvExtra *extra = nullptr);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
@@ -130,9 +145,18 @@ hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwi
 hipError_t launch_conv(hipStream_t s, float *q, float *k, float *v, float *state_out,
                        const float *x, const float *state, const float *w, size_t n, size_t q_dim,
                        size_t k_dim, size_t v_dim);
+// An RMS scale 1/sqrt(Σ ss / cols + eps) over `groups` partial sums of
+// squares (planes.h), for an operation whose input arrived as x·w unscaled.
+struct Rms {
+    const float *ss = nullptr;
+    unsigned groups = 0;
+    float cols = 1.0f;
+    float eps = 0.0f;
+};
+// with rms, the gate logits (alpha, beta) are scaled by it first
 hipError_t launch_delta_net(hipStream_t s, float *out, const float *q, const float *k,
                             const float *v, const float *gates, const float *decay, float *state,
-                            size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim);
+                            size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim, const Rms *rms = nullptr);
 hipError_t launch_embed(hipStream_t s, float *out, const dwim_weight *w, const uint32_t *tokens,
                         size_t n);
 // first index of each row's maximum, into the first `rows` words of scratch
@@ -162,6 +186,15 @@ hipError_t launch_qk_prep(hipStream_t s, float *q, float *k, const float *v, con
 hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                                   const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
                                   size_t n_kv_heads, const float *gate, int area);
+
+// One token through a gated-DeltaNet mixer (k_gdn.hip): the gate logits
+// W_ab·xw (xw = x·attn_norm unscaled, scaled by rms), conv + SiLU of qkv with
+// its state carried to conv_state_out, l2 norms, the delta rule on `state`,
+// and z ← silu(z)·rmsnorm(o, norm_w) with its planes into `area` (>= 0).
+hipError_t launch_gdn(dwim_dev *dev, const float *qkv, const float *conv_state, float *conv_state_out,
+                      const float *conv_w, const dwim_weight *w_ab, const float *xw, const Rms &rms,
+                      const float *decay, float *state, float *z, const float *norm_w, float eps, size_t nk,
+                      size_t nv, size_t head_dim, int area);
 
 // ---- batches of tokens (k_gemm_q4k.hip) ----
 // out (+)= w · x for n tokens on the f16 matrix cores (x's hi/lo parts are

@@ -87,6 +87,26 @@ def test_greedy_tokens_match_the_oracle():
     assert close_calls <= 2
 
 
+@pytest.mark.gpu
+def test_full_width_layers_agree_with_cpu():
+    """The one-token path at the 27B shape's widths (hidden 5120, SwiGLU
+    17408, 24/4 attention heads of 256, 16/48 DeltaNet heads of 128): four
+    layers (three DeltaNet, one attention) and a 512-token vocabulary, so the
+    oracle builds in seconds.  This runs the split products, the planes
+    handed between them with their RMS scales, and the fused DeltaNet step
+    at their real shapes; the logits after each token agree within 2e-3 of
+    (1 + |logit|)."""
+    cfg = M.config_27b(False)
+    cfg.layers, cfg.vocab = 4, 512
+    gpu = D.Hip(0)
+    g = M.Model(gpu, cfg, SEED + 2, max_len=32)
+    o = O.Model(cfg.as_dict(), SEED + 2)
+    _close(g.forward([3, 17, 42, 7, 9], 0), o.forward([3, 17, 42, 7, 9], 0), 2e-3, "5 tokens")
+    for i, t in enumerate([11, 400, 2, 77, 301, 5, 64, 128]):
+        _close(g.forward([t], 5 + i), o.forward([t], 5 + i), 2e-3, f"token {i}")
+    g.close()
+
+
 # ---- drafting, verifying and rewinding (qwen35/mod.rs:1045-1290)
 
 PREFIX, BATCH = [3, 17, 42, 7, 9], [11, 2, 30, 5]
