@@ -51,19 +51,37 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
 
     const float scale = 1.0f / sqrtf((float)kD);
     const float a = decay[h], dt = decay[n_v_heads + h];
+    // token t + 1's inputs are loaded while token t is computed
+    struct In {
+        float4 k4[kKeys / 4], q4[kKeys / 4];
+        float v, alpha, beta;
+    };
+    auto fetch = [&](size_t t, In &in) {
+        const float4 *kt = (const float4 *)(k + (t * n_k_heads + kh) * kD + p * kKeys);
+        const float4 *qt = (const float4 *)(q + (t * n_k_heads + kh) * kD + p * kKeys);
+#pragma unroll
+        for (int i = 0; i < kKeys / 4; i++) {
+            in.k4[i] = kt[i];
+            in.q4[i] = qt[i];
+        }
+        in.v = v[(t * n_v_heads + h) * kD + c0 + c];
+        in.alpha = gates[t * 2 * n_v_heads + h];
+        in.beta = gates[t * 2 * n_v_heads + n_v_heads + h];
+    };
+    In cur, nxt;
+    if (n > 0) fetch(0, nxt);
     for (size_t t = 0; t < n; t++) {
-        const float *kt = k + (t * n_k_heads + kh) * kD + p * kKeys;
-        const float *qt = q + (t * n_k_heads + kh) * kD + p * kKeys;
+        cur = nxt;
+        if (t + 1 < n) fetch(t + 1, nxt);
         float kk[kKeys], qq[kKeys];
 #pragma unroll
-        for (int i = 0; i < kKeys; i += 4) {
-            float4 k4 = *(const float4 *)(kt + i), q4 = *(const float4 *)(qt + i);
-            kk[i] = k4.x; kk[i + 1] = k4.y; kk[i + 2] = k4.z; kk[i + 3] = k4.w;
-            qq[i] = q4.x; qq[i + 1] = q4.y; qq[i + 2] = q4.z; qq[i + 3] = q4.w;
+        for (int i = 0; i < kKeys / 4; i++) {
+            kk[4 * i] = cur.k4[i].x; kk[4 * i + 1] = cur.k4[i].y; kk[4 * i + 2] = cur.k4[i].z; kk[4 * i + 3] = cur.k4[i].w;
+            qq[4 * i] = cur.q4[i].x; qq[4 * i + 1] = cur.q4[i].y; qq[4 * i + 2] = cur.q4[i].z; qq[4 * i + 3] = cur.q4[i].w;
         }
-        const float vj = v[(t * n_v_heads + h) * kD + c0 + c];
-        const float alpha = gs * gates[t * 2 * n_v_heads + h];
-        const float beta = sigmoidf_(gs * gates[t * 2 * n_v_heads + n_v_heads + h]);
+        const float vj = cur.v;
+        const float alpha = gs * cur.alpha;
+        const float beta = sigmoidf_(gs * cur.beta);
         const float g = expf(a * softplusf_(alpha + dt));
         float kv = 0.0f;
 #pragma unroll

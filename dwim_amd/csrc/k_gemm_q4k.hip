@@ -2,20 +2,27 @@
 // (+)= w[r] · x[t] (dwim gpu/cpu.rs:110-149) on the f16 matrix cores, at
 // close to f32 accuracy.
 //
-// Each weight w (the exact Q4_K value d·sc·q − dmin·m) and each activation x
-// is split in two f16 parts, hi = f16(w), lo = f16(w − hi), and the products
-// hi·hi + hi·lo + lo·hi are summed in f32 by v_mfma_f32_16x16x32_f16: 22 of
-// each operand's bits, the dropped lo·lo term below 2^-21 of the product.
-// k_split writes the activations' parts once per product; the weights are
-// dequantized into LDS by the workgroup that uses them.
+// A Q4_K weight is d·sc·q − dmin·m (per 256-block f16 d and dmin, per
+// 32-sub-block 6-bit sc and m, 4-bit q).  So, per block and row,
+//     w · x = d · Σ_k (sc·q)_k x_k − Σ_sb (dmin·m_sb) X_sb,   X_sb = Σ_{k∈sb} x_k,
+// and sc·q (an integer up to 945) is exact in f16.  The activations are split
+// in two f16 parts x = hi + lo (22 bits), so the first sum is two MFMA chains
+// on exact products, summed in f32 over the whole block and then scaled by
+// d.  The second is one more MFMA per block: its 32 k-slots hold the 8
+// sub-blocks' dmin·m (as f16 hi and lo parts) against X_sb (hi and lo):
+//     [hi, hi, lo, 0] · [X_hi, X_lo, X_hi, 0].
+// 17 MFMAs per block and 16×16 tile, where splitting the weights too would
+// take 24.  k_split writes the activations' parts and sums once per product.
 //
-// A workgroup of 4 waves computes a 128-row × 128-token tile, each wave a
-// 64 × 64 quarter as 4 × 4 MFMA tiles.  It walks the row in steps of one
-// quant group (64 weights): the 128 rows' 64 weights into LDS as hi and lo
-// f16 (two threads a row, each 16 quant bytes: 32 weights), the 128 tokens'
-// 64 activations likewise, then 2 × 16 × 3 MFMAs a wave.  LDS rows are padded
-// to 72 halves so that the 16 lanes reading one k-slice of 16 rows hit
-// different banks.
+// A workgroup of 8 waves computes a 256-row × 128-token tile, in steps of
+// one quant group (64 weights), double-buffered in LDS, one barrier a step.
+// Its waves have two roles, one of each on every SIMD, so that the matrix
+// cores and the vector ALUs work at once: four matrix waves (a 128 × 64 part
+// each, 8 × 4 MFMA tiles) multiply step s out of one buffer while four loader
+// waves dequantize step s + 1 (loaded from global memory during step s − 1)
+// into the other and issue the loads of step s + 2.  LDS rows are 128 bytes whose 16-byte chunks are XOR-swizzled by row,
+// so that the 16 lanes reading one k-slice of 16 rows hit different banks.  Workgroups are numbered XCD-major: those on
+// one XCD share its L2 and mostly one token tile.
 #include "device_util.h"
 #include "layout.h"
 #include "quant_math.h"
@@ -24,192 +31,316 @@
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int kRows = 128, kToks = 128, kStep = 64, kPad = 72;  // halves a padded LDS row
-constexpr int kThreads = 256;
+constexpr int kRows = 256, kToks = 128, kStep = 64;
+constexpr int kThreads = 512;
 
-// x [n][cols] f32 -> xh, xl [n][cols] f16 (hi and lo parts)
-__global__ void k_split(const float *__restrict__ x, _Float16 *__restrict__ xh, _Float16 *__restrict__ xl, size_t total) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    const float v = x[i];
-    const _Float16 h = (_Float16)v;
-    xh[i] = h;
-    xl[i] = (_Float16)(v - (float)h);
-}
-
-DEV void scale_min(const uint8_t *s, int j, float &sc, float &mn) {
-    if (j < 4) {
-        sc = (float)(s[j] & 63);
-        mn = (float)(s[j + 4] & 63);
-    } else {
-        sc = (float)((s[j + 4] & 0xf) | ((s[j - 4] >> 6) << 4));
-        mn = (float)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+// x [n][cols] f32 -> xh, xl [n][cols] f16 (hi and lo parts), and per
+// (token, block) xm [n][nb][16] f16: the 8 sub-block sums' hi parts, then
+// their lo parts.  A thread per (token, sub-block).
+__global__ void k_split(const float *__restrict__ x, _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+                        _Float16 *__restrict__ xm, size_t n, size_t cols) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // sub-block index over [n][cols/32]
+    if (i >= n * (cols / 32)) return;
+    const float4 *src = (const float4 *)(x + i * 32);
+    float s = 0.0f;
+    uint32_t hh[16], ll[16];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float4 v = src[k];
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; q += 2) {
+            const _Float16 h0 = (_Float16)e[q], h1 = (_Float16)e[q + 1];
+            const _Float16 l0 = (_Float16)(e[q] - (float)h0), l1 = (_Float16)(e[q + 1] - (float)h1);
+            hh[2 * k + q / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16;
+            ll[2 * k + q / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | (uint32_t)__builtin_bit_cast(uint16_t, l1) << 16;
+        }
+        s += (v.x + v.y) + (v.z + v.w);
     }
+    uint4 *dh = (uint4 *)(xh + i * 32), *dl = (uint4 *)(xl + i * 32);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        dh[k] = make_uint4(hh[4 * k], hh[4 * k + 1], hh[4 * k + 2], hh[4 * k + 3]);
+        dl[k] = make_uint4(ll[4 * k], ll[4 * k + 1], ll[4 * k + 2], ll[4 * k + 3]);
+    }
+    const size_t t = i / (cols / 32), sb = i % (cols / 32), b = sb / 8, j = sb % 8;
+    _Float16 *m = xm + (t * (cols / 256) + b) * 16;
+    const _Float16 sh = (_Float16)s;
+    m[j] = sh;
+    m[8 + j] = (_Float16)(s - (float)sh);
 }
 
 struct GemmArgs {
     const uint8_t *w;
-    size_t rows, cols, n;
-    const _Float16 *xh, *xl;
+    unsigned rows, cols, n;
+    unsigned rtiles, ttiles, grid;  // row tiles, token tiles, workgroups launched (a multiple of 8)
+    const _Float16 *xh, *xl, *xm;
     float *out;
     int add;
 };
 
-// The global loads of one step (a quant group of a block): this thread's 16
-// quant bytes of its row and, at a block's first group, the row's header; and
-// 32 halves of each part of its token's activations.
+// the physical 16-byte chunk of logical chunk c (0..7) in LDS row r
+DEV int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+// byte k of a 16-byte block header held in registers
+DEV int hbyte(const uint4 &h, int k) {
+    const uint32_t w = k < 4 ? h.x : k < 8 ? h.y : k < 12 ? h.z : h.w;
+    return (int)((w >> (8 * (k & 3))) & 0xffu);
+}
+
+// sub-block j's 6-bit scale and min from the header's 12 packed bytes at
+// offset 4 (ggml get_scale_min_k4)
+DEV void scale_min(const uint4 &h, int j, int &sc, int &mn) {
+    if (j < 4) {
+        sc = hbyte(h, 4 + j) & 63;
+        mn = hbyte(h, 8 + j) & 63;
+    } else {
+        sc = (hbyte(h, 8 + j) & 0xf) | ((hbyte(h, j) >> 6) << 4);
+        mn = (hbyte(h, 8 + j) >> 4) | ((hbyte(h, 4 + j) >> 6) << 4);
+    }
+}
+
+DEV uint32_t pack2(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | (uint32_t)__builtin_bit_cast(uint16_t, b) << 16;
+}
+
+// A loader thread's global loads of one step: its row's 32 quant bytes of
+// the group and 16-byte header, its token's 64 hi or lo activations, and 16
+// bytes of its token's sub-block sums (the header and sums are reloaded every
+// step; they only change per block).
 struct StepLoad {
-    uint4 q, hdr, xh[4], xl[4];
+    uint4 q[2], hdr, x[8], m;
 };
 
 __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
-    extern __shared__ _Float16 lds[];
-    _Float16 *ah = lds, *al = ah + kRows * kPad, *bh = al + kRows * kPad, *bl = bh + kToks * kPad;
+    extern __shared__ uint4 lds[];
+    // [2][256 rows][8 chunks] weights, [2][128][8] activation hi, lo,
+    // [2][256][2] min operands, [2][128][2] sub-block sums, [2][256] d and 1/d
+    uint4 *A = lds, *Bh = A + 2 * kRows * 8, *Bl = Bh + 2 * kToks * 8, *Am = Bl + 2 * kToks * 8,
+          *Xm = Am + 2 * kRows * 2;
+    float *Dd = (float *)(Xm + 2 * kToks * 2), *Di = Dd + 2 * kRows;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave >> 1, wc = wave & 1;  // the wave's 64-row, 64-token quarter
-    const size_t row0 = (size_t)blockIdx.x * kRows, tok0 = (size_t)blockIdx.y * kToks;
-    const size_t nb = a.cols / 256, tiles = q4kt::tiles(a.rows), steps = 4 * nb;
+    // XCD-major numbering: workgroup bx runs on XCD bx % 8
+    const unsigned per = a.grid / 8, lin = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (lin >= a.rtiles * a.ttiles) return;
+    const unsigned tt = lin / a.rtiles, rt = lin % a.rtiles;
+    const unsigned row0 = rt * kRows, tok0 = tt * kToks;
+    const unsigned nb = a.cols / 256, steps = 4 * nb, wtiles = (a.rows + 15) / 16;
 
-    // the weights this thread dequantizes: row lr of the tile, quant bytes 16·lh..16·lh+15
-    const int lr = tid >> 1, lh = tid & 1;
-    const size_t wtile = (row0 + lr) / 16;
-    const bool wlive = wtile < tiles;
-    // the activations this thread stages: token lt, 32 of the step's 64
-    const int lt = tid >> 1, lx = tid & 1;
-    const bool xlive = tok0 + lt < a.n;
-
-    auto fetch = [&](size_t s, StepLoad &L) {
-        const size_t b = s / 4, g = s % 4;
-        if (wlive) {
-            const uint8_t *u = a.w + q4kt::unit(wtile, b, nb);
-            L.q = *(const uint4 *)(u + q4kt::qs_off(g, (row0 + lr) % 16) + 16 * lh);
-            if (g == 0) L.hdr = *(const uint4 *)(u + q4kt::meta_off((row0 + lr) % 16));
-        } else {
-            L.q = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);  // (stored 0 weights)
-            L.hdr = make_uint4(0, 0, 0, 0);
+    if (wave >= 4) {
+        // ---------------- loader waves: 256 threads
+        const int lt = tid - 256;
+        // weights: row ar, the group's 32 quant bytes
+        const int ar = lt;
+        const unsigned wtile = (row0 + ar) / 16;
+        const bool wlive = wtile < wtiles;
+        // activations: token bt, part bq (hi, lo), 64 halves
+        const int bt = lt >> 1, bq = lt & 1;
+        const bool xlive = tok0 + bt < a.n;
+        // sub-block sums: token bt, 16 bytes bq
+        typedef const __attribute__((address_space(1))) u4v *gq;
+        const uint8_t *wsrc = a.w + (size_t)(wlive ? wtile : 0) * nb * q4kt::kUnit;
+        const gq qsrc = (gq)(wsrc + q4kt::qs_off(0, (row0 + ar) % 16));
+        const gq hsrc = (gq)(wsrc + q4kt::meta_off((row0 + ar) % 16));
+        const gq xs0 = (gq)((bq ? a.xl : a.xh) + (size_t)(tok0 + (xlive ? bt : 0)) * a.cols);
+        const gq ms0 = (gq)(a.xm + (size_t)(tok0 + (xlive ? bt : 0)) * nb * 16 + 8 * bq);
+        const uint4 z4 = make_uint4(0, 0, 0, 0);
+        // step s: block s / 4 (unit b·2304), group s % 4 (512 bytes); x at
+        // s·64 halves; sums at b·16 halves
+        auto fetch = [&](unsigned s, StepLoad &L) {
+            const unsigned b = s / 4, g = s % 4;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const uint4 q = __builtin_bit_cast(uint4, qsrc[(b * q4kt::kUnit + g * 512) / 16 + k]);
+                L.q[k] = wlive ? q : z4;
+            }
+            const uint4 h = __builtin_bit_cast(uint4, hsrc[b * q4kt::kUnit / 16]);
+            L.hdr = wlive ? h : z4;  // zero: d = dmin = 0
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint4 v = __builtin_bit_cast(uint4, xs0[s * (kStep / 8) + k]);
+                L.x[k] = xlive ? v : z4;
+            }
+            const uint4 m = __builtin_bit_cast(uint4, ms0[b * 2]);
+            L.m = xlive ? m : z4;
+        };
+        // dequantize step s into buffer s % 2 (and at a block's first group
+        // the block's data into its buffer)
+        auto stage = [&](unsigned s, const StepLoad &L) {
+            const unsigned g = s % 4, buf = s % 2, bb = (s / 4) % 2;
+            const uint4 &hdr = L.hdr;
+            int sc0, mn0, sc1, mn1;
+            scale_min(hdr, 2 * g, sc0, mn0);
+            scale_min(hdr, 2 * g + 1, sc1, mn1);
+            if ((hdr.x & 0x7fffu) == 0) sc0 = sc1 = 0;  // d = 0: the block's products are zero
+            // sc·q exactly in f16: a nibble q ORed into the mantissa of 1024
+            // gives 1024 + q (the high nibble, masked in place, 1024 + 16q),
+            // minus 1024 exactly, times sc (sc/16), exactly; two weights a
+            // packed op
+            const half2v s0 = half2v{(_Float16)sc0, (_Float16)sc0};
+            const half2v s1 = half2v{(_Float16)((float)sc1 * 0.0625f), (_Float16)((float)sc1 * 0.0625f)};
+            const half2v k1024 = half2v{(_Float16)1024.0f, (_Float16)1024.0f};
+            uint4 *row = A + (buf * kRows + ar) * 8;
+#pragma unroll
+            for (int hq = 0; hq < 2; hq++) {  // quant bytes 16·hq..16·hq+15: k = 16·hq.. and 32 + 16·hq..
+                const uint32_t words[4] = {L.q[hq].x, L.q[hq].y, L.q[hq].z, L.q[hq].w};
+                uint32_t lo[8], hi[8];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t p = __builtin_amdgcn_perm(0u, words[k], e ? 0x0c030c02u : 0x0c010c00u);
+                        const half2v ql = __builtin_bit_cast(half2v, (p & 0x000f000fu) | 0x64006400u);
+                        // the high nibble is stored XOR 8
+                        const half2v qh = __builtin_bit_cast(half2v, ((p ^ 0x00800080u) & 0x00f000f0u) | 0x64006400u);
+                        lo[2 * k + e] = __builtin_bit_cast(uint32_t, (half2v)((ql - k1024) * s0));
+                        hi[2 * k + e] = __builtin_bit_cast(uint32_t, (half2v)((qh - k1024) * s1));
+                    }
+                }
+                row[swz(ar, 2 * hq)] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                row[swz(ar, 2 * hq + 1)] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+                row[swz(ar, 4 + 2 * hq)] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                row[swz(ar, 5 + 2 * hq)] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+            }
+            uint4 *xr = (bq ? Bl : Bh) + (buf * kToks + bt) * 8;
+#pragma unroll
+            for (int k = 0; k < 8; k++) xr[swz(bt, k)] = L.x[k];
+            if (g == 0) {
+                // the block's min operands −dmin·m_sb (hi, lo), d (1 when d
+                // is 0) and 1/d, and the tokens' sub-block sums
+                const float d0 = dq::from_f16((uint16_t)(hdr.x & 0xffffu));
+                const float d = d0 != 0.0f ? d0 : 1.0f;
+                const float dmin = -dq::from_f16((uint16_t)(hdr.x >> 16));  // the min term is subtracted
+                uint32_t mh[4], ml[4];
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    int sa, ma, sb_, mb;
+                    scale_min(hdr, j, sa, ma);
+                    scale_min(hdr, j + 1, sb_, mb);
+                    const float va = dmin * (float)ma, vb = dmin * (float)mb;
+                    const _Float16 ha = (_Float16)va, hb = (_Float16)vb;
+                    mh[j / 2] = pack2(ha, hb);
+                    ml[j / 2] = pack2((_Float16)(va - (float)ha), (_Float16)(vb - (float)hb));
+                }
+                Am[(bb * kRows + ar) * 2] = make_uint4(mh[0], mh[1], mh[2], mh[3]);
+                Am[(bb * kRows + ar) * 2 + 1] = make_uint4(ml[0], ml[1], ml[2], ml[3]);
+                Dd[bb * kRows + ar] = d;
+                Di[bb * kRows + ar] = 1.0f / d;
+                Xm[(bb * kToks + bt) * 2 + bq] = L.m;
+            }
+        };
+        StepLoad nxt;
+        fetch(0, nxt);
+        stage(0, nxt);
+        fetch(steps > 1 ? 1 : 0, nxt);
+        __syncthreads();
+        for (unsigned s = 0; s < steps; s++) {
+            // step s + 1 into the idle buffer (after the last step a copy of
+            // it, which nothing reads), step s + 2 into registers
+            stage(s + 1, nxt);
+            fetch(s + 2 < steps ? s + 2 : steps - 1, nxt);
+            __syncthreads();
         }
-        const size_t off = (tok0 + (xlive ? lt : 0)) * a.cols + b * 256 + g * kStep + 32 * lx;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            L.xh[k] = ((const uint4 *)(a.xh + off))[k];
-            L.xl[k] = ((const uint4 *)(a.xl + off))[k];
-        }
-        if (!xlive)
-#pragma unroll
-            for (int k = 0; k < 4; k++) L.xh[k] = L.xl[k] = make_uint4(0, 0, 0, 0);
-    };
+        return;
+    }
 
-    float4v acc[4][4];
+    // ---------------- matrix waves: wave (wr, wc) computes rows 128·wr..,
+    // tokens 64·wc.., as 8 × 4 tiles of 16 × 16.  acc holds the sums in
+    // units of the current block's d: 1/d_b at the block's start, its 16
+    // products of exact f16 integers accumulate, then times d_b and its min
+    // term (negated) added at its end.
+    const int wr = wave >> 1, wc = wave & 1;
+    const int r16 = lane & 15, kg = lane >> 4;
+    float4v acc[8][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 8; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-
-    StepLoad cur, nxt;
-    fetch(0, cur);
-    uint8_t hdr[16];
-    float d = 0.0f, dmin = 0.0f;
-    for (size_t s = 0; s < steps; s++) {
-        const int g = (int)(s % 4);
-        if (g == 0) {
-            // this row's block header: d, dmin and the 6-bit scales and mins
-            __builtin_memcpy(hdr, &cur.hdr, 16);
-            d = dq::from_f16((uint16_t)(hdr[0] | hdr[1] << 8));
-            dmin = dq::from_f16((uint16_t)(hdr[2] | hdr[3] << 8));
-        }
-        // stage the weights: sub-blocks 2g (low nibbles) and 2g+1 (high nibbles)
-        {
-            float sc0, mn0, sc1, mn1;
-            scale_min(hdr + 4, 2 * g, sc0, mn0);
-            scale_min(hdr + 4, 2 * g + 1, sc1, mn1);
-            const float d0 = d * sc0, m0 = dmin * mn0, d1 = d * sc1, m1 = dmin * mn1;
-            const uint32_t words[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
-            // 16 low-nibble weights (sub-block 2g), 16 high (2g+1): hi and lo
-            // halves packed in pairs, written 8 halves at a time
-            uint32_t hh0[8], hl0[8], hh1[8], hl1[8];
+    __syncthreads();
+    auto step = [&](unsigned s, int g) {
+        const unsigned buf = s % 2, bb = (s / 4) % 2;
+        if (g == 0 && s > 0) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t lo = words[k] & 0x0f0f0f0fu, hi = ((words[k] ^ 0x80808080u) >> 4) & 0x0f0f0f0fu;
-                float w0[4], w1[4];
-                w0[0] = d0 * (float)(lo & 0xffu) - m0;
-                w0[1] = d0 * (float)((lo >> 8) & 0xffu) - m0;
-                w0[2] = d0 * (float)((lo >> 16) & 0xffu) - m0;
-                w0[3] = d0 * (float)(lo >> 24) - m0;
-                w1[0] = d1 * (float)(hi & 0xffu) - m1;
-                w1[1] = d1 * (float)((hi >> 8) & 0xffu) - m1;
-                w1[2] = d1 * (float)((hi >> 16) & 0xffu) - m1;
-                w1[3] = d1 * (float)(hi >> 24) - m1;
-#pragma unroll
-                for (int e = 0; e < 2; e++) {
-                    const half2v h0 = half2v{(_Float16)w0[2 * e], (_Float16)w0[2 * e + 1]};
-                    const half2v h1 = half2v{(_Float16)w1[2 * e], (_Float16)w1[2 * e + 1]};
-                    const half2v l0 = half2v{(_Float16)(w0[2 * e] - (float)h0[0]), (_Float16)(w0[2 * e + 1] - (float)h0[1])};
-                    const half2v l1 = half2v{(_Float16)(w1[2 * e] - (float)h1[0]), (_Float16)(w1[2 * e + 1] - (float)h1[1])};
-                    hh0[2 * k + e] = __builtin_bit_cast(uint32_t, h0);
-                    hl0[2 * k + e] = __builtin_bit_cast(uint32_t, l0);
-                    hh1[2 * k + e] = __builtin_bit_cast(uint32_t, h1);
-                    hl1[2 * k + e] = __builtin_bit_cast(uint32_t, l1);
-                }
-            }
-            uint32_t *dh = (uint32_t *)(ah + lr * kPad + 16 * lh), *dl = (uint32_t *)(al + lr * kPad + 16 * lh);
-            *(uint4 *)dh = make_uint4(hh0[0], hh0[1], hh0[2], hh0[3]);
-            *(uint4 *)(dh + 4) = make_uint4(hh0[4], hh0[5], hh0[6], hh0[7]);
-            *(uint4 *)(dh + 16) = make_uint4(hh1[0], hh1[1], hh1[2], hh1[3]);
-            *(uint4 *)(dh + 20) = make_uint4(hh1[4], hh1[5], hh1[6], hh1[7]);
-            *(uint4 *)dl = make_uint4(hl0[0], hl0[1], hl0[2], hl0[3]);
-            *(uint4 *)(dl + 4) = make_uint4(hl0[4], hl0[5], hl0[6], hl0[7]);
-            *(uint4 *)(dl + 16) = make_uint4(hl1[0], hl1[1], hl1[2], hl1[3]);
-            *(uint4 *)(dl + 20) = make_uint4(hl1[4], hl1[5], hl1[6], hl1[7]);
-        }
-        // stage the activations: 32 halves of each part
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            *(uint4 *)(bh + lt * kPad + 32 * lx + 8 * k) = cur.xh[k];
-            *(uint4 *)(bl + lt * kPad + 32 * lx + 8 * k) = cur.xl[k];
-        }
-        __syncthreads();
-        // the next step's loads fly while this step's products run
-        if (s + 1 < steps) {
-            fetch(s + 1, nxt);
-            if ((s + 1) % 4 != 0) nxt.hdr = cur.hdr;
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-            const int ko = kk * 32 + 8 * (lane >> 4);
-            half8 fah[4], fal[4], fbh[4], fbl[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = wr * 64 + i * 16 + (lane & 15);
-                fah[i] = *(const half8 *)(ah + r * kPad + ko);
-                fal[i] = *(const half8 *)(al + r * kPad + ko);
-                const int t = wc * 64 + i * 16 + (lane & 15);
-                fbh[i] = *(const half8 *)(bh + t * kPad + ko);
-                fbl[i] = *(const half8 *)(bl + t * kPad + ko);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 8; i++) {
+                const float4 v = *(const float4 *)&Di[bb * kRows + wr * 128 + i * 16 + 4 * kg];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fah[i], fbh[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fah[i], fbl[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fal[i], fbh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j][0] *= v.x;
+                    acc[i][j][1] *= v.y;
+                    acc[i][j][2] *= v.z;
+                    acc[i][j][3] *= v.w;
+                }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            // every fragment of the slab is read before its 64 MFMAs
+            const int c = 4 * ks + kg;
+            half8 fh[4], fl[4], fa[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int t = wc * 64 + j * 16 + r16;
+                fh[j] = __builtin_bit_cast(half8, Bh[(buf * kToks + t) * 8 + swz(t, c)]);
+                fl[j] = __builtin_bit_cast(half8, Bl[(buf * kToks + t) * 8 + swz(t, c)]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int r = wr * 128 + i * 16 + r16;
+                fa[i] = __builtin_bit_cast(half8, A[(buf * kRows + r) * 8 + swz(r, c)]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fl[j], acc[i][j], 0, 0, 0);
                 }
         }
+        if (g == 3) {
+            // the block ends: times d, plus its min term [−hi, −hi, −lo, 0]·[X_hi, X_lo, X_hi, 0]
+            const half8 zero = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            half8 mx[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int t = wc * 64 + j * 16 + r16;
+                mx[j] = kg == 3 ? zero : __builtin_bit_cast(half8, Xm[(bb * kToks + t) * 2 + (kg == 1)]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int r = wr * 128 + i * 16 + r16;
+                const half8 ma = kg == 3 ? zero : __builtin_bit_cast(half8, Am[(bb * kRows + r) * 2 + (kg == 2)]);
+                const float4 v = *(const float4 *)&Dd[bb * kRows + wr * 128 + i * 16 + 4 * kg];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc[i][j][0] *= v.x;
+                    acc[i][j][1] *= v.y;
+                    acc[i][j][2] *= v.z;
+                    acc[i][j][3] *= v.w;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ma, mx[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
         __syncthreads();
-        cur = nxt;
+    };
+    for (unsigned b = 0; b < nb; b++) {
+        step(4 * b, 0);
+        step(4 * b + 1, 1);
+        step(4 * b + 2, 2);
+        step(4 * b + 3, 3);
     }
     // C tile (i, j): lane holds rows 16i + 4(lane/16) + e of token 16j + lane%16
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const size_t t = tok0 + wc * 64 + j * 16 + (lane & 15);
+        const unsigned t = tok0 + wc * 64 + j * 16 + r16;
         if (t >= a.n) continue;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const size_t r = row0 + wr * 64 + i * 16 + 4 * (lane >> 4);
-            float *o = a.out + t * a.rows + r;
+        for (int i = 0; i < 8; i++) {
+            const unsigned r = row0 + wr * 128 + i * 16 + 4 * kg;
+            float *o = a.out + (size_t)t * a.rows + r;
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 if (r + e < a.rows) o[e] = a.add ? o[e] + acc[i][j][e] : acc[i][j][e];
@@ -217,12 +348,14 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     }
 }
 
+constexpr size_t kLds = (size_t)16 * (2 * kRows * 8 + 4 * kToks * 8 + 2 * kRows * 2 + 2 * kToks * 2) + 2 * 4 * 2 * kRows;
+
 }  // namespace
 
-size_t gemm_split_bytes(size_t n, size_t cols) { return 2 * n * cols * sizeof(_Float16); }
+size_t gemm_split_bytes(size_t n, size_t cols) { return 2 * n * cols * sizeof(_Float16) + n * (cols / 256) * 32; }
 
 hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
-    if (w->fmt != DWIM_Q4_K || w->cols % 256) return hipErrorInvalidValue;
+    if (w->fmt != DWIM_Q4_K || w->cols % 256 || w->rows >= (1u << 31) || n >= (1u << 31)) return hipErrorInvalidValue;
     const size_t need = gemm_split_bytes(n, w->cols);
     if (dev->split_cap < need) {
         if (dev->split) hipFree(dev->split);
@@ -232,20 +365,30 @@ hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, cons
         if (e != hipSuccess) return e;
         dev->split_cap = need;
     }
-    _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * w->cols;
-    const size_t total = n * w->cols;
-    k_split<<<(unsigned)((total + 255) / 256), 256, 0, dev->stream>>>(x, xh, xl, total);
+    _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * w->cols, *xm = xl + n * w->cols;
+    const size_t subs = n * (w->cols / 32);
+    k_split<<<(unsigned)((subs + 255) / 256), 256, 0, dev->stream>>>(x, xh, xl, xm, n, w->cols);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     static bool raised = false;
-    const size_t lds = (size_t)2 * (kRows + kToks) * kPad * sizeof(_Float16);
     if (!raised) {
-        e = hipFuncSetAttribute((const void *)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        e = hipFuncSetAttribute((const void *)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
         if (e != hipSuccess) return e;
         raised = true;
     }
-    GemmArgs a{(const uint8_t *)w->q, w->rows, w->cols, n, xh, xl, out, add};
-    dim3 grid((unsigned)((w->rows + kRows - 1) / kRows), (unsigned)((n + kToks - 1) / kToks));
-    k_gemm_q4k<<<grid, kThreads, lds, dev->stream>>>(a);
+    GemmArgs a{};
+    a.w = (const uint8_t *)w->q;
+    a.rows = (unsigned)w->rows;
+    a.cols = (unsigned)w->cols;
+    a.n = (unsigned)n;
+    a.rtiles = (unsigned)((w->rows + kRows - 1) / kRows);
+    a.ttiles = (unsigned)((n + kToks - 1) / kToks);
+    a.grid = (a.rtiles * a.ttiles + 7) / 8 * 8;
+    a.xh = xh;
+    a.xl = xl;
+    a.xm = xm;
+    a.out = out;
+    a.add = add;
+    k_gemm_q4k<<<a.grid, kThreads, kLds, dev->stream>>>(a);
     return hipGetLastError();
 }

@@ -256,41 +256,69 @@ hipError_t launch_fmt(hipStream_t s, const Weights &w, const float *x, float *ou
 
 }  // namespace
 
-// Batches through a bf16 matrix of few rows (at most 128, as DeltaNet's
-// gate projection has): a block per 8 tokens, the rows' k-slice transposed in
-// LDS so that the threads of a token read consecutive rows, f32 sums in k
-// order as the reference's dot product keeps them per lane (gpu/cpu.rs:370-384
-// sums 8 lanes; the tolerance covers the order).
-constexpr int kSkTok = 8, kSkK = 64;
+// Batches through a bf16 matrix of few rows (at most 96, as DeltaNet's gate
+// projection has): a block of 256 threads per 8 tokens, thread (token t =
+// tid / 32, rows rg, rg + 32, rg + 64) summing in f32 over k (the
+// reference's dot product, gpu/cpu.rs:370-384, sums 8 lanes; the tolerance
+// covers the order).  The k-chunks of 64 are staged in LDS as f32, W [row][k]
+// and x [token][k], each read as float4 along k; the next chunk's global
+// loads are issued before the current chunk is summed.
+constexpr int kSkTok = 8, kSkK = 64, kSkRows = 96;
 
 __global__ void __launch_bounds__(256) k_skinny_bf16(const uint16_t *__restrict__ w, const float *__restrict__ x,
                                                      float *__restrict__ out, size_t rows, size_t cols, size_t n,
                                                      int add) {
-    __shared__ float wt[kSkK][129];  // [k][row], padded
-    __shared__ float xs[kSkTok][kSkK];
-    const int tid = threadIdx.x, tt = tid >> 5, rg = tid & 31;  // token tt, rows rg + 32i
+    __shared__ float4 ws[kSkRows][kSkK / 4 + 1];  // [row][k/4], padded
+    __shared__ float4 xs[kSkTok][kSkK / 4];
+    const int tid = threadIdx.x, tt = tid >> 5, rg = tid & 31;
     const size_t t0 = (size_t)blockIdx.x * kSkTok;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (size_t k0 = 0; k0 < cols; k0 += kSkK) {
-        for (int i = tid; i < kSkK * 128; i += 256) {
-            const int r = i / kSkK, k = i % kSkK;
-            wt[k][r] = r < (int)rows ? dq::bf16_to_f32(w[r * cols + k0 + k]) : 0.0f;
-        }
-        for (int i = tid; i < kSkTok * kSkK; i += 256) {
-            const int t = i / kSkK, k = i % kSkK;
-            xs[t][k] = t0 + t < n ? x[(t0 + t) * cols + k0 + k] : 0.0f;
-        }
-        __syncthreads();
-        for (int k = 0; k < kSkK; k++) {
-            const float xv = xs[tt][k];
+    // a chunk: 96 rows × 64 k of bf16 = 768 16-byte loads (3 a thread), and
+    // 8 tokens × 64 k of f32 = 128 16-byte loads (threads < 128)
+    uint4 wr[3];
+    float4 xr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto load = [&](size_t k0) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] += wt[k][rg + 32 * i] * xv;
+        for (int i = 0; i < 3; i++) {
+            const int e = tid + 256 * i, r = e >> 3, kk = (e & 7) * 8;
+            wr[i] = r < (int)rows ? *(const uint4 *)(w + (size_t)r * cols + k0 + kk) : make_uint4(0, 0, 0, 0);
         }
+        if (tid < kSkTok * kSkK / 4) {
+            const int t = tid >> 4, kk = (tid & 15) * 4;
+            xr = t0 + t < n ? *(const float4 *)(x + (t0 + t) * cols + k0 + kk) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    load(0);
+    float acc[3] = {0.0f, 0.0f, 0.0f};
+    for (size_t k0 = 0; k0 < cols; k0 += kSkK) {
         __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+            const int e = tid + 256 * i, r = e >> 3, q = (e & 7) * 2;
+            const uint32_t v[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+            ws[r][q] = make_float4(dq::bf16_to_f32((uint16_t)(v[0] & 0xffffu)), dq::bf16_to_f32((uint16_t)(v[0] >> 16)),
+                                   dq::bf16_to_f32((uint16_t)(v[1] & 0xffffu)), dq::bf16_to_f32((uint16_t)(v[1] >> 16)));
+            ws[r][q + 1] = make_float4(dq::bf16_to_f32((uint16_t)(v[2] & 0xffffu)), dq::bf16_to_f32((uint16_t)(v[2] >> 16)),
+                                       dq::bf16_to_f32((uint16_t)(v[3] & 0xffffu)), dq::bf16_to_f32((uint16_t)(v[3] >> 16)));
+        }
+        if (tid < kSkTok * kSkK / 4) xs[tid >> 4][tid & 15] = xr;
+        __syncthreads();
+        if (k0 + kSkK < cols) load(k0 + kSkK);
+#pragma unroll 4
+        for (int q = 0; q < kSkK / 4; q++) {
+            const float4 xv = xs[tt][q];
+#pragma unroll
+            for (int i = 0; i < 3; i++) {
+                const float4 wv = ws[rg + 32 * i][q];
+                acc[i] += wv.x * xv.x;
+                acc[i] += wv.y * xv.y;
+                acc[i] += wv.z * xv.z;
+                acc[i] += wv.w * xv.w;
+            }
+        }
     }
     if (t0 + tt >= n) return;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 3; i++) {
         const size_t r = rg + 32 * i;
         if (r < rows) {
             float *o = out + (t0 + tt) * rows + r;
@@ -308,7 +336,7 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
     case DWIM_Q4_0: return launch_fmt<DWIM_Q4_0>(s, w, x, out, n, add);
     case DWIM_Q8_0: return launch_fmt<DWIM_Q8_0>(s, w, x, out, n, add);
     default:
-        if (n >= 16 && wt->rows <= 128 && wt->cols % kSkK == 0) {
+        if (n >= 16 && wt->rows <= kSkRows && wt->cols % kSkK == 0) {
             k_skinny_bf16<<<(unsigned)((n + kSkTok - 1) / kSkTok), 256, 0, s>>>((const uint16_t *)wt->q, x, out,
                                                                                wt->rows, wt->cols, n, add);
             return hipGetLastError();
