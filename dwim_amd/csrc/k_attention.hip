@@ -247,6 +247,240 @@ __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ o
     }
 }
 
+
+// ---------------------------------------------------------------- prefill
+//
+// Causal GQA for a batch of tokens on the f16 matrix cores (flash attention
+// with an online softmax), head_dim 256.  A block of 4 waves takes one query
+// head and 64 tokens, a wave 16 of them; the queries stay in registers as f16
+// hi + lo parts (times 1/16 = 1/sqrt(256), exact).  The block walks the
+// positions in blocks of 32:
+//   * the keys, int8 (exact in f16), give per 32-dimension group g the sums
+//     Σ q·k8 (two MFMAs, hi and lo), which the group's f16 cache scale then
+//     weights: S = Σ_g s_k[p][g] · Σ_{d∈g} q_d k8_d;
+//   * the online softmax (gpu/cpu.rs:388-423 takes the max first, then
+//     exp(s − max) / Σ): each row's running max and sum, the output rescaled
+//     when the max grows;
+//   * the values, dequantized exactly (v8·s as f32) into f16 hi + lo,
+//     transposed in LDS so that the MFMA operands read 8 positions as one
+//     16-byte chunk, and P as hi + lo: O += P_hi·V_hi + P_hi·V_lo + P_lo·V_hi.
+typedef _Float16 ahalf8 __attribute__((ext_vector_type(8)));
+typedef float afloat4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFD = 256, kFQ = 64, kFP = 32, kFThreads = 256;
+
+struct PrefillArgs {
+    float *out;
+    const float *q, *gate;
+    const int8_t *kq, *vq;
+    const uint16_t *ks, *vs;
+    unsigned n, pos, heads, kv_heads;
+};
+
+DEV ahalf8 hi8(const float *v) {
+    ahalf8 h;
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = (_Float16)v[i];
+    return h;
+}
+DEV ahalf8 lo8(const float *v, const ahalf8 &h) {
+    ahalf8 l;
+#pragma unroll
+    for (int i = 0; i < 8; i++) l[i] = (_Float16)(v[i] - (float)h[i]);
+    return l;
+}
+
+__global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a) {
+    __shared__ uint4 kf[kFP * kFD / 8];          // keys as f16, [pos][256], 16-byte chunks swizzled by pos
+    __shared__ float ksc[kFP][kFD / 32];         // key scales
+    __shared__ uint32_t v8[kFP][kFD / 4];        // values, int8, [pos][256]
+    __shared__ float vsc[kFP][kFD / 32];         // value scales
+    __shared__ uint4 vt[2][kFD][kFP / 8];        // values hi / lo, [dim][pos]
+    __shared__ uint4 pw[4][2][16][kFP / 8];      // per wave: P hi / lo, [row][pos]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, kg = lane >> 4;
+    const unsigned h = blockIdx.y, kvh = h / (a.heads / a.kv_heads);
+    const unsigned t0 = blockIdx.x * kFQ;
+    const unsigned kv_dim = a.kv_heads * kFD;
+    const unsigned last = min(t0 + kFQ, a.n) - 1;   // the block's last token
+    const unsigned len = a.pos + last + 1;         // positions it attends to
+
+    // the wave's 16 queries as A fragments: row r16, dims 32g + 8kg..+7
+    ahalf8 qh[8], ql[8];
+    {
+        const unsigned t = t0 + 16 * w + r16;
+        const bool live = t < a.n;
+        const float *qr = a.q + ((size_t)(live ? t : 0) * a.heads + h) * kFD;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            float v[8];
+            const float4 x0 = *(const float4 *)(qr + 32 * g + 8 * kg), x1 = *(const float4 *)(qr + 32 * g + 8 * kg + 4);
+            v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = live ? v[i] * 0.0625f : 0.0f;
+            qh[g] = hi8(v);
+            ql[g] = lo8(v, qh[g]);
+        }
+    }
+    // this lane's rows (C layout): 4kg + e of the wave's 16; their tokens
+    unsigned tr[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) tr[e] = t0 + 16 * w + 4 * kg + e;
+    float m[4], l[4];
+    afloat4 o[16];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        m[e] = -INFINITY;
+        l[e] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) o[i] = afloat4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (unsigned p0 = 0; p0 < len; p0 += kFP) {
+        // ---- stage the 32 positions: keys to f16, values raw, scales
+        __syncthreads();
+        {
+            const int pp = tid >> 3, c = tid & 7;  // position, 32-byte piece
+            const unsigned p = p0 + pp;
+            const bool live = p < len;
+            const size_t row = (size_t)(live ? p : 0) * kv_dim + (size_t)kvh * kFD;
+            const uint4 k0 = live ? *(const uint4 *)(a.kq + row + 32 * c) : make_uint4(0, 0, 0, 0);
+            const uint4 k1 = live ? *(const uint4 *)(a.kq + row + 32 * c + 16) : make_uint4(0, 0, 0, 0);
+            const uint4 w0 = live ? *(const uint4 *)(a.vq + row + 32 * c) : make_uint4(0, 0, 0, 0);
+            const uint4 w1 = live ? *(const uint4 *)(a.vq + row + 32 * c + 16) : make_uint4(0, 0, 0, 0);
+            const uint16_t sk = live ? a.ks[row / 32 + c] : 0, sv = live ? a.vs[row / 32 + c] : 0;
+            ksc[pp][c] = dq::from_f16(sk);
+            vsc[pp][c] = dq::from_f16(sv);
+            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {  // 8 keys a 16-byte chunk of f16
+                uint32_t hw[4];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint32_t word = kw[2 * q + e];
+                    const _Float16 b0 = (_Float16)(float)(int8_t)(word & 0xffu), b1 = (_Float16)(float)(int8_t)((word >> 8) & 0xffu);
+                    const _Float16 b2 = (_Float16)(float)(int8_t)((word >> 16) & 0xffu), b3 = (_Float16)(float)(int8_t)(word >> 24);
+                    hw[2 * e] = (uint32_t)__builtin_bit_cast(uint16_t, b0) | (uint32_t)__builtin_bit_cast(uint16_t, b1) << 16;
+                    hw[2 * e + 1] = (uint32_t)__builtin_bit_cast(uint16_t, b2) | (uint32_t)__builtin_bit_cast(uint16_t, b3) << 16;
+                }
+                const int chunk = 4 * c + q;  // of 32 per row
+                kf[pp * 32 + (chunk ^ (pp & 15))] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            }
+            const uint32_t vw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++) v8[pp][8 * c + q] = vw[q];
+        }
+        __syncthreads();
+        // ---- the values transposed: thread (dims 4dq..4dq+3, positions 8j..8j+7)
+        {
+            const int dq4 = tid & 63, j = tid >> 6;
+            float vv[4][8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int p = 8 * j + i;
+                const uint32_t word = v8[p][dq4];
+                const float sc = vsc[p][dq4 / 8];
+#pragma unroll
+                for (int d = 0; d < 4; d++) vv[d][i] = (float)(int8_t)((word >> (8 * d)) & 0xffu) * sc;
+            }
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const ahalf8 hh = hi8(vv[d]), ll = lo8(vv[d], hh);
+                vt[0][4 * dq4 + d][j] = __builtin_bit_cast(uint4, hh);
+                vt[1][4 * dq4 + d][j] = __builtin_bit_cast(uint4, ll);
+            }
+        }
+        __syncthreads();
+        // ---- scores of the wave's 16 rows against the 32 positions (2 tiles)
+        afloat4 sacc[2];
+#pragma unroll
+        for (int tcol = 0; tcol < 2; tcol++) {
+            sacc[tcol] = afloat4{0.0f, 0.0f, 0.0f, 0.0f};
+            const int pp = 16 * tcol + r16;  // B column: position
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const ahalf8 kb = __builtin_bit_cast(ahalf8, kf[pp * 32 + ((4 * g + kg) ^ (pp & 15))]);
+                afloat4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[g], kb, afloat4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[g], kb, c, 0, 0, 0);
+                const float sc = ksc[pp][g];  // C column r16 is this position
+#pragma unroll
+                for (int e = 0; e < 4; e++) sacc[tcol][e] += sc * c[e];
+            }
+        }
+        // ---- mask, online softmax (rows 4kg + e; the 16 lanes of a row group hold its columns)
+        float pv[2][4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int tcol = 0; tcol < 2; tcol++) {
+                const unsigned p = p0 + 16 * tcol + r16;
+                const bool ok = p <= a.pos + tr[e] && p < len;
+                pv[tcol][e] = ok ? sacc[tcol][e] : -INFINITY;
+                mx = fmaxf(mx, pv[tcol][e]);
+            }
+#pragma unroll
+            for (int k = 1; k < 16; k <<= 1) mx = fmaxf(mx, __shfl_xor(mx, k, 64));
+            const float mn = fmaxf(m[e], mx);
+            const float alpha = mn == -INFINITY ? 1.0f : expf(m[e] - mn);
+            float sum = 0.0f;
+#pragma unroll
+            for (int tcol = 0; tcol < 2; tcol++) {
+                const float pe = pv[tcol][e] == -INFINITY ? 0.0f : expf(pv[tcol][e] - mn);
+                pv[tcol][e] = pe;
+                sum += pe;
+            }
+#pragma unroll
+            for (int k = 1; k < 16; k <<= 1) sum += __shfl_xor(sum, k, 64);
+            l[e] = l[e] * alpha + sum;
+            m[e] = mn;
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[i][e] *= alpha;
+        }
+        // ---- P to the A layout through the wave's LDS tile (hi, lo)
+        {
+            _Float16 *ph = (_Float16 *)&pw[w][0][0][0], *pl = (_Float16 *)&pw[w][1][0][0];
+#pragma unroll
+            for (int tcol = 0; tcol < 2; tcol++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int row = 4 * kg + e, col = 16 * tcol + r16;
+                    const _Float16 hv = (_Float16)pv[tcol][e];
+                    ph[row * kFP + col] = hv;
+                    pl[row * kFP + col] = (_Float16)(pv[tcol][e] - (float)hv);
+                }
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const ahalf8 pa_h = __builtin_bit_cast(ahalf8, pw[w][0][r16][kg]);
+        const ahalf8 pa_l = __builtin_bit_cast(ahalf8, pw[w][1][r16][kg]);
+        // ---- O += P·V over the 16 dimension tiles
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int d = 16 * i + r16;  // B column: dimension
+            const ahalf8 vh = __builtin_bit_cast(ahalf8, vt[0][d][kg]);
+            const ahalf8 vl = __builtin_bit_cast(ahalf8, vt[1][d][kg]);
+            o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa_h, vh, o[i], 0, 0, 0);
+            o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa_h, vl, o[i], 0, 0, 0);
+            o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa_l, vh, o[i], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    // ---- out = O / l, gated
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const unsigned t = tr[e];
+        if (t >= a.n) continue;
+        const float inv = 1.0f / l[e];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const size_t idx = ((size_t)t * a.heads + h) * kFD + 16 * i + r16;
+            float r = o[i][e] * inv;
+            if (a.gate) r *= sigmoidf_(a.gate[idx]);
+            a.out[idx] = r;
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k, const dwim_cache *v,
@@ -266,6 +500,14 @@ hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, con
             return hipErrorInvalidValue;
         pv = planes_area(dev, area, n_heads * head_dim);
         dev->prepared = 0;
+    }
+    if (n >= 16 && area < 0 && head_dim == (size_t)kFD && n_heads % n_kv_heads == 0) {
+        // a batch of tokens: flash attention on the matrix cores
+        PrefillArgs pa{out, q, gate, k->q, v->q, k->s, v->s, (unsigned)n, (unsigned)pos, (unsigned)n_heads,
+                       (unsigned)n_kv_heads};
+        dim3 grid((unsigned)((n + kFQ - 1) / kFQ), (unsigned)n_heads);
+        k_attn_prefill<<<grid, kFThreads, 0, dev->stream>>>(pa);
+        return hipGetLastError();
     }
     size_t len = pos + n;
     const size_t ch = kPos;
