@@ -5,22 +5,38 @@
 // S stored s[key][value].
 //
 // Every value column j of S evolves on its own: kv[j], the update of column j
-// and o[j] read only column j.  So a block owns 32 columns of one head (grid =
-// 4 × n_v_heads) and keeps its 128×32 slice of the fp32 state in registers
+// and o[j] read only column j.  So a block owns 16 columns of one head (grid
+// = 8 × n_v_heads) and keeps its 128×16 slice of the fp32 state in registers
 // across all the batch's tokens: thread (column c, part p) holds keys
-// 16p..16p+15 of column c, and the 8 parts of a column are 8 adjacent lanes
-// whose partial sums meet by shuffles.  The slice is read from HBM once and
-// written once per call, through LDS so that both are coalesced.
+// 8p..8p+7 of column c, and the 16 parts of a column are 16 adjacent lanes
+// whose partial sums meet by DPP moves.  The token loop is a chain of
+// dependent steps, so it is kept short: the gates (g, beta) of a run of
+// tokens are computed once per block into LDS, the next token's inputs are
+// loaded while the current one is computed, and each sum runs in two
+// accumulators.  The slice is read from HBM once and written once per call,
+// through LDS so that both are coalesced.
 #include "device_util.h"
 #include "runtime.h"
 
 namespace {
 
 constexpr int kD = 128;      // head_dim (the reference asserts 128, gpu/cuda/mod.rs:1437)
-constexpr int kCols = 32;    // value columns per block
-constexpr int kParts = 8;    // key parts per column
+constexpr int kCols = 16;    // value columns per block
+constexpr int kParts = 16;   // key parts per column
 constexpr int kKeys = kD / kParts;
 constexpr int kThreads = kCols * kParts;
+constexpr int kGRun = 1024;  // tokens whose gates a block tabulates at once
+
+// sum over 16 aligned adjacent lanes, every lane getting it: quad xor 1 and
+// 2, then the half-row mirror (lane i and 7 − i) and the row mirror (i and
+// 15 − i)
+DEV float sum16(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false));
+    return v;
+}
 
 __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out, const float *__restrict__ q,
                                                         const float *__restrict__ k, const float *__restrict__ v,
@@ -29,6 +45,7 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
                                                         size_t n, int n_k_heads, int n_v_heads, Rms rms) {
     __shared__ float tile[kD][kCols + 1];
     __shared__ float red[kThreads / 64];
+    __shared__ float2 gb[kGRun];  // per token: g, beta
     // the gates' RMS scale, when the gate projection took x·w unscaled
     float gs = 1.0f;
     if (rms.ss) {
@@ -42,7 +59,7 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
     const int c = threadIdx.x / kParts, p = threadIdx.x % kParts;
     float *S = state + (size_t)h * kD * kD;
 
-    // state slice in: rows of 32 columns, coalesced
+    // state slice in: rows of 16 columns, coalesced
     for (int e = threadIdx.x; e < kD * kCols; e += kThreads) tile[e / kCols][e % kCols] = S[(e / kCols) * kD + c0 + e % kCols];
     __syncthreads();
     float s[kKeys];
@@ -54,7 +71,7 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
     // token t + 1's inputs are loaded while token t is computed
     struct In {
         float4 k4[kKeys / 4], q4[kKeys / 4];
-        float v, alpha, beta;
+        float v;
     };
     auto fetch = [&](size_t t, In &in) {
         const float4 *kt = (const float4 *)(k + (t * n_k_heads + kh) * kD + p * kKeys);
@@ -65,40 +82,52 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
             in.q4[i] = qt[i];
         }
         in.v = v[(t * n_v_heads + h) * kD + c0 + c];
-        in.alpha = gates[t * 2 * n_v_heads + h];
-        in.beta = gates[t * 2 * n_v_heads + n_v_heads + h];
     };
     In cur, nxt;
     if (n > 0) fetch(0, nxt);
-    for (size_t t = 0; t < n; t++) {
-        cur = nxt;
-        if (t + 1 < n) fetch(t + 1, nxt);
-        float kk[kKeys], qq[kKeys];
-#pragma unroll
-        for (int i = 0; i < kKeys / 4; i++) {
-            kk[4 * i] = cur.k4[i].x; kk[4 * i + 1] = cur.k4[i].y; kk[4 * i + 2] = cur.k4[i].z; kk[4 * i + 3] = cur.k4[i].w;
-            qq[4 * i] = cur.q4[i].x; qq[4 * i + 1] = cur.q4[i].y; qq[4 * i + 2] = cur.q4[i].z; qq[4 * i + 3] = cur.q4[i].w;
+    for (size_t r0 = 0; r0 < n; r0 += kGRun) {
+        // this run's gates: g = exp(a·softplus(alpha + dt_bias)), beta = sigmoid(beta_logit)
+        const size_t rn = n - r0 < (size_t)kGRun ? n - r0 : (size_t)kGRun;
+        __syncthreads();
+        for (size_t t = threadIdx.x; t < rn; t += kThreads) {
+            const float alpha = gs * gates[(r0 + t) * 2 * n_v_heads + h];
+            const float beta = sigmoidf_(gs * gates[(r0 + t) * 2 * n_v_heads + n_v_heads + h]);
+            gb[t] = make_float2(expf(a * softplusf_(alpha + dt)), beta);
         }
-        const float vj = cur.v;
-        const float alpha = gs * cur.alpha;
-        const float beta = sigmoidf_(gs * cur.beta);
-        const float g = expf(a * softplusf_(alpha + dt));
-        float kv = 0.0f;
+        __syncthreads();
+        for (size_t tt = 0; tt < rn; tt++) {
+            const size_t t = r0 + tt;
+            cur = nxt;
+            if (t + 1 < n) fetch(t + 1, nxt);
+            float kk[kKeys], qq[kKeys];
 #pragma unroll
-        for (int i = 0; i < kKeys; i++) {
-            s[i] *= g;
-            kv += s[i] * kk[i];
-        }
-        kv = group_sum<kParts>(kv);
-        const float u = vj - kv;
-        float o = 0.0f;
+            for (int i = 0; i < kKeys / 4; i++) {
+                kk[4 * i] = cur.k4[i].x; kk[4 * i + 1] = cur.k4[i].y; kk[4 * i + 2] = cur.k4[i].z; kk[4 * i + 3] = cur.k4[i].w;
+                qq[4 * i] = cur.q4[i].x; qq[4 * i + 1] = cur.q4[i].y; qq[4 * i + 2] = cur.q4[i].z; qq[4 * i + 3] = cur.q4[i].w;
+            }
+            const float2 g2 = gb[tt];
+            const float g = g2.x, beta = g2.y;
+            float kv0 = 0.0f, kv1 = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kKeys; i++) {
-            s[i] += kk[i] * u * beta;
-            o += s[i] * qq[i] * scale;
+            for (int i = 0; i < kKeys; i += 2) {
+                s[i] *= g;
+                s[i + 1] *= g;
+                kv0 += s[i] * kk[i];
+                kv1 += s[i + 1] * kk[i + 1];
+            }
+            const float kv = sum16(kv0 + kv1);
+            const float ub = (cur.v - kv) * beta;
+            float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kKeys; i += 2) {
+                s[i] += kk[i] * ub;
+                s[i + 1] += kk[i + 1] * ub;
+                o0 += s[i] * qq[i];
+                o1 += s[i + 1] * qq[i + 1];
+            }
+            const float o = sum16(o0 + o1) * scale;
+            if (p == 0) out[(t * n_v_heads + h) * kD + c0 + c] = o;
         }
-        o = group_sum<kParts>(o);
-        if (p == 0) out[(t * n_v_heads + h) * kD + c0 + c] = o;
     }
 
     // state slice out, through LDS
