@@ -4,7 +4,7 @@
 // X0 (each in [-128, 127]), written as three int8 rows [3][cols]; beside them,
 // per 64 activations, the four groups' scales and then their four f32 sums
 // ([cols/64][8] floats).  A device holds two such areas, so that a kernel can
-// read one and write the other.
+// read one and write the other, and four more for the tokens of a batch.
 //
 // A group of 16 is the 16 rows of one tile of a Q4_K matrix-vector product,
 // so the product that computes those rows writes their planes itself.  When
@@ -70,8 +70,10 @@ __device__ __forceinline__ void write16(const View &v, size_t i, float x) {
 }
 
 // Activations 4j..4j+3 of a group that 4 consecutive (4-aligned) lanes hold
-// four each.
-__device__ __forceinline__ void write4x4(const View &v, size_t j, float4 x) {
+// four each.  pair (the same for the whole wave): the two groups of each 32
+// take the scale of the pair, their larger max|x| (a product that sees equal
+// scales may then sum the pair in int32 before scaling).
+__device__ __forceinline__ void write4x4(const View &v, size_t j, float4 x, bool pair = false) {
     float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
     float s = (x.x + x.y) + (x.z + x.w);
 #pragma unroll
@@ -79,6 +81,7 @@ __device__ __forceinline__ void write4x4(const View &v, size_t j, float4 x) {
         m = fmaxf(m, __shfl_xor(m, k, 64));
         s += __shfl_xor(s, k, 64);
     }
+    if (pair) m = fmaxf(m, __shfl_xor(m, 4, 64));
     const float inv = m > 0.0f ? kScale / m : 0.0f;
     const float e[4] = {x.x, x.y, x.z, x.w};
     uint32_t p0 = 0, p1 = 0, p2 = 0;

@@ -137,6 +137,14 @@ struct MvExtra {
 };
 hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                               int count, int swiglu, int area, const MvExtra *extra = nullptr);
+// n tokens (rows of x, [n][cols]) on the int8 matrix cores, in launches of
+// up to four tokens that share the weight loads: the planes of each token
+// (RMS-normalized by `norm` when given, the normalized rows to xn_out when
+// that is given) in the batch areas, then outs[j] ([n][rows_j]) += or = W_j·x
+// by adds[j], or a SwiGLU pair into outs[0] as launch_mv_q4k_mfma.
+hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
+                                     int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
+                                     float *xn_out);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,

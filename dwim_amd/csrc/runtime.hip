@@ -58,7 +58,7 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
     }
     // the split matrix products' partial sums and counters
     dev->mv_tiles_cap = 4096;
-    if (hipMalloc(&dev->mv_partials, (size_t)dev->mv_tiles_cap * 4 * 32 * sizeof(float)) != hipSuccess ||
+    if (hipMalloc(&dev->mv_partials, (size_t)dev->mv_tiles_cap * 4 * 4 * 32 * sizeof(float)) != hipSuccess ||
         hipMalloc(&dev->mv_counters, (size_t)dev->mv_tiles_cap * sizeof(unsigned)) != hipSuccess ||
         hipMemset(dev->mv_counters, 0, (size_t)dev->mv_tiles_cap * sizeof(unsigned)) != hipSuccess) {
         dev->refs = 0;

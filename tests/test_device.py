@@ -236,6 +236,40 @@ def test_q4_k_swiglu_and_matmul_add_match_cpu(gpu):
             close_batch(gpu.read(out) - res, want - res, f"matmul_add {cols}x{rows} n={n}")
 
 
+def test_q4_k_small_batches_on_the_matrix_cores(gpu):
+    # 2..15 tokens run on the int8 matrix cores in launches of up to four
+    # tokens (7 = 4 + 3, 13 = 4 + 3 + 3 + 3); the 17408 columns split each
+    # tile's blocks over several workgroups
+    for rows, cols, ns in [(1100, 5120, (2, 3, 4, 5, 7, 13)), (300, 17408, (4, 6, 15)), (64, 256, (3,))]:
+        w = _k_quantized(O.Q4_K, rows)(rows, cols)
+        gw = gpu.upload(to_tensor(w))
+        for n in ns:
+            x = O.Rng(rows + n).floats(n * cols)
+            want = O.matmul(w, x)
+            out = gpu.alloc(n * rows)
+            gpu.matmul(out, gw, gpu.buffer(x))
+            got = gpu.read(out)
+            for t in range(n):
+                close(got[t * rows:(t + 1) * rows], want[t * rows:(t + 1) * rows], 1e-4)
+            # and against the one-token product of each row of x
+            one = gpu.alloc(rows)
+            gpu.matmul(one, gw, gpu.buffer(x[(n - 1) * cols:]))
+            close(got[(n - 1) * rows:], gpu.read(one), 1e-5)
+    # a SwiGLU pair (two matrices a workgroup) and an add over split rows
+    make = _k_quantized(O.Q4_K, 71)
+    gate, up = make(1100, 5120), make(1100, 5120)
+    x = O.Rng(72).floats(6 * 5120)
+    want = O.silu_mul(O.matmul(gate, x), O.matmul(up, x))
+    out, scratch = gpu.alloc(6 * 1100), gpu.alloc(6 * 1100)
+    gpu.swiglu(out, gpu.upload(to_tensor(gate)), gpu.upload(to_tensor(up)), gpu.buffer(x), scratch)
+    close(gpu.read(out), want, 1e-4)
+    w = make(300, 17408)
+    inp, res = O.Rng(73).floats(4 * 17408), O.Rng(74).floats(4 * 300)
+    out = gpu.buffer(res)
+    gpu.matmul_add(out, gpu.upload(to_tensor(w)), gpu.buffer(inp), gpu.alloc(4 * 300))
+    close(gpu.read(out), O.add(res, O.matmul(w, inp)), 1e-4)
+
+
 @pytest.mark.parametrize("fmt", [D.Q4_K, D.Q6_K, D.BF16])
 def test_synthetic_weights_are_the_host_quantizers_bits(gpu, fmt):
     rows, cols = 333, 1024
