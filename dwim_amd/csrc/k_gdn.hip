@@ -11,8 +11,10 @@
 //   * the causal conv + SiLU of the 384 channels it reads (the key head's q
 //     and k, its own v), then the l2 norms of q and k;
 //   * the delta rule over its 128×128 fp32 state, read from HBM once and
-//     written once, through LDS so that both are coalesced: thread (column c,
-//     part p) holds keys 16p..16p+15 of column c;
+//     written once, straight from registers: thread (value c, part p) holds
+//     keys 16p..16p+15 of value column c, so that the 64 lanes of a wave read
+//     and write 64 consecutive values of a key row; the sums over keys meet
+//     across the eight parts in LDS;
 //   * o = Sᵀq/√128, RMS-normalized by the head's norm weights and gated by
 //     silu(z): z_h ← silu(z_h)·rmsnorm(o), with its planes for the out
 //     product when asked.
@@ -26,7 +28,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kT = 1024;
-constexpr int kParts = 8;
+constexpr int kParts = kT / kD;  // key parts: thread tid takes value tid % kD, keys of part tid / kD
 constexpr int kKeys = kD / kParts;
 
 struct GdnArgs {
@@ -48,40 +50,19 @@ struct GdnArgs {
 
 DEV float bf16f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-// sums of NV values over the 1024 threads, every thread getting them
-template <int NV>
-DEV void block_sums(float (&v)[NV], float (*red)[kT / 64]) {
-#pragma unroll
-    for (int i = 0; i < NV; i++) v[i] = group_sum<64>(v[i]);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0)
-#pragma unroll
-        for (int i = 0; i < NV; i++) red[i][wave] = v[i];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < NV; i++) {
-        float t = 0.0f;
-        for (int w = 0; w < kT / 64; w++) t += red[i][w];
-        v[i] = t;
-    }
-}
-
 __global__ void __launch_bounds__(kT) k_gdn(const GdnArgs a) {
-    __shared__ float st[kD][kD + 1];  // the head's state, [key][value]
-    __shared__ float qs[kD], ks[kD], vs[kD], os[kD];
-    __shared__ float red[3][kT / 64];
-    __shared__ float nred[2][4];  // the q/k and o norms' wave sums
+    __shared__ float part[2][kParts][kD];  // per-part sums over keys, per value column: k·S, then q·S
+    __shared__ float qs[kD], ks[kD], vs[kD];
+    __shared__ float red[4][kT / 64];   // wave sums: gate logits, RMS partials, q and k squares
+    __shared__ float ored[2];          // the o norm's wave sums
     const int tid = threadIdx.x;
     const unsigned h = blockIdx.x, kh = h / (a.nv / a.nk);
     const unsigned ch = (2 * a.nk + a.nv) * kD;
     float *S = a.state + (size_t)h * kD * kD;
 
-    // ---- every load first: the state (16 floats a thread, coalesced), the
-    // conv inputs of 384 channels, the gate rows and x·w, the RMS partials
-    float4 sv[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) sv[i] = ((const float4 *)S)[tid + kT * i];
+    // ---- every load first: the conv inputs of 384 channels, the gate rows
+    // and x·w, the RMS partials, then the state (16 floats a thread, a wave's
+    // loads 256 contiguous bytes), which is needed last
     // conv channel of thread tid < 384: q of kh, k of kh, v of h
     const int which = tid / kD, cc = tid % kD;
     const unsigned chan = which == 0 ? kh * kD + cc : which == 1 ? (a.nk + kh) * kD + cc : (2 * a.nk + h) * kD + cc;
@@ -98,40 +79,12 @@ __global__ void __launch_bounds__(kT) k_gdn(const GdnArgs a) {
     const float ssp = a.rms.ss[g0];
     const float zc = a.z[h * kD + (tid % kD)], nwc = a.norm_w[tid % kD];
     const float dec_a = a.decay[h], dec_dt = a.decay[a.nv + h];
-
-    // ---- the state into LDS
+    const int c = tid % kD, p = tid / kD;
+    float s[kKeys];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * (tid + kT * i);  // element of [key][value]
-        st[e / kD][e % kD] = sv[i].x;
-        st[e / kD][e % kD + 1] = sv[i].y;
-        st[e / kD][e % kD + 2] = sv[i].z;
-        st[e / kD][e % kD + 3] = sv[i].w;
-    }
+    for (int i = 0; i < kKeys; i++) s[i] = S[(p * kKeys + i) * kD + c];
 
-    // ---- the gate logits and the RMS scale (one block reduction)
-    float sums[3];
-    {
-        float da = 0.0f, db = 0.0f;
-        if ((unsigned)tid < n8) {
-            const uint32_t pa[4] = {wa.x, wa.y, wa.z, wa.w}, pb[4] = {wb.x, wb.y, wb.z, wb.w};
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                da += bf16f((uint16_t)(pa[i] & 0xffffu)) * xs[2 * i] + bf16f((uint16_t)(pa[i] >> 16)) * xs[2 * i + 1];
-                db += bf16f((uint16_t)(pb[i] & 0xffffu)) * xs[2 * i] + bf16f((uint16_t)(pb[i] >> 16)) * xs[2 * i + 1];
-            }
-        }
-        sums[0] = da;
-        sums[1] = db;
-        sums[2] = (unsigned)tid < a.rms.groups ? ssp : 0.0f;
-        block_sums<3>(sums, red);
-    }
-    const float gs = 1.0f / sqrtf(sums[2] / a.rms.cols + a.rms.eps);
-    const float alpha = gs * sums[0], beta = sigmoidf_(gs * sums[1]);
-    const float g = expf(dec_a * softplusf_(alpha + dec_dt));
-
-    // ---- conv + SiLU, its state carried over, and the l2 norms of q and k
+    // ---- conv + SiLU of the 384 channels, their state carried over
     float y = 0.0f;
     if (tid < 3 * kD) {
         float acc = 0.0f;
@@ -147,70 +100,80 @@ __global__ void __launch_bounds__(kT) k_gdn(const GdnArgs a) {
             a.conv_state_out[2 * ch + chan] = cx;
         }
     }
-    {
-        float sq[2] = {which == 0 && tid < 3 * kD ? y * y : 0.0f, which == 1 ? y * y : 0.0f};
-        // waves 0-1 hold q, 2-3 hold k: two-wave sums
-        sq[0] = group_sum<64>(sq[0]);
-        sq[1] = group_sum<64>(sq[1]);
-        const int lane = tid & 63, wave = tid >> 6;
-        if (lane == 0 && wave < 4) nred[0][wave] = wave < 2 ? sq[0] : sq[1];
-        __syncthreads();
-        if (tid < kD) qs[tid] = y * (1.0f / sqrtf((nred[0][0] + nred[0][1]) + a.eps));
-        else if (tid < 2 * kD) ks[tid - kD] = y * (1.0f / sqrtf((nred[0][2] + nred[0][3]) + a.eps));
-        else if (tid < 3 * kD) vs[tid - 2 * kD] = y;
-        __syncthreads();
-    }
 
-    // ---- the delta rule: thread (column c, part p), keys 16p..16p+15
-    const int c = tid / kParts, p = tid % kParts;
-    float s[kKeys], kk[kKeys], qq[kKeys];
+    // ---- one block reduction: the gate logits, the RMS scale and the l2
+    // norms of q (waves 0-1) and k (waves 2-3)
+    float da = 0.0f, db = 0.0f;
+    if ((unsigned)tid < n8) {
+        const uint32_t pa[4] = {wa.x, wa.y, wa.z, wa.w}, pb[4] = {wb.x, wb.y, wb.z, wb.w};
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-    for (int i = 0; i < kKeys; i++) {
-        s[i] = st[p * kKeys + i][c];
-        kk[i] = ks[p * kKeys + i];
-        qq[i] = qs[p * kKeys + i];
+        for (int i = 0; i < 4; i++) {
+            da += bf16f((uint16_t)(pa[i] & 0xffffu)) * xs[2 * i] + bf16f((uint16_t)(pa[i] >> 16)) * xs[2 * i + 1];
+            db += bf16f((uint16_t)(pb[i] & 0xffffu)) * xs[2 * i] + bf16f((uint16_t)(pb[i] >> 16)) * xs[2 * i + 1];
+        }
     }
+    {
+        const float v[4] = {da, db, (unsigned)tid < a.rms.groups ? ssp : 0.0f, tid < 2 * kD ? y * y : 0.0f};
+        const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float t = group_sum<64>(v[i]);
+            if (lane == 0) red[i][wave] = t;
+        }
+    }
+    __syncthreads();
+    float sums[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        float t = 0.0f;
+        for (int w = 0; w < kT / 64; w++) t += red[i][w];
+        sums[i] = t;
+    }
+    const float gs = 1.0f / sqrtf(sums[2] / a.rms.cols + a.rms.eps);
+    const float alpha = gs * sums[0], beta = sigmoidf_(gs * sums[1]);
+    const float g = expf(dec_a * softplusf_(alpha + dec_dt));
+    if (tid < kD) qs[tid] = y * (1.0f / sqrtf((red[3][0] + red[3][1]) + a.eps));
+    else if (tid < 2 * kD) ks[tid - kD] = y * (1.0f / sqrtf((red[3][2] + red[3][3]) + a.eps));
+    else if (tid < 3 * kD) vs[tid - 2 * kD] = y;
+    __syncthreads();
+
+    // ---- the delta rule: thread (value c, part p), keys 16p..16p+15
     float kv = 0.0f;
 #pragma unroll
     for (int i = 0; i < kKeys; i++) {
         s[i] *= g;
-        kv += s[i] * kk[i];
+        kv += s[i] * ks[p * kKeys + i];
     }
-    kv = group_sum<kParts>(kv);
-    const float u = vs[c] - kv;
+    part[0][p][c] = kv;
+    __syncthreads();
+    kv = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kParts; q++) kv += part[0][q][c];
+    const float ub = (vs[c] - kv) * beta;
     const float scale = 1.0f / sqrtf((float)kD);
     float o = 0.0f;
 #pragma unroll
     for (int i = 0; i < kKeys; i++) {
-        s[i] += kk[i] * u * beta;
-        o += s[i] * qq[i] * scale;
+        s[i] += ks[p * kKeys + i] * ub;
+        o += s[i] * qs[p * kKeys + i];
     }
-    o = group_sum<kParts>(o);
-    if (p == 0) os[c] = o;
 #pragma unroll
-    for (int i = 0; i < kKeys; i++) st[p * kKeys + i][c] = s[i];
+    for (int i = 0; i < kKeys; i++) S[(p * kKeys + i) * kD + c] = s[i];
+    part[1][p][c] = o * scale;
     __syncthreads();
 
-    // ---- the state out, coalesced; the gated norm of o (threads < 128)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * (tid + kT * i);
-        float4 w;
-        w.x = st[e / kD][e % kD];
-        w.y = st[e / kD][e % kD + 1];
-        w.z = st[e / kD][e % kD + 2];
-        w.w = st[e / kD][e % kD + 3];
-        ((float4 *)S)[tid + kT * i] = w;
-    }
+    // ---- the gated norm of o (threads < 128)
+    float ov = 0.0f;
     if (tid < kD) {
-        const float ov = os[tid];
-        float ss = group_sum<64>(ov * ov);
-        if ((tid & 63) == 0) nred[1][tid >> 6] = ss;
+#pragma unroll
+        for (int q = 0; q < kParts; q++) ov += part[1][q][tid];
+        const float ss = group_sum<64>(ov * ov);
+        if ((tid & 63) == 0) ored[tid >> 6] = ss;
     }
     __syncthreads();
     if (tid < kD) {
-        const float ov = os[tid];
-        const float sc = 1.0f / sqrtf((nred[1][0] + nred[1][1]) / (float)kD + a.eps);
+        const float sc = 1.0f / sqrtf((ored[0] + ored[1]) / (float)kD + a.eps);
         const float r = zc * sigmoidf_(zc) * (ov * (sc * nwc));
         a.z[h * kD + tid] = r;
         if (a.out.q) planes::write16(a.out, h * kD + tid, r);
