@@ -5,19 +5,68 @@
 
 #define DEV __device__ __forceinline__
 
-// Sum over groups of `width` consecutive lanes (width a power of two <= 64),
-// every lane of a group getting the group's total.
+// Lane exchanges without LDS: DPP within rows of 16 lanes, and gfx950's
+// permlane swaps across them.  After a step every lane of the grown group
+// holds the same value, so each step may pair any two halves of it.
+namespace xlane {
+template <int CTRL>
+DEV float mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// {v[l], v[l ^ 16]} and {v[l], v[l ^ 32]}, in some order: their sum or max
+// is the pair's
+DEV void swap16(float v, float &a, float &b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+DEV void swap32(float v, float &a, float &b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+}  // namespace xlane
+
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64;
+// all lanes of a group active), every lane of a group getting the group's
+// total: lane pairs xor 1 and xor 2 (quad permutes), then the two quads of 8
+// (half-row mirror), the two halves of a row of 16 (row mirror), rows
+// 16 apart and 32 apart (permlane swaps).
 template <int WIDTH>
 DEV float group_sum(float v) {
-#pragma unroll
-    for (int m = WIDTH / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+    if (WIDTH >= 2) v += xlane::mov<0xb1>(v);
+    if (WIDTH >= 4) v += xlane::mov<0x4e>(v);
+    if (WIDTH >= 8) v += xlane::mov<0x141>(v);
+    if (WIDTH >= 16) v += xlane::mov<0x140>(v);
+    if (WIDTH >= 32) {
+        float a, b;
+        xlane::swap16(v, a, b);
+        v = a + b;
+    }
+    if (WIDTH >= 64) {
+        float a, b;
+        xlane::swap32(v, a, b);
+        v = a + b;
+    }
     return v;
 }
 
 template <int WIDTH>
 DEV float group_max(float v) {
-#pragma unroll
-    for (int m = WIDTH / 2; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    if (WIDTH >= 2) v = fmaxf(v, xlane::mov<0xb1>(v));
+    if (WIDTH >= 4) v = fmaxf(v, xlane::mov<0x4e>(v));
+    if (WIDTH >= 8) v = fmaxf(v, xlane::mov<0x141>(v));
+    if (WIDTH >= 16) v = fmaxf(v, xlane::mov<0x140>(v));
+    if (WIDTH >= 32) {
+        float a, b;
+        xlane::swap16(v, a, b);
+        v = fmaxf(a, b);
+    }
+    if (WIDTH >= 64) {
+        float a, b;
+        xlane::swap32(v, a, b);
+        v = fmaxf(a, b);
+    }
     return v;
 }
 

@@ -16,6 +16,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "device_util.h"
+
 namespace planes {
 
 constexpr size_t kGroup = 16;
@@ -54,12 +56,7 @@ __device__ __forceinline__ void put_stat(const View &v, size_t group, float sum,
 // Activation i = 16·group + lane of a group that 16 consecutive lanes (a
 // 16-aligned run of the wave, all active) hold one each.
 __device__ __forceinline__ void write16(const View &v, size_t i, float x) {
-    float m = fabsf(x), s = x;
-#pragma unroll
-    for (int k = 8; k > 0; k >>= 1) {
-        m = fmaxf(m, __shfl_xor(m, k, 64));
-        s += __shfl_xor(s, k, 64);
-    }
+    const float m = group_max<16>(fabsf(x)), s = group_sum<16>(x);
     const float inv = m > 0.0f ? kScale / m : 0.0f;
     int d0, d1, d2;
     digits(x, inv, d0, d1, d2);
@@ -74,14 +71,9 @@ __device__ __forceinline__ void write16(const View &v, size_t i, float x) {
 // take the scale of the pair, their larger max|x| (a product that sees equal
 // scales may then sum the pair in int32 before scaling).
 __device__ __forceinline__ void write4x4(const View &v, size_t j, float4 x, bool pair = false) {
-    float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
-    float s = (x.x + x.y) + (x.z + x.w);
-#pragma unroll
-    for (int k = 2; k > 0; k >>= 1) {
-        m = fmaxf(m, __shfl_xor(m, k, 64));
-        s += __shfl_xor(s, k, 64);
-    }
-    if (pair) m = fmaxf(m, __shfl_xor(m, 4, 64));
+    float m = group_max<4>(fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+    const float s = group_sum<4>((x.x + x.y) + (x.z + x.w));
+    if (pair) m = group_max<8>(m);
     const float inv = m > 0.0f ? kScale / m : 0.0f;
     const float e[4] = {x.x, x.y, x.z, x.w};
     uint32_t p0 = 0, p1 = 0, p2 = 0;
