@@ -36,6 +36,7 @@ struct Shape {
 // head for all G query heads.  Values: wave w takes elements 32w..32w+31 (one
 // Q8 block: one scale per position), lane l elements 32w + 4(l % 8)..+3 of
 // positions l/8 + 8i; the 8 position groups meet by shuffles.
+template <int G>
 __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ partials, const float *__restrict__ q,
                                                             const int8_t *__restrict__ kq,
                                                             const uint16_t *__restrict__ ks,
@@ -47,7 +48,7 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
     __shared__ float p_s[kMaxG * kPos];
     __shared__ float stat_s[kMaxG * 2];
     const size_t chunk = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
-    const int D = (int)sh.head_dim, G = (int)(sh.n_heads / sh.n_kv_heads);
+    const int D = (int)sh.head_dim;
     const size_t kv_dim = sh.n_kv_heads * sh.head_dim;
     const size_t len = sh.pos + t + 1;  // the token attends up to its own position
     const size_t p0 = chunk * kPos;
@@ -114,6 +115,7 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
             kv[i] = (float)(int8_t)((wa >> (8 * (i & 3))) & 0xff);
             kv[16 + i] = (float)(int8_t)((wc >> (8 * (i & 3))) & 0xff);
         }
+#pragma unroll
         for (int g = 0; g < G; g++) {
             float sc = 0.0f;
             if (klive) {
@@ -140,9 +142,10 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
     }
     __syncthreads();
     if (vlive) {
-        float acc[kMaxG][4];
+        float acc[G][4];
 #pragma unroll
-        for (int g = 0; g < kMaxG; g++)
+        for (int g = 0; g < G; g++)
+#pragma unroll
             for (int e = 0; e < 4; e++) acc[g][e] = 0.0f;
 #pragma unroll
         for (int i = 0; i < kPos / 8; i++) {
@@ -152,29 +155,41 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
             const float v0 = (float)(int8_t)(w & 0xff) * vsc, v1 = (float)(int8_t)((w >> 8) & 0xff) * vsc,
                         v2 = (float)(int8_t)((w >> 16) & 0xff) * vsc, v3 = (float)(int8_t)(w >> 24) * vsc;
 #pragma unroll
-            for (int g = 0; g < kMaxG; g++)
-                if (g < G) {
-                    const float pr = vp < cnt ? p_s[g * kPos + vp] : 0.0f;
-                    acc[g][0] += pr * v0;
-                    acc[g][1] += pr * v1;
-                    acc[g][2] += pr * v2;
-                    acc[g][3] += pr * v3;
-                }
+            for (int g = 0; g < G; g++) {
+                const float pr = vp < cnt ? p_s[g * kPos + vp] : 0.0f;
+                acc[g][0] += pr * v0;
+                acc[g][1] += pr * v1;
+                acc[g][2] += pr * v2;
+                acc[g][3] += pr * v3;
+            }
         }
+        // the 8 position groups (lanes 8 apart) meet: lanes l, l ^ 8 by a
+        // row rotation, l ^ 16 and l ^ 32 by permlane swaps
 #pragma unroll
-        for (int g = 0; g < kMaxG; g++)
-            if (g < G)
+        for (int g = 0; g < G; g++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float v = acc[g][e];
-                    v += __shfl_xor(v, 8, 64);
-                    v += __shfl_xor(v, 16, 64);
-                    v += __shfl_xor(v, 32, 64);
-                    acc[g][e] = v;
-                }
-        if (lane < 8)  // (a partial row is (D + 2) floats: 8-byte alignment only)
-            for (int g = 0; g < G; g++)
-                for (int e = 0; e < 4; e++) part[g * part_stride + 32 * wave + 4 * lane + e] = acc[g][e];
+            for (int e = 0; e < 4; e++) {
+                float v = acc[g][e];
+                v += xlane::mov<0x128>(v);
+                float x, y;
+                xlane::swap16(v, x, y);
+                v = x + y;
+                xlane::swap32(v, x, y);
+                acc[g][e] = x + y;
+            }
+        // position group pg stores head pg's four values (a partial row is
+        // (D + 2) floats: 8-byte alignment only)
+        const int pg = lane >> 3;
+        float o[4] = {acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+#pragma unroll
+        for (int g = 1; g < G; g++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = pg == g ? acc[g][e] : o[e];
+        if (pg < G) {
+            float2 *dst = (float2 *)(part + pg * part_stride + 32 * wave + 4 * (lane & 7));
+            dst[0] = make_float2(o[0], o[1]);
+            dst[1] = make_float2(o[2], o[3]);
+        }
     }
     if (threadIdx.x < (unsigned)G) {
         part[threadIdx.x * part_stride + D] = stat_s[2 * threadIdx.x];
@@ -523,7 +538,13 @@ hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, con
     }
     Shape sh{n, pos, n_heads, head_dim, n_kv_heads, ch, chunks};
     dim3 g1((unsigned)chunks, (unsigned)n_kv_heads, (unsigned)n);
-    k_attn_partial<<<g1, kPThreads, 0, dev->stream>>>(dev->partials, q, k->q, k->s, v->q, v->s, sh);
+    switch (n_heads / n_kv_heads) {
+#define DWIM_PARTIAL(G) \
+    case G: k_attn_partial<G><<<g1, kPThreads, 0, dev->stream>>>(dev->partials, q, k->q, k->s, v->q, v->s, sh); break;
+        DWIM_PARTIAL(1) DWIM_PARTIAL(2) DWIM_PARTIAL(3) DWIM_PARTIAL(4) DWIM_PARTIAL(5) DWIM_PARTIAL(6)
+        DWIM_PARTIAL(7) DWIM_PARTIAL(8)
+#undef DWIM_PARTIAL
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     dim3 g2((unsigned)n_heads, (unsigned)n);
