@@ -200,68 +200,92 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
 // out[t][h] = Σ_c e^(m_c − M) o_c / Σ_c e^(m_c − M) l_c, times sigmoid(gate)
 // when a gate is given (gpu/cpu.rs:244-248); with one token, its planes too.
 // Thread group cg = thread / (D/4) takes every CG-th chunk, four elements a
-// thread; the groups meet in LDS.
+// thread, merging them as it goes (a running max, the sums rescaled when it
+// grows), four chunks' loads at a time; the groups meet in LDS.
 __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ out, const float *__restrict__ partials,
                                                            Shape sh, const float *__restrict__ gate, planes::View pv) {
-    __shared__ float red[16];
+    __shared__ float gm[kThreads / 8], gl[kThreads / 8];  // per chunk group (head_dim >= 32)
     __shared__ float4 part_s[kThreads];
     const size_t h = blockIdx.x, t = blockIdx.y;
     const int D = (int)sh.head_dim, TPR = D / 4, CG = kThreads / TPR;
     const int dg = threadIdx.x % TPR, cg = threadIdx.x / TPR;
     const size_t stride = (size_t)(D + 2);
     const float *part = partials + (t * sh.n_heads + h) * sh.chunks * stride;
-    float M = -INFINITY;
-    for (size_t c = threadIdx.x; c < sh.chunks; c += kThreads) M = fmaxf(M, part[c * stride + D]);
-    M = group_max<64>(M);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) red[wave] = M;
-    __syncthreads();
-    M = red[0];
-    for (int w = 1; w < kThreads / 64; w++) M = fmaxf(M, red[w]);
-    float L = 0.0f;
+    float M = -INFINITY, L = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 4
-    for (size_t c = cg; c < sh.chunks; c += CG) {
-        const float m = part[c * stride + D];
-        if (m == -INFINITY) continue;
-        const float e = expf(m - M);
-        L += e * part[c * stride + D + 1];
-        const float *o = part + c * stride + 4 * dg;  // (D + 2)·4 bytes apart: 8-byte aligned only
-        acc.x += e * o[0];
-        acc.y += e * o[1];
-        acc.z += e * o[2];
-        acc.w += e * o[3];
+    constexpr int kU = 4;
+    for (size_t c0 = cg; c0 < sh.chunks; c0 += (size_t)kU * CG) {
+        float m[kU], l[kU];
+        float2 oa[kU], ob[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const size_t c = c0 + (size_t)u * CG;
+            const size_t cc = c < sh.chunks ? c : c0;  // past the end: a chunk already counted, dropped below
+            const float *row = part + cc * stride;
+            m[u] = c < sh.chunks ? row[D] : -INFINITY;
+            l[u] = row[D + 1];
+            oa[u] = *(const float2 *)(row + 4 * dg);  // (D + 2)·4 bytes apart: 8-byte aligned only
+            ob[u] = *(const float2 *)(row + 4 * dg + 2);
+        }
+        // the batch's max first, then one rescale and independent terms
+        float Mb = M;
+#pragma unroll
+        for (int u = 0; u < kU; u++) Mb = fmaxf(Mb, m[u]);
+        if (Mb == -INFINITY) continue;  // nothing yet
+        const float ra = expf(M - Mb);  // (M = −∞: 0)
+        L *= ra;
+        acc.x *= ra;
+        acc.y *= ra;
+        acc.z *= ra;
+        acc.w *= ra;
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            // an empty chunk, or none: no term (its row holds only m and l)
+            const bool live = m[u] != -INFINITY;
+            const float rb = expf(m[u] - Mb);
+            if (!live) oa[u] = ob[u] = make_float2(0.0f, 0.0f);
+            L += live ? l[u] * rb : 0.0f;
+            acc.x += oa[u].x * rb;
+            acc.y += oa[u].y * rb;
+            acc.z += ob[u].x * rb;
+            acc.w += ob[u].y * rb;
+        }
+        M = Mb;
     }
-    // L: every thread of a chunk group added the same terms; take group 0's
-    __syncthreads();
-    if (dg == 0) red[cg] = L;
+    // the groups meet: every thread of a group holds the same M and L
+    if (dg == 0) {
+        gm[cg] = M;
+        gl[cg] = L;
+    }
     part_s[threadIdx.x] = acc;
     __syncthreads();
-    L = 0.0f;
-    for (int k = 0; k < CG; k++) L += red[k];
-    if (cg == 0) {
-        float4 sum = acc;
-        for (int k = 1; k < CG; k++) {
-            const float4 o = part_s[k * TPR + dg];
-            sum.x += o.x;
-            sum.y += o.y;
-            sum.z += o.z;
-            sum.w += o.w;
-        }
-        part_s[dg] = sum;
+    if (cg != 0) return;
+    float Mt = -INFINITY;
+    for (int k = 0; k < CG; k++) Mt = fmaxf(Mt, gm[k]);
+    float Lt = 0.0f;
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k = 0; k < CG; k++) {
+        if (gm[k] == -INFINITY) continue;
+        const float r = expf(gm[k] - Mt);
+        const float4 o = part_s[k * TPR + dg];
+        Lt += gl[k] * r;
+        sum.x += o.x * r;
+        sum.y += o.y * r;
+        sum.z += o.z * r;
+        sum.w += o.w * r;
     }
-    __syncthreads();
-    for (int d = threadIdx.x; d < D; d += kThreads) {
-        const float4 sum = part_s[d / 4];
-        const float a = (d & 3) == 0 ? sum.x : (d & 3) == 1 ? sum.y : (d & 3) == 2 ? sum.z : sum.w;
-        const size_t i = (t * sh.n_heads + h) * D + d;
-        float o = a / L;
-        if (gate) o *= sigmoidf_(gate[i]);
-        out[i] = o;
-        if (pv.q) planes::write16(pv, i, o);  // D is whole groups of 16 lanes
+    const size_t i = (t * sh.n_heads + h) * D + 4 * dg;
+    float4 o = make_float4(sum.x / Lt, sum.y / Lt, sum.z / Lt, sum.w / Lt);
+    if (gate) {
+        const float4 gv = *(const float4 *)(gate + i);
+        o.x *= sigmoidf_(gv.x);
+        o.y *= sigmoidf_(gv.y);
+        o.z *= sigmoidf_(gv.z);
+        o.w *= sigmoidf_(gv.w);
     }
+    *(float4 *)(out + i) = o;
+    if (pv.q) planes::write4x4(pv, i / 4, o);  // a group of 16 is 4 lanes
 }
-
 
 // ---------------------------------------------------------------- prefill
 //
