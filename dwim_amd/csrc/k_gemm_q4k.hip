@@ -30,6 +30,7 @@
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef unsigned u4v __attribute__((ext_vector_type(4)));
 
@@ -138,15 +139,26 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         const int ar = lt;
         const unsigned wtile = (row0 + ar) / 16;
         const bool wlive = wtile < wtiles;
-        // activations: token bt, part bq (hi, lo), 64 halves
+        typedef const __attribute__((address_space(1))) u4v *gq;
+        // activations: 16-byte chunk xc of the group's 64 halves of tokens
+        // xt + 32k (k = 0..3), hi and lo parts: eight lanes read a token's
+        // 128 bytes, so that a wave's load touches eight cache lines
+        const int xc = lt & 7, xt = lt >> 3;
+        bool xlv[4];
+        gq xsrc[4];
+        // sub-block sums: token bt, 16 bytes bq
         const int bt = lt >> 1, bq = lt & 1;
         const bool xlive = tok0 + bt < a.n;
-        // sub-block sums: token bt, 16 bytes bq
-        typedef const __attribute__((address_space(1))) u4v *gq;
         const uint8_t *wsrc = a.w + (size_t)(wlive ? wtile : 0) * nb * q4kt::kUnit;
         const gq qsrc = (gq)(wsrc + q4kt::qs_off(0, (row0 + ar) % 16));
         const gq hsrc = (gq)(wsrc + q4kt::meta_off((row0 + ar) % 16));
-        const gq xs0 = (gq)((bq ? a.xl : a.xh) + (size_t)(tok0 + (xlive ? bt : 0)) * a.cols);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const unsigned t = tok0 + xt + 32 * k;
+            xlv[k] = t < a.n;
+            xsrc[k] = (gq)(a.xh + (size_t)(xlv[k] ? t : tok0) * a.cols + 8 * xc);
+        }
+        const size_t lo_off = (size_t)(a.xl - a.xh) / 8;  // the lo parts, in 16-byte chunks
         const gq ms0 = (gq)(a.xm + (size_t)(tok0 + (xlive ? bt : 0)) * nb * 16 + 8 * bq);
         const uint4 z4 = make_uint4(0, 0, 0, 0);
         // step s: block s / 4 (unit b·2304), group s % 4 (512 bytes); x at
@@ -162,8 +174,8 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
             L.hdr = wlive ? h : z4;  // zero: d = dmin = 0
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                const uint4 v = __builtin_bit_cast(uint4, xs0[s * (kStep / 8) + k]);
-                L.x[k] = xlive ? v : z4;
+                const uint4 v = __builtin_bit_cast(uint4, xsrc[k & 3][s * (kStep / 8) + (k >= 4 ? lo_off : 0)]);
+                L.x[k] = xlv[k & 3] ? v : z4;
             }
             const uint4 m = __builtin_bit_cast(uint4, ms0[b * 2]);
             L.m = xlive ? m : z4;
@@ -206,9 +218,11 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
                 row[swz(ar, 4 + 2 * hq)] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
                 row[swz(ar, 5 + 2 * hq)] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
             }
-            uint4 *xr = (bq ? Bl : Bh) + (buf * kToks + bt) * 8;
 #pragma unroll
-            for (int k = 0; k < 8; k++) xr[swz(bt, k)] = L.x[k];
+            for (int k = 0; k < 8; k++) {
+                const int t = xt + 32 * (k & 3);
+                (k >= 4 ? Bl : Bh)[(buf * kToks + t) * 8 + swz(t, xc)] = L.x[k];
+            }
             if (g == 0) {
                 // the block's min operands −dmin·m_sb (hi, lo), d (1 when d
                 // is 0) and 1/d, and the tokens' sub-block sums
@@ -233,94 +247,129 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
                 Xm[(bb * kToks + bt) * 2 + bq] = L.m;
             }
         };
-        StepLoad nxt;
-        fetch(0, nxt);
-        stage(0, nxt);
-        fetch(steps > 1 ? 1 : 0, nxt);
+        // two steps' loads in flight: step s + 1 is staged from registers
+        // loaded two steps earlier (past the last step, copies of it that
+        // nothing reads); one barrier a step, as the matrix waves
+        StepLoad L0, L1;
+        auto cl = [&](unsigned s) { return s < steps ? s : steps - 1; };
+        fetch(0, L0);
+        fetch(cl(1), L1);
+        stage(0, L0);
+        fetch(cl(2), L0);
         __syncthreads();
-        for (unsigned s = 0; s < steps; s++) {
-            // step s + 1 into the idle buffer (after the last step a copy of
-            // it, which nothing reads), step s + 2 into registers
-            stage(s + 1, nxt);
-            fetch(s + 2 < steps ? s + 2 : steps - 1, nxt);
+        for (unsigned s = 0; s < steps; s += 2) {
+            stage(s + 1, L1);
+            fetch(cl(s + 3), L1);
             __syncthreads();
+            if (s + 1 < steps) {
+                stage(s + 2, L0);
+                fetch(cl(s + 4), L0);
+                __syncthreads();
+            }
         }
         return;
     }
 
     // ---------------- matrix waves: wave (wr, wc) computes rows 128·wr..,
-    // tokens 64·wc.., as 8 × 4 tiles of 16 × 16.  acc holds the sums in
-    // units of the current block's d: 1/d_b at the block's start, its 16
-    // products of exact f16 integers accumulate, then times d_b and its min
-    // term (negated) added at its end.
+    // tokens 64·wc.., as 4 × 2 tiles of 32 × 32 (v_mfma_f32_32x32x16_f16:
+    // lane l holds A's row l % 32, B's column l % 32, at k 8(l / 32)..+7 of
+    // a 16-wide k slice; C's column l % 32, rows 8g + 4(l / 32) + e).  A
+    // step's four k slices are software-pipelined: slice k + 1's fragments are
+    // read while slice k's MFMAs run.  acc holds the sums in units of the
+    // current block's d: 1/d_b at the block's start, its products of exact
+    // f16 integers accumulate, then times d_b and its min term (negated)
+    // added at its end.
     const int wr = wave >> 1, wc = wave & 1;
-    const int r16 = lane & 15, kg = lane >> 4;
-    float4v acc[8][4];
+    const int r32 = lane & 31, kh = lane >> 5;
+    float16v acc[4][2];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 2; j++) acc[i][j] = float16v{};
     __syncthreads();
+    struct Frags {
+        half8 a[4], bh[2], bl[2];
+    };
+    // a lane's LDS rows (A: rows 128wr + 32i + l % 32; B: tokens 64wc + 32j
+    // + l % 32) share the swizzle (l % 32 / 2) % 8, so per k slice one
+    // pointer each, the tiles, buffers and hi/lo at constant offsets
+    const int sw = (r32 >> 1) & 7;
+    const uint4 *pa[4], *pb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const int c = (2 * ks + kh) ^ sw;
+        pa[ks] = A + (wr * 128 + r32) * 8 + c;
+        pb[ks] = Bh + (wc * 64 + r32) * 8 + c;
+    }
+    auto read = [&](unsigned buf, int ks, Frags &f) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            f.bh[j] = __builtin_bit_cast(half8, pb[ks][(buf * kToks + j * 32) * 8]);
+            f.bl[j] = __builtin_bit_cast(half8, pb[ks][(buf * kToks + j * 32) * 8 + 2 * kToks * 8]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) f.a[i] = __builtin_bit_cast(half8, pa[ks][(buf * kRows + i * 32) * 8]);
+    };
+    auto mma = [&](const Frags &f) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.bh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.bl[j], acc[i][j], 0, 0, 0);
+            }
+    };
+    // per-row factors of this lane's rows: tile i, rows 8g + 4kh + e
+    auto scale_rows = [&](const float *v) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 d = *(const float4 *)&v[wr * 128 + i * 32 + 8 * g + 4 * kh];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    acc[i][j][4 * g] *= d.x;
+                    acc[i][j][4 * g + 1] *= d.y;
+                    acc[i][j][4 * g + 2] *= d.z;
+                    acc[i][j][4 * g + 3] *= d.w;
+                }
+            }
+    };
+    Frags f0, f1;
     auto step = [&](unsigned s, int g) {
         const unsigned buf = s % 2, bb = (s / 4) % 2;
-        if (g == 0 && s > 0) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 v = *(const float4 *)&Di[bb * kRows + wr * 128 + i * 16 + 4 * kg];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    acc[i][j][0] *= v.x;
-                    acc[i][j][1] *= v.y;
-                    acc[i][j][2] *= v.z;
-                    acc[i][j][3] *= v.w;
-                }
-            }
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            // every fragment of the slab is read before its 64 MFMAs
-            const int c = 4 * ks + kg;
-            half8 fh[4], fl[4], fa[8];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int t = wc * 64 + j * 16 + r16;
-                fh[j] = __builtin_bit_cast(half8, Bh[(buf * kToks + t) * 8 + swz(t, c)]);
-                fl[j] = __builtin_bit_cast(half8, Bl[(buf * kToks + t) * 8 + swz(t, c)]);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int r = wr * 128 + i * 16 + r16;
-                fa[i] = __builtin_bit_cast(half8, A[(buf * kRows + r) * 8 + swz(r, c)]);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fh[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fl[j], acc[i][j], 0, 0, 0);
-                }
-        }
+        read(buf, 0, f0);
+        if (g == 0 && s > 0) scale_rows(Di + bb * kRows);
+        read(buf, 1, f1);
+        mma(f0);
+        read(buf, 2, f0);
+        mma(f1);
+        read(buf, 3, f1);
+        mma(f0);
+        mma(f1);
         if (g == 3) {
-            // the block ends: times d, plus its min term [−hi, −hi, −lo, 0]·[X_hi, X_lo, X_hi, 0]
+            // the block ends: times d, plus its min term: [−hi, −hi]·[X_hi, X_lo]
+            // and [−lo, 0]·[X_hi, 0] over the 8 sub-blocks of each k half
+            scale_rows(Dd + bb * kRows);
             const half8 zero = half8{0, 0, 0, 0, 0, 0, 0, 0};
-            half8 mx[4];
+            half8 x1[2], x2[2];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int t = wc * 64 + j * 16 + r16;
-                mx[j] = kg == 3 ? zero : __builtin_bit_cast(half8, Xm[(bb * kToks + t) * 2 + (kg == 1)]);
+            for (int j = 0; j < 2; j++) {
+                const int t = wc * 64 + j * 32 + r32;
+                const half8 xh = __builtin_bit_cast(half8, Xm[(bb * kToks + t) * 2]);
+                const half8 xl = __builtin_bit_cast(half8, Xm[(bb * kToks + t) * 2 + 1]);
+                x1[j] = kh == 0 ? xh : xl;
+                x2[j] = kh == 0 ? xh : zero;
             }
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int r = wr * 128 + i * 16 + r16;
-                const half8 ma = kg == 3 ? zero : __builtin_bit_cast(half8, Am[(bb * kRows + r) * 2 + (kg == 2)]);
-                const float4 v = *(const float4 *)&Dd[bb * kRows + wr * 128 + i * 16 + 4 * kg];
+            for (int i = 0; i < 4; i++) {
+                const int r = wr * 128 + i * 32 + r32;
+                const half8 mh = __builtin_bit_cast(half8, Am[(bb * kRows + r) * 2]);
+                const half8 ml = kh == 0 ? __builtin_bit_cast(half8, Am[(bb * kRows + r) * 2 + 1]) : zero;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    acc[i][j][0] *= v.x;
-                    acc[i][j][1] *= v.y;
-                    acc[i][j][2] *= v.z;
-                    acc[i][j][3] *= v.w;
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ma, mx[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 2; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(mh, x1[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ml, x2[j], acc[i][j], 0, 0, 0);
                 }
             }
         }
@@ -332,19 +381,21 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         step(4 * b + 2, 2);
         step(4 * b + 3, 3);
     }
-    // C tile (i, j): lane holds rows 16i + 4(lane/16) + e of token 16j + lane%16
+    // C tile (i, j): lane holds rows 32i + 8g + 4kh + e of token 32j + l % 32
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const unsigned t = tok0 + wc * 64 + j * 16 + r16;
+    for (int j = 0; j < 2; j++) {
+        const unsigned t = tok0 + wc * 64 + j * 32 + r32;
         if (t >= a.n) continue;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const unsigned r = row0 + wr * 128 + i * 16 + 4 * kg;
-            float *o = a.out + (size_t)t * a.rows + r;
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (r + e < a.rows) o[e] = a.add ? o[e] + acc[i][j][e] : acc[i][j][e];
-        }
+            for (int g = 0; g < 4; g++) {
+                const unsigned r = row0 + wr * 128 + i * 32 + 8 * g + 4 * kh;
+                float *o = a.out + (size_t)t * a.rows + r;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (r + e < a.rows) o[e] = a.add ? o[e] + acc[i][j][4 * g + e] : acc[i][j][4 * g + e];
+            }
     }
 }
 
