@@ -75,13 +75,21 @@ __global__ void k_split(const float *__restrict__ x, _Float16 *__restrict__ xh, 
     m[8 + j] = (_Float16)(s - (float)sh);
 }
 
+// what a product does with its result r and the output's old value o
+// (gpu/mod.rs:259 the add, gpu/cpu.rs:238-242 the SwiGLU's silu(gate)·up)
+DEV float gemm_out(int mode, float o, float r) {
+    return mode == kGemmAdd ? o + r : mode == kGemmSiluGate ? o * sigmoidf_(o) * r : r;
+}
+
 struct GemmArgs {
     const uint8_t *w;
     unsigned rows, cols, n;
     unsigned rtiles, ttiles, grid;  // row tiles, token tiles, workgroups launched (a multiple of 8)
+    unsigned parts;                 // workgroups a tile (k split): > 1, partial results to part_out
     const _Float16 *xh, *xl, *xm;
     float *out;
-    int add;
+    float *part_out;                // [parts][n][rows]
+    int mode;                       // GemmMode
 };
 
 // the physical 16-byte chunk of logical chunk c (0..7) in LDS row r
@@ -127,10 +135,14 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // XCD-major numbering: workgroup bx runs on XCD bx % 8
     const unsigned per = a.grid / 8, lin = (blockIdx.x % 8) * per + blockIdx.x / 8;
-    if (lin >= a.rtiles * a.ttiles) return;
-    const unsigned tt = lin / a.rtiles, rt = lin % a.rtiles;
+    const unsigned tiles = a.rtiles * a.ttiles;
+    if (lin >= tiles * a.parts) return;
+    const unsigned part = lin / tiles, tile = lin % tiles;
+    const unsigned tt = tile / a.rtiles, rt = tile % a.rtiles;
     const unsigned row0 = rt * kRows, tok0 = tt * kToks;
-    const unsigned nb = a.cols / 256, steps = 4 * nb, wtiles = (a.rows + 15) / 16;
+    // this part's blocks [b0, b0 + nb) of the row's nbt
+    const unsigned nbt = a.cols / 256, b0 = part * nbt / a.parts, nb = (part + 1) * nbt / a.parts - b0;
+    const unsigned steps = 4 * nb, wtiles = (a.rows + 15) / 16;
 
     if (wave >= 4) {
         // ---------------- loader waves: 256 threads
@@ -149,17 +161,17 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         // sub-block sums: token bt, 16 bytes bq
         const int bt = lt >> 1, bq = lt & 1;
         const bool xlive = tok0 + bt < a.n;
-        const uint8_t *wsrc = a.w + (size_t)(wlive ? wtile : 0) * nb * q4kt::kUnit;
+        const uint8_t *wsrc = a.w + ((size_t)(wlive ? wtile : 0) * nbt + b0) * q4kt::kUnit;
         const gq qsrc = (gq)(wsrc + q4kt::qs_off(0, (row0 + ar) % 16));
         const gq hsrc = (gq)(wsrc + q4kt::meta_off((row0 + ar) % 16));
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const unsigned t = tok0 + xt + 32 * k;
             xlv[k] = t < a.n;
-            xsrc[k] = (gq)(a.xh + (size_t)(xlv[k] ? t : tok0) * a.cols + 8 * xc);
+            xsrc[k] = (gq)(a.xh + (size_t)(xlv[k] ? t : tok0) * a.cols + 256 * b0 + 8 * xc);
         }
         const size_t lo_off = (size_t)(a.xl - a.xh) / 8;  // the lo parts, in 16-byte chunks
-        const gq ms0 = (gq)(a.xm + (size_t)(tok0 + (xlive ? bt : 0)) * nb * 16 + 8 * bq);
+        const gq ms0 = (gq)(a.xm + ((size_t)(tok0 + (xlive ? bt : 0)) * nbt + b0) * 16 + 8 * bq);
         const uint4 z4 = make_uint4(0, 0, 0, 0);
         // step s: block s / 4 (unit b·2304), group s % 4 (512 bytes); x at
         // s·64 halves; sums at b·16 halves
@@ -382,6 +394,9 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         step(4 * b + 3, 3);
     }
     // C tile (i, j): lane holds rows 32i + 8g + 4kh + e of token 32j + l % 32
+    // (a part of a k-split product: its own slice of part_out, plainly)
+    float *const dst = a.parts > 1 ? a.part_out + (size_t)part * a.n * a.rows : a.out;
+    const int mode = a.parts > 1 ? kGemmStore : a.mode;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const unsigned t = tok0 + wc * 64 + j * 32 + r32;
@@ -391,12 +406,46 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const unsigned r = row0 + wr * 128 + i * 32 + 8 * g + 4 * kh;
-                float *o = a.out + (size_t)t * a.rows + r;
+                float *o = dst + (size_t)t * a.rows + r;
+                if (a.rows % 4 == 0 && r + 3 < a.rows) {
+                    // four rows of the token: one 16-byte access
+                    float4 v = mode == kGemmStore ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : *(const float4 *)o;
+                    v.x = gemm_out(mode, v.x, acc[i][j][4 * g]);
+                    v.y = gemm_out(mode, v.y, acc[i][j][4 * g + 1]);
+                    v.z = gemm_out(mode, v.z, acc[i][j][4 * g + 2]);
+                    v.w = gemm_out(mode, v.w, acc[i][j][4 * g + 3]);
+                    *(float4 *)o = v;
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (r + e < a.rows) o[e] = a.add ? o[e] + acc[i][j][4 * g + e] : acc[i][j][4 * g + e];
+                    for (int e = 0; e < 4; e++)
+                        if (r + e < a.rows) o[e] = gemm_out(mode, o[e], acc[i][j][4 * g + e]);
+                }
             }
     }
+}
+
+// out = Σ_p parts[p] by the mode, the parts in order (the same bits every run)
+__global__ void k_gemm_reduce(float *__restrict__ out, const float *__restrict__ parts, size_t count, unsigned np,
+                              int mode) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    float v = parts[i];
+    for (unsigned p = 1; p < np; p++) v += parts[p * count + i];
+    out[i] = gemm_out(mode, mode == kGemmStore ? 0.0f : out[i], v);
+}
+
+// Parts a tile: a workgroup fills a CU (its LDS), so a product of W tiles
+// runs in about W / 256 rounds.  Measured on MI355X at 2048 tokens, splitting
+// the blocks of a row pays when under half the CUs would work (W ≤ 128), and
+// when a second round would be short but its tiles long (256 < W ≤ 384, at
+// least 48 blocks a row: the 17408-column down product, 10% faster); the
+// partial results cost P·n·rows floats of traffic more.
+unsigned gemm_parts(unsigned tiles, unsigned nb) {
+    unsigned p = 1;
+    if (tiles <= 128) p = 256 / tiles < 4 ? 256 / tiles : 4;
+    else if (tiles > 256 && tiles <= 384 && nb >= 48) p = 4;
+    while (p > 1 && nb / p < 4) p--;
+    return p;
 }
 
 constexpr size_t kLds = (size_t)16 * (2 * kRows * 8 + 4 * kToks * 8 + 2 * kRows * 2 + 2 * kToks * 2) + 2 * 4 * 2 * kRows;
@@ -405,9 +454,9 @@ constexpr size_t kLds = (size_t)16 * (2 * kRows * 8 + 4 * kToks * 8 + 2 * kRows 
 
 size_t gemm_split_bytes(size_t n, size_t cols) { return 2 * n * cols * sizeof(_Float16) + n * (cols / 256) * 32; }
 
-hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
-    if (w->fmt != DWIM_Q4_K || w->cols % 256 || w->rows >= (1u << 31) || n >= (1u << 31)) return hipErrorInvalidValue;
-    const size_t need = gemm_split_bytes(n, w->cols);
+hipError_t gemm_prepare(dwim_dev *dev, const float *x, size_t n, size_t cols) {
+    if (cols % 256 || n >= (1u << 31)) return hipErrorInvalidValue;
+    const size_t need = gemm_split_bytes(n, cols);
     if (dev->split_cap < need) {
         if (dev->split) hipFree(dev->split);
         dev->split = nullptr;
@@ -416,17 +465,25 @@ hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, cons
         if (e != hipSuccess) return e;
         dev->split_cap = need;
     }
-    _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * w->cols, *xm = xl + n * w->cols;
-    const size_t subs = n * (w->cols / 32);
-    k_split<<<(unsigned)((subs + 255) / 256), 256, 0, dev->stream>>>(x, xh, xl, xm, n, w->cols);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * cols, *xm = xl + n * cols;
+    const size_t subs = n * (cols / 32);
+    k_split<<<(unsigned)((subs + 255) / 256), 256, 0, dev->stream>>>(x, xh, xl, xm, n, cols);
+    dev->split_n = n;
+    dev->split_cols = cols;
+    return hipGetLastError();
+}
+
+hipError_t gemm_run(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, int mode) {
+    if (w->fmt != DWIM_Q4_K || w->rows >= (1u << 31) || dev->split_n != n || dev->split_cols != w->cols)
+        return hipErrorInvalidValue;
+    hipError_t e;
     static bool raised = false;
     if (!raised) {
         e = hipFuncSetAttribute((const void *)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
         if (e != hipSuccess) return e;
         raised = true;
     }
+    _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * w->cols, *xm = xl + n * w->cols;
     GemmArgs a{};
     a.w = (const uint8_t *)w->q;
     a.rows = (unsigned)w->rows;
@@ -434,12 +491,34 @@ hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, cons
     a.n = (unsigned)n;
     a.rtiles = (unsigned)((w->rows + kRows - 1) / kRows);
     a.ttiles = (unsigned)((n + kToks - 1) / kToks);
-    a.grid = (a.rtiles * a.ttiles + 7) / 8 * 8;
+    a.parts = gemm_parts(a.rtiles * a.ttiles, (unsigned)(w->cols / 256));
+    if (a.parts > 1) {
+        const size_t need_parts = (size_t)a.parts * n * w->rows;
+        if (dev->gemm_parts_cap < need_parts) {
+            if (dev->gemm_parts) hipFree(dev->gemm_parts);
+            dev->gemm_parts = nullptr;
+            dev->gemm_parts_cap = 0;
+            e = hipMalloc(&dev->gemm_parts, need_parts * sizeof(float));
+            if (e != hipSuccess) return e;
+            dev->gemm_parts_cap = need_parts;
+        }
+        a.part_out = dev->gemm_parts;
+    }
+    a.grid = (a.rtiles * a.ttiles * a.parts + 7) / 8 * 8;
     a.xh = xh;
     a.xl = xl;
     a.xm = xm;
     a.out = out;
-    a.add = add;
+    a.mode = mode;
     k_gemm_q4k<<<a.grid, kThreads, kLds, dev->stream>>>(a);
+    e = hipGetLastError();
+    if (e != hipSuccess || a.parts == 1) return e;
+    const size_t count = n * w->rows;
+    k_gemm_reduce<<<(unsigned)((count + 255) / 256), 256, 0, dev->stream>>>(out, a.part_out, count, a.parts, mode);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n, int add) {
+    hipError_t e = gemm_prepare(dev, x, n, w->cols);
+    return e != hipSuccess ? e : gemm_run(dev, w, out, n, add ? kGemmAdd : kGemmStore);
 }

@@ -28,11 +28,9 @@ hipError_t launch_matvec_q4k_multi(dwim_dev *dev, const dwim_weight *const *ws, 
             if (e != hipSuccess) return e;
             in = xn;
         }
-        for (int j = 0; j < count; j++) {
-            hipError_t e = launch_gemm_q4k(dev, ws[j], outs[j], in, n, 0);
-            if (e != hipSuccess) return e;
-        }
-        return hipSuccess;
+        hipError_t e = gemm_prepare(dev, in, n, ws[0]->cols);
+        for (int j = 0; j < count && e == hipSuccess; j++) e = gemm_run(dev, ws[j], outs[j], n, kGemmStore);
+        return e;
     }
 }
 
@@ -45,20 +43,19 @@ hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_
         return launch_mv_q4k_mfma_tokens(dev, ws, outs, nullptr, 2, 1, x, n, norm, eps, nullptr);
     }
     {
-        // x normalized, gate·x into out, up·x into the work scratch, then silu(out)·up
-        const size_t cols = gate->cols, rows = gate->rows;
-        float *work = dev_work(dev, n * rows + (norm ? n * cols : 0));
-        if (!work) return hipErrorOutOfMemory;
+        // x normalized, split once; gate·x into out, then out = silu(out)·(up·x)
+        const size_t cols = gate->cols;
         const float *in = x;
         if (norm) {
-            float *xn = work + n * rows;
+            float *xn = dev_work(dev, n * cols);
+            if (!xn) return hipErrorOutOfMemory;
             hipError_t e = launch_rmsnorm(dev->stream, xn, x, norm, n, cols, eps);
             if (e != hipSuccess) return e;
             in = xn;
         }
-        hipError_t e = launch_gemm_q4k(dev, gate, out, in, n, 0);
-        if (e == hipSuccess) e = launch_gemm_q4k(dev, up, work, in, n, 0);
-        if (e == hipSuccess) e = launch_silu_mul(dev->stream, out, work, n * rows);
+        hipError_t e = gemm_prepare(dev, in, n, cols);
+        if (e == hipSuccess) e = gemm_run(dev, gate, out, n, kGemmStore);
+        if (e == hipSuccess) e = gemm_run(dev, up, out, n, kGemmSiluGate);
         return e;
     }
 }

@@ -28,8 +28,11 @@ struct dwim_dev {
     size_t prepared = 0;     // width of the planes dwim_prepare wrote (0: none, or replaced)
     void *split = nullptr;   // the f16 hi/lo parts of a batch's activations (k_gemm_q4k)
     size_t split_cap = 0;    // bytes
+    size_t split_n = 0, split_cols = 0;  // the batch the split holds
     float *work = nullptr;   // normalized activations / a product's second result
     size_t work_cap = 0;     // floats
+    float *gemm_parts = nullptr;  // a k-split batch product's partial results (k_gemm_q4k)
+    size_t gemm_parts_cap = 0;    // floats
     // Split one-token Q4_K products (k_mv_q4k_mfma.hip): the partial sums of
     // up to mv_tiles_cap 16-row tiles (4 parts × 32 floats each) and a counter
     // per tile, zero between launches.
@@ -208,5 +211,11 @@ hipError_t launch_gdn(dwim_dev *dev, const float *qkv, const float *conv_state, 
 // out (+)= w · x for n tokens on the f16 matrix cores (x's hi/lo parts are
 // written to the device's split scratch first)
 hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n, int add);
+// The same in two steps, so that products of one x share its split:
+// gemm_prepare writes x's parts ([n][cols]) to the device's split scratch,
+// gemm_run multiplies a weight of that many columns by them, out by the mode.
+enum GemmMode { kGemmStore = 0, kGemmAdd = 1, kGemmSiluGate = 2 /* out = silu(out)·(w·x) */ };
+hipError_t gemm_prepare(dwim_dev *dev, const float *x, size_t n, size_t cols);
+hipError_t gemm_run(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, int mode);
 // the device's work scratch, grown to at least `floats`
 float *dev_work(dwim_dev *dev, size_t floats);

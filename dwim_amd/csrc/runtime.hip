@@ -91,6 +91,7 @@ void dwim_dev_release_resources(dwim_dev *dev) {
     if (dev->planes) hipFree(dev->planes);
     if (dev->split) hipFree(dev->split);
     if (dev->work) hipFree(dev->work);
+    if (dev->gemm_parts) hipFree(dev->gemm_parts);
     hipStreamDestroy(dev->stream);
     delete dev;
 }
