@@ -10,13 +10,16 @@
 // across all the batch's tokens: thread (column c, part p) holds keys
 // 8p..8p+7 of column c, and the 16 parts of a column are 16 adjacent lanes
 // whose partial sums meet by DPP moves.  The token loop is a chain of
-// dependent steps, so it is kept short: the gates (g, beta) of a run of
-// tokens are computed once per block into LDS, the next token's inputs are
-// loaded while the current one is computed, and each sum runs in two
-// accumulators.  The slice is read from HBM once and written once per call,
-// through LDS so that both are coalesced.
+// dependent steps, so it is kept short and free of global loads: the inputs
+// of a run of 64 tokens (keys, queries, the block's values, the gates g and
+// beta) are staged in LDS at once, the next run's loaded into registers while
+// this run's tokens are computed, and each sum runs in two accumulators.  The
+// slice is read from HBM once and written once per call, through LDS so that
+// both are coalesced.
 #include "device_util.h"
 #include "runtime.h"
+
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -25,7 +28,7 @@ constexpr int kCols = 16;    // value columns per block
 constexpr int kParts = 16;   // key parts per column
 constexpr int kKeys = kD / kParts;
 constexpr int kThreads = kCols * kParts;
-constexpr int kGRun = 1024;  // tokens whose gates a block tabulates at once
+constexpr int kRun = 64;  // tokens whose inputs a block stages in LDS at once
 
 // sum over 16 aligned adjacent lanes, every lane getting it: quad xor 1 and
 // 2, then the half-row mirror (lane i and 7 − i) and the row mirror (i and
@@ -43,9 +46,13 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
                                                         const float *__restrict__ gates,
                                                         const float *__restrict__ decay, float *__restrict__ state,
                                                         size_t n, int n_k_heads, int n_v_heads, Rms rms) {
-    __shared__ float tile[kD][kCols + 1];
+    // a run's keys and queries [token][key] (also the state slice's staging
+    // at the start and the end), values [token][column] and gates
+    __shared__ v4f kq[2][kRun][kD / 4];
+    __shared__ float vs[kRun][kCols];
+    __shared__ float2 gb[kRun];  // per token: g, beta
     __shared__ float red[kThreads / 64];
-    __shared__ float2 gb[kGRun];  // per token: g, beta
+    float(*tile)[kCols + 1] = (float(*)[kCols + 1]) & kq[0][0][0];  // [kD][kCols + 1]
     // the gates' RMS scale, when the gate projection took x·w unscaled
     float gs = 1.0f;
     if (rms.ss) {
@@ -68,42 +75,56 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
 
     const float scale = 1.0f / sqrtf((float)kD);
     const float a = decay[h], dt = decay[n_v_heads + h];
-    // token t + 1's inputs are loaded while token t is computed
-    struct In {
-        float4 k4[kKeys / 4], q4[kKeys / 4];
-        float v;
-    };
-    auto fetch = [&](size_t t, In &in) {
-        const float4 *kt = (const float4 *)(k + (t * n_k_heads + kh) * kD + p * kKeys);
-        const float4 *qt = (const float4 *)(q + (t * n_k_heads + kh) * kD + p * kKeys);
+    // a run's inputs, loaded into registers while the run before it is
+    // computed: thread i takes float4s i, i + 256, ... of the run's keys and
+    // queries ([2][kRun][32] float4s), and value (token i / 16, column i % 16)
+    // for i < kRun·16 (four a thread), and the gate logits of token i < kRun
+    constexpr int kKQ = 2 * kRun * kD / 4 / kThreads, kV = kRun * kCols / kThreads;
+    v4f rkq[kKQ];  // (vector types: an array of float4 structs stays in private memory)
+    float rv[kV], ra = 0.0f, rb = 0.0f;
+    auto fetch = [&](size_t r0) {
+        const size_t rn = n - r0 < (size_t)kRun ? n - r0 : (size_t)kRun;
 #pragma unroll
-        for (int i = 0; i < kKeys / 4; i++) {
-            in.k4[i] = kt[i];
-            in.q4[i] = qt[i];
+        for (int u = 0; u < kKQ; u++) {
+            const int f = threadIdx.x + kThreads * u, which = f / (kRun * kD / 4), tok = (f / (kD / 4)) % kRun;
+            const size_t t = r0 + ((size_t)tok < rn ? tok : 0);
+            rkq[u] = ((const v4f *)((which ? q : k) + (t * n_k_heads + kh) * kD))[f % (kD / 4)];
         }
-        in.v = v[(t * n_v_heads + h) * kD + c0 + c];
+#pragma unroll
+        for (int u = 0; u < kV; u++) {
+            const int f = threadIdx.x + kThreads * u, tok = f / kCols;
+            const size_t t = r0 + ((size_t)tok < rn ? tok : 0);
+            rv[u] = v[(t * n_v_heads + h) * kD + c0 + f % kCols];
+        }
+        if (threadIdx.x < kRun) {
+            const size_t t = r0 + (threadIdx.x < rn ? threadIdx.x : 0);
+            ra = gates[t * 2 * n_v_heads + h];
+            rb = gates[t * 2 * n_v_heads + n_v_heads + h];
+        }
     };
-    In cur, nxt;
-    if (n > 0) fetch(0, nxt);
-    for (size_t r0 = 0; r0 < n; r0 += kGRun) {
-        // this run's gates: g = exp(a·softplus(alpha + dt_bias)), beta = sigmoid(beta_logit)
-        const size_t rn = n - r0 < (size_t)kGRun ? n - r0 : (size_t)kGRun;
-        __syncthreads();
-        for (size_t t = threadIdx.x; t < rn; t += kThreads) {
-            const float alpha = gs * gates[(r0 + t) * 2 * n_v_heads + h];
-            const float beta = sigmoidf_(gs * gates[(r0 + t) * 2 * n_v_heads + n_v_heads + h]);
-            gb[t] = make_float2(expf(a * softplusf_(alpha + dt)), beta);
+    if (n > 0) fetch(0);
+    for (size_t r0 = 0; r0 < n; r0 += kRun) {
+        const size_t rn = n - r0 < (size_t)kRun ? n - r0 : (size_t)kRun;
+        __syncthreads();  // the run before has been read
+#pragma unroll
+        for (int u = 0; u < kKQ; u++) {
+            const int f = threadIdx.x + kThreads * u;
+            (&kq[0][0][0])[f] = rkq[u];
         }
+#pragma unroll
+        for (int u = 0; u < kV; u++) (&vs[0][0])[threadIdx.x + kThreads * u] = rv[u];
+        // g = exp(a·softplus(alpha + dt_bias)), beta = sigmoid(beta_logit)
+        if (threadIdx.x < kRun) gb[threadIdx.x] = make_float2(expf(a * softplusf_(gs * ra + dt)), sigmoidf_(gs * rb));
         __syncthreads();
+        if (r0 + kRun < n) fetch(r0 + kRun);
         for (size_t tt = 0; tt < rn; tt++) {
             const size_t t = r0 + tt;
-            cur = nxt;
-            if (t + 1 < n) fetch(t + 1, nxt);
             float kk[kKeys], qq[kKeys];
 #pragma unroll
             for (int i = 0; i < kKeys / 4; i++) {
-                kk[4 * i] = cur.k4[i].x; kk[4 * i + 1] = cur.k4[i].y; kk[4 * i + 2] = cur.k4[i].z; kk[4 * i + 3] = cur.k4[i].w;
-                qq[4 * i] = cur.q4[i].x; qq[4 * i + 1] = cur.q4[i].y; qq[4 * i + 2] = cur.q4[i].z; qq[4 * i + 3] = cur.q4[i].w;
+                const v4f k4 = kq[0][tt][p * (kKeys / 4) + i], q4 = kq[1][tt][p * (kKeys / 4) + i];
+                kk[4 * i] = k4.x; kk[4 * i + 1] = k4.y; kk[4 * i + 2] = k4.z; kk[4 * i + 3] = k4.w;
+                qq[4 * i] = q4.x; qq[4 * i + 1] = q4.y; qq[4 * i + 2] = q4.z; qq[4 * i + 3] = q4.w;
             }
             const float2 g2 = gb[tt];
             const float g = g2.x, beta = g2.y;
@@ -116,7 +137,7 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
                 kv1 += s[i + 1] * kk[i + 1];
             }
             const float kv = sum16(kv0 + kv1);
-            const float ub = (cur.v - kv) * beta;
+            const float ub = (vs[tt][c] - kv) * beta;
             float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
             for (int i = 0; i < kKeys; i += 2) {
@@ -131,6 +152,7 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
     }
 
     // state slice out, through LDS
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < kKeys; i++) tile[p * kKeys + i][c] = s[i];
     __syncthreads();
