@@ -164,6 +164,79 @@ def cpu_baseline():
             "seconds": time.time() - t0}
 
 
+def mtp_leg(dev, D, M, prompt_len=32768, sessions=2, tokens=64, k=3):
+    """the 27B-shape model with a 1-layer MTP drafter,
+    `sessions` sessions sharing the weights, each prefilled with a
+    `prompt_len`-token uniform-random prompt; then `tokens` tokens of greedy
+    speculative decoding (k drafts a step, verified as one (k + 1)-token
+    batch: the batch matvecs run on the int8 matrix cores), timed, and from
+    the same state (mark / rewind_to_mark) `tokens` tokens of plain greedy
+    decoding, timed; the two sequences must be equal (qwen35/mod.rs:2100-2149).
+    The loop is the reference's Local::step with a greedy sampler
+    (inference/local.rs:320-368)."""
+    cfg = M.config_27b(drafter=True)
+    model = M.Model(dev, cfg, seed=4321, body_format=D.Q4_K, head_format=D.Q6_K, max_len=prompt_len + 2 * tokens + 16)
+    rng = np.random.default_rng(55)
+    seqs = [0] + [model.add_sequence() for _ in range(sessions - 1)]
+    out = {"sessions": sessions, "prompt": prompt_len, "tokens": tokens, "drafts_per_step": k}
+    prefill_s = spec_s = plain_s = 0.0
+    accepted = drafted = steps = 0
+    match = True
+    for seq in seqs:
+        model.select_sequence(seq)
+        prompt = rng.integers(0, cfg.vocab, prompt_len).astype(np.uint32)
+        dev.sync()
+        t0 = time.perf_counter()
+        first = model.forward_greedy(prompt, 0)
+        dev.sync()
+        prefill_s += time.perf_counter() - t0
+        model.mark()
+        # speculative
+        t0 = time.perf_counter()
+        spec, token, pos = [], first, prompt_len
+        while len(spec) < tokens:
+            spec.append(token)
+            drafts = model.draft(token, pos, k)
+            steps += 1
+            if not drafts:
+                token = model.forward_greedy([token], pos)
+                pos += 1
+                continue
+            drafted += len(drafts)
+            _, picks = model.verify([token] + drafts, pos, want_logits=False)
+            keep = 1
+            for i, d in enumerate(drafts):
+                if picks[i] != d or len(spec) >= tokens:
+                    break
+                spec.append(d)
+                keep += 1
+                accepted += 1
+            model.rewind(keep)
+            pos += keep
+            token = picks[keep - 1]
+        dev.sync()
+        spec_s += time.perf_counter() - t0
+        # plain greedy from the same state
+        model.rewind_to_mark()
+        t0 = time.perf_counter()
+        plain, token, pos = [], first, prompt_len
+        while len(plain) < tokens:
+            plain.append(token)
+            token = model.forward_greedy([token], pos)
+            pos += 1
+        dev.sync()
+        plain_s += time.perf_counter() - t0
+        match = match and spec[:tokens] == plain
+    model.close()
+    out.update({"prefill_tok_s": sessions * prompt_len / prefill_s,
+                "speculative_tok_s": sessions * tokens / spec_s, "plain_tok_s": sessions * tokens / plain_s,
+                "verify_steps": steps, "drafted": drafted, "accepted": accepted,
+                "acceptance": accepted / drafted if drafted else 0.0,
+                "speculative_equals_greedy": bool(match),
+                "note": "random-init drafter: acceptance near zero, so each step yields about one token"})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +245,9 @@ def main():
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-only", action="store_true", help="only the decode-matvec roofline leg")
+    ap.add_argument("--mtp", action="store_true",
+                    help="also the speculative-decoding leg (config 5: MTP drafter, 2 sessions of 32768-token prompts)")
+    ap.add_argument("--mtp-prompt", type=int, default=32768)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
@@ -250,6 +326,8 @@ def main():
                      "kernel_us": roof["us"], "algorithmic_bytes": roof["bytes"]},
     }
     model.close()
+    if args.mtp:
+        result["mtp"] = mtp_leg(dev, D, M, prompt_len=args.mtp_prompt)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

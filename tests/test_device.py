@@ -213,7 +213,9 @@ def test_prepared_activations_serve_several_matrices(gpu):
 
 def test_q4_k_swiglu_and_matmul_add_match_cpu(gpu):
     rng = O.Rng(24)
-    for rows, cols, n in [(256, 5120, 1), (1024, 1024, 1), (512, 1280, 3), (256, 512, 9)]:
+    # n >= 16 runs the f16 GEMM: SwiGLU in the up product's epilogue, the add,
+    # and (few tiles: 4×1 here) the k split with its ordered reduce
+    for rows, cols, n in [(256, 5120, 1), (1024, 1024, 1), (512, 1280, 3), (256, 512, 9), (1024, 5120, 40)]:
         make = _k_quantized(O.Q4_K, rows + n)
         gate, up = make(rows, cols), make(rows, cols)
         x = rng.floats(n * cols)
