@@ -359,6 +359,20 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         read(buf, 3, f1);
         mma(f0);
         mma(f1);
+        // the order the scheduler keeps: slice 0's 8 fragment reads, then the
+        // 16 MFMAs of slices 0-2 each with the next slice's reads between
+        // them (a read after every two MFMAs), then slice 3's MFMAs; left to
+        // itself it reuses one set of fragment registers and waits for each
+        // read
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int k = 0; k < 3; k++)
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
         if (g == 3) {
             // the block ends: times d, plus its min term: [−hi, −hi]·[X_hi, X_lo]
             // and [−lo, 0]·[X_hi, 0] over the 8 sub-blocks of each k half
