@@ -121,12 +121,13 @@ extern "C" int dwim_memory(dwim_dev *dev, uint64_t *free_bytes) {
     return 0;
 }
 
-// Prefill batches of 2048 tokens: the batch GEMM's 256 × 128 tiles then come
-// to over 4 workgroups a CU for the 27B shape's matrices (at 512 tokens the
-// 17408-row products make 272 tiles for 256 CUs, a second round nearly
-// empty), and a batch's activations (2048 × 17408 f32 at most) stay small
-// next to 288 GB.
-extern "C" size_t dwim_batch(dwim_dev *) { return 2048; }
+// Prefill batches of 4096 tokens: the batch GEMM's 256 × 128 tiles then come
+// to over 8 workgroups a CU for the 27B shape's matrices, so that the last,
+// partly filled round of workgroups is a small share (at 2048 tokens the
+// 17408-row products make 1088 tiles for 256 CUs: 4.25 rounds; measured 4%
+// faster prefill at 4096), and a batch's activations (4096 × 17408 f32 at
+// most) stay small next to 288 GB.
+extern "C" size_t dwim_batch(dwim_dev *) { return 4096; }
 
 extern "C" int dwim_sync(dwim_dev *dev) {
     DWIM_HIP(hipStreamSynchronize(dev->stream));
