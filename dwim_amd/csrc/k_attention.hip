@@ -290,10 +290,11 @@ __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ o
 // ---------------------------------------------------------------- prefill
 //
 // Causal GQA for a batch of tokens on the f16 matrix cores (flash attention
-// with an online softmax), head_dim 256.  A block of 4 waves takes one query
-// head and 64 tokens, a wave 16 of them; the queries stay in registers as f16
-// hi + lo parts (times 1/16 = 1/sqrt(256), exact).  The block walks the
-// positions in blocks of 32:
+// with an online softmax), head_dim 256.  A block of 8 waves takes one query
+// head and 128 tokens, a wave 16 of them (the keys' and values' conversion
+// serves 128 queries); the queries stay in registers as f16 hi + lo parts
+// (times 1/16 = 1/sqrt(256), exact).  The block walks the positions in
+// blocks of 32, the next block's loads in flight meanwhile:
 //   * the keys, int8 (exact in f16), give per 32-dimension group g the sums
 //     Σ q·k8 (two MFMAs, hi and lo), which the group's f16 cache scale then
 //     weights: S = Σ_g s_k[p][g] · Σ_{d∈g} q_d k8_d;
@@ -306,7 +307,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ o
 typedef _Float16 ahalf8 __attribute__((ext_vector_type(8)));
 typedef float afloat4 __attribute__((ext_vector_type(4)));
 
-constexpr int kFD = 256, kFQ = 64, kFP = 32, kFThreads = 256;
+constexpr int kFD = 256, kFQ = 128, kFP = 32, kFThreads = 512;
 
 struct PrefillArgs {
     float *out;
@@ -335,7 +336,7 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
     __shared__ uint32_t v8[kFP][kFD / 4];        // values, int8, [pos][256]
     __shared__ float vsc[kFP][kFD / 32];         // value scales
     __shared__ uint4 vt[2][kFD][kFP / 8];        // values hi / lo, [dim][pos]
-    __shared__ uint4 pw[4][2][16][kFP / 8];      // per wave: P hi / lo, [row][pos]
+    __shared__ uint4 pw[kFThreads / 64][2][16][kFP / 8];  // per wave: P hi / lo, [row][pos]
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, kg = lane >> 4;
     const unsigned h = blockIdx.y, kvh = h / (a.heads / a.kv_heads);
     const unsigned t0 = blockIdx.x * kFQ;
@@ -374,58 +375,76 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
 #pragma unroll
     for (int i = 0; i < 16; i++) o[i] = afloat4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // staging: threads 0-255 take the keys, 256-511 the values, of position
+    // pp = (tid % 256) / 8, 32-byte piece c; the next step's are loaded while
+    // this step is computed
+    const int sp = (tid & 255) >> 3, sc8 = tid & 7;
+    const bool skeys = tid < 256;
+    const int8_t *const ssrc = skeys ? a.kq : a.vq;
+    const uint16_t *const sscl = skeys ? a.ks : a.vs;
+    uint4 nx0, nx1;
+    uint16_t nxs;
+    auto fetch = [&](unsigned p0) {
+        const unsigned p = p0 + sp;
+        const bool live = p < len;
+        const size_t row = (size_t)(live ? p : 0) * kv_dim + (size_t)kvh * kFD;
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        const uint4 v0 = *(const uint4 *)(ssrc + row + 32 * sc8), v1 = *(const uint4 *)(ssrc + row + 32 * sc8 + 16);
+        const uint16_t sv = sscl[row / 32 + sc8];
+        nx0 = live ? v0 : z;
+        nx1 = live ? v1 : z;
+        nxs = live ? sv : 0;
+    };
+    fetch(0);
     for (unsigned p0 = 0; p0 < len; p0 += kFP) {
         // ---- stage the 32 positions: keys to f16, values raw, scales
         __syncthreads();
         {
-            const int pp = tid >> 3, c = tid & 7;  // position, 32-byte piece
-            const unsigned p = p0 + pp;
-            const bool live = p < len;
-            const size_t row = (size_t)(live ? p : 0) * kv_dim + (size_t)kvh * kFD;
-            const uint4 k0 = live ? *(const uint4 *)(a.kq + row + 32 * c) : make_uint4(0, 0, 0, 0);
-            const uint4 k1 = live ? *(const uint4 *)(a.kq + row + 32 * c + 16) : make_uint4(0, 0, 0, 0);
-            const uint4 w0 = live ? *(const uint4 *)(a.vq + row + 32 * c) : make_uint4(0, 0, 0, 0);
-            const uint4 w1 = live ? *(const uint4 *)(a.vq + row + 32 * c + 16) : make_uint4(0, 0, 0, 0);
-            const uint16_t sk = live ? a.ks[row / 32 + c] : 0, sv = live ? a.vs[row / 32 + c] : 0;
-            ksc[pp][c] = dq::from_f16(sk);
-            vsc[pp][c] = dq::from_f16(sv);
-            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            const uint4 x0 = nx0, x1 = nx1;
+            const uint16_t xs = nxs;
+            if (p0 + kFP < len) fetch(p0 + kFP);
+            if (skeys) {
+                ksc[sp][sc8] = dq::from_f16(xs);
+                const uint32_t kw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int q = 0; q < 4; q++) {  // 8 keys a 16-byte chunk of f16
-                uint32_t hw[4];
+                for (int q = 0; q < 4; q++) {  // 8 keys a 16-byte chunk of f16
+                    uint32_t hw[4];
 #pragma unroll
-                for (int e = 0; e < 2; e++) {
-                    const uint32_t word = kw[2 * q + e];
-                    const _Float16 b0 = (_Float16)(float)(int8_t)(word & 0xffu), b1 = (_Float16)(float)(int8_t)((word >> 8) & 0xffu);
-                    const _Float16 b2 = (_Float16)(float)(int8_t)((word >> 16) & 0xffu), b3 = (_Float16)(float)(int8_t)(word >> 24);
-                    hw[2 * e] = (uint32_t)__builtin_bit_cast(uint16_t, b0) | (uint32_t)__builtin_bit_cast(uint16_t, b1) << 16;
-                    hw[2 * e + 1] = (uint32_t)__builtin_bit_cast(uint16_t, b2) | (uint32_t)__builtin_bit_cast(uint16_t, b3) << 16;
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t word = kw[2 * q + e];
+                        const _Float16 b0 = (_Float16)(float)(int8_t)(word & 0xffu), b1 = (_Float16)(float)(int8_t)((word >> 8) & 0xffu);
+                        const _Float16 b2 = (_Float16)(float)(int8_t)((word >> 16) & 0xffu), b3 = (_Float16)(float)(int8_t)(word >> 24);
+                        hw[2 * e] = (uint32_t)__builtin_bit_cast(uint16_t, b0) | (uint32_t)__builtin_bit_cast(uint16_t, b1) << 16;
+                        hw[2 * e + 1] = (uint32_t)__builtin_bit_cast(uint16_t, b2) | (uint32_t)__builtin_bit_cast(uint16_t, b3) << 16;
+                    }
+                    const int chunk = 4 * sc8 + q;  // of 32 per row
+                    kf[sp * 32 + (chunk ^ (sp & 15))] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
                 }
-                const int chunk = 4 * c + q;  // of 32 per row
-                kf[pp * 32 + (chunk ^ (pp & 15))] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-            }
-            const uint32_t vw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            } else {
+                vsc[sp][sc8] = dq::from_f16(xs);
+                const uint32_t vw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int q = 0; q < 8; q++) v8[pp][8 * c + q] = vw[q];
+                for (int q = 0; q < 8; q++) v8[sp][8 * sc8 + q] = vw[q];
+            }
         }
         __syncthreads();
-        // ---- the values transposed: thread (dims 4dq..4dq+3, positions 8j..8j+7)
+        // ---- the values transposed: thread (dims 4dq + 2hf, + 1; positions 8j..8j+7)
         {
-            const int dq4 = tid & 63, j = tid >> 6;
-            float vv[4][8];
+            const int dq4 = tid & 63, j = (tid >> 6) & 3, hf = tid >> 8;
+            float vv[2][8];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int p = 8 * j + i;
                 const uint32_t word = v8[p][dq4];
                 const float sc = vsc[p][dq4 / 8];
 #pragma unroll
-                for (int d = 0; d < 4; d++) vv[d][i] = (float)(int8_t)((word >> (8 * d)) & 0xffu) * sc;
+                for (int d = 0; d < 2; d++) vv[d][i] = (float)(int8_t)((word >> (8 * (2 * hf + d))) & 0xffu) * sc;
             }
 #pragma unroll
-            for (int d = 0; d < 4; d++) {
+            for (int d = 0; d < 2; d++) {
                 const ahalf8 hh = hi8(vv[d]), ll = lo8(vv[d], hh);
-                vt[0][4 * dq4 + d][j] = __builtin_bit_cast(uint4, hh);
-                vt[1][4 * dq4 + d][j] = __builtin_bit_cast(uint4, ll);
+                vt[0][4 * dq4 + 2 * hf + d][j] = __builtin_bit_cast(uint4, hh);
+                vt[1][4 * dq4 + 2 * hf + d][j] = __builtin_bit_cast(uint4, ll);
             }
         }
         __syncthreads();
@@ -457,8 +476,7 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
                 pv[tcol][e] = ok ? sacc[tcol][e] : -INFINITY;
                 mx = fmaxf(mx, pv[tcol][e]);
             }
-#pragma unroll
-            for (int k = 1; k < 16; k <<= 1) mx = fmaxf(mx, __shfl_xor(mx, k, 64));
+            mx = group_max<16>(mx);
             const float mn = fmaxf(m[e], mx);
             const float alpha = mn == -INFINITY ? 1.0f : expf(m[e] - mn);
             float sum = 0.0f;
@@ -468,8 +486,7 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
                 pv[tcol][e] = pe;
                 sum += pe;
             }
-#pragma unroll
-            for (int k = 1; k < 16; k <<= 1) sum += __shfl_xor(sum, k, 64);
+            sum = group_sum<16>(sum);
             l[e] = l[e] * alpha + sum;
             m[e] = mn;
 #pragma unroll
