@@ -131,7 +131,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     // [2][256][2] min operands, [2][128][2] sub-block sums, [2][256] d and 1/d
     uint4 *A = lds, *Bh = A + 2 * kRows * 8, *Bl = Bh + 2 * kToks * 8, *Am = Bl + 2 * kToks * 8,
           *Xm = Am + 2 * kRows * 2;
-    float *Dd = (float *)(Xm + 2 * kToks * 2), *Di = Dd + 2 * kRows;
+    float *Dd = (float *)(Xm + 2 * kToks * 2), *Dr = Dd + 2 * kRows;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // XCD-major numbering: workgroup bx runs on XCD bx % 8
     const unsigned per = a.grid / 8, lin = (blockIdx.x % 8) * per + blockIdx.x / 8;
@@ -192,6 +192,8 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
             const uint4 m = __builtin_bit_cast(uint4, ms0[b * 2]);
             L.m = xlive ? m : z4;
         };
+        // the current block's unit and quant factor, the previous block's unit
+        float unit = 1.0f, qscale = 1.0f, prev_unit = 1.0f;
         // dequantize step s into buffer s % 2 (and at a block's first group
         // the block's data into its buffer)
         auto stage = [&](unsigned s, const StepLoad &L) {
@@ -201,12 +203,21 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
             scale_min(hdr, 2 * g, sc0, mn0);
             scale_min(hdr, 2 * g + 1, sc1, mn1);
             if ((hdr.x & 0x7fffu) == 0) sc0 = sc1 = 0;  // d = 0: the block's products are zero
+            const float d0 = dq::from_f16((uint16_t)(hdr.x & 0xffffu));
+            const float dmin = dq::from_f16((uint16_t)(hdr.x >> 16));
+            if (g == 0) {
+                // the block's unit: d, or (d = 0, or dmin·63/d past f16 range for
+                // the min operands) a larger one, the quants scaled by d/unit
+                unit = fmaxf(d0 != 0.0f ? fabsf(d0) : 1.0f, fabsf(dmin) * (63.0f / 30000.0f));
+                qscale = d0 / unit;  // 1 but for such blocks
+            }
             // sc·q exactly in f16: a nibble q ORed into the mantissa of 1024
             // gives 1024 + q (the high nibble, masked in place, 1024 + 16q),
             // minus 1024 exactly, times sc (sc/16), exactly; two weights a
             // packed op
-            const half2v s0 = half2v{(_Float16)sc0, (_Float16)sc0};
-            const half2v s1 = half2v{(_Float16)((float)sc1 * 0.0625f), (_Float16)((float)sc1 * 0.0625f)};
+            const float f0 = (float)sc0 * qscale, f1 = (float)sc1 * qscale * 0.0625f;  // (exact when qscale = 1)
+            const half2v s0 = half2v{(_Float16)f0, (_Float16)f0};
+            const half2v s1 = half2v{(_Float16)f1, (_Float16)f1};
             const half2v k1024 = half2v{(_Float16)1024.0f, (_Float16)1024.0f};
             uint4 *row = A + (buf * kRows + ar) * 8;
 #pragma unroll
@@ -236,26 +247,27 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
                 (k >= 4 ? Bl : Bh)[(buf * kToks + t) * 8 + swz(t, xc)] = L.x[k];
             }
             if (g == 0) {
-                // the block's min operands −dmin·m_sb (hi, lo), d (1 when d
-                // is 0) and 1/d, and the tokens' sub-block sums
-                const float d0 = dq::from_f16((uint16_t)(hdr.x & 0xffffu));
-                const float d = d0 != 0.0f ? d0 : 1.0f;
-                const float dmin = -dq::from_f16((uint16_t)(hdr.x >> 16));  // the min term is subtracted
+                // the block's min operands −dmin·m_sb/unit (hi, lo), the unit
+                // (for the end) and the previous block's unit over this one
+                // (the accumulators' change of units), and the tokens'
+                // sub-block sums
+                const float nm = -dmin / unit;  // the min term is subtracted
                 uint32_t mh[4], ml[4];
 #pragma unroll
                 for (int j = 0; j < 8; j += 2) {
                     int sa, ma, sb_, mb;
                     scale_min(hdr, j, sa, ma);
                     scale_min(hdr, j + 1, sb_, mb);
-                    const float va = dmin * (float)ma, vb = dmin * (float)mb;
+                    const float va = nm * (float)ma, vb = nm * (float)mb;
                     const _Float16 ha = (_Float16)va, hb = (_Float16)vb;
                     mh[j / 2] = pack2(ha, hb);
                     ml[j / 2] = pack2((_Float16)(va - (float)ha), (_Float16)(vb - (float)hb));
                 }
                 Am[(bb * kRows + ar) * 2] = make_uint4(mh[0], mh[1], mh[2], mh[3]);
                 Am[(bb * kRows + ar) * 2 + 1] = make_uint4(ml[0], ml[1], ml[2], ml[3]);
-                Dd[bb * kRows + ar] = d;
-                Di[bb * kRows + ar] = 1.0f / d;
+                Dd[bb * kRows + ar] = unit;
+                Dr[bb * kRows + ar] = prev_unit / unit;
+                prev_unit = unit;
                 Xm[(bb * kToks + bt) * 2 + bq] = L.m;
             }
         };
@@ -288,9 +300,10 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     // a 16-wide k slice; C's column l % 32, rows 8g + 4(l / 32) + e).  A
     // step's four k slices are software-pipelined: slice k + 1's fragments are
     // read while slice k's MFMAs run.  acc holds the sums in units of the
-    // current block's d: 1/d_b at the block's start, its products of exact
-    // f16 integers accumulate, then times d_b and its min term (negated)
-    // added at its end.
+    // current block's d (its "unit"): the block's products of exact f16
+    // integers and its min term (its operands pre-divided by the unit)
+    // accumulate, and at the next block's start acc is multiplied by
+    // unit_b / unit_{b+1}, once, at the end by the last unit.
     const int wr = wave >> 1, wc = wave & 1;
     const int r32 = lane & 31, kh = lane >> 5;
     float16v acc[4][2];
@@ -351,7 +364,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     auto step = [&](unsigned s, int g) {
         const unsigned buf = s % 2, bb = (s / 4) % 2;
         read(buf, 0, f0);
-        if (g == 0 && s > 0) scale_rows(Di + bb * kRows);
+        if (g == 0 && s > 0) scale_rows(Dr + bb * kRows);
         read(buf, 1, f1);
         mma(f0);
         read(buf, 2, f0);
@@ -374,9 +387,8 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
             }
         __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
         if (g == 3) {
-            // the block ends: times d, plus its min term: [−hi, −hi]·[X_hi, X_lo]
-            // and [−lo, 0]·[X_hi, 0] over the 8 sub-blocks of each k half
-            scale_rows(Dd + bb * kRows);
+            // the block's min term, in its unit: [−hi, −hi]·[X_hi, X_lo] and
+            // [−lo, 0]·[X_hi, 0] over the 8 sub-blocks of each k half
             const half8 zero = half8{0, 0, 0, 0, 0, 0, 0, 0};
             half8 x1[2], x2[2];
 #pragma unroll
@@ -407,6 +419,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         step(4 * b + 2, 2);
         step(4 * b + 3, 3);
     }
+    scale_rows(Dd + ((nb - 1) % 2) * kRows);  // out of the last block's unit
     // C tile (i, j): lane holds rows 32i + 8g + 4kh + e of token 32j + l % 32
     // (a part of a k-split product: its own slice of part_out, plainly)
     float *const dst = a.parts > 1 ? a.part_out + (size_t)part * a.n * a.rows : a.out;

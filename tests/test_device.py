@@ -193,6 +193,24 @@ def test_q4_k_one_token_at_the_edges_of_its_activations(gpu):
             close(got, want, 1e-4)
 
 
+def test_q4_k_near_constant_blocks(gpu):
+    # blocks of nearly one value: d tiny next to dmin (the batch GEMM then
+    # takes a larger unit than d for the block), next to ordinary ones
+    rows, cols = 64, 1024
+    rng = np.random.default_rng(9)
+    vals = rng.normal(0, 0.05, (rows, cols)).astype(np.float32)
+    vals[::3, :256] = 0.4 + rng.normal(0, 1e-7, (len(range(0, rows, 3)), 256))
+    vals[1::3, 512:768] = -0.3 + rng.normal(0, 1e-6, (len(range(1, rows, 3)), 256))
+    w = O.Weight.quantized(O.Q4_K, vals)
+    gw = gpu.upload(to_tensor(w))
+    for n in (1, 4, 40):
+        x = O.Rng(90 + n).floats(n * cols)
+        want = O.matmul(w, x)
+        out = gpu.alloc(n * rows)
+        gpu.matmul(out, gw, gpu.buffer(x))
+        close(gpu.read(out), want, 1e-4)
+
+
 def test_prepared_activations_serve_several_matrices(gpu):
     cols = 1536
     make = _k_quantized(O.Q4_K, 61)
