@@ -22,6 +22,7 @@
 //   BF16  8 weights: out += Σw·x.
 // Q4_K, the format of the model's body, has a kernel of its own below.
 #include "device_util.h"
+#include "planes.h"
 #include "quant_math.h"
 #include "runtime.h"
 
@@ -332,7 +333,13 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
     Weights w{wt->q, wt->s, wt->s2, wt->s3, wt->rows, wt->cols};
     switch (wt->fmt) {
     case DWIM_Q4_K: return launch_matvec_q4k(dev, wt, out, x, n, add);
-    case DWIM_Q6_K: return launch_fmt<DWIM_Q6_K>(s, w, x, out, n, add);
+    case DWIM_Q6_K:
+        if (n == 1 && !add && wt->cols <= 10240) {  // (a workgroup's 8 waves take 5 blocks each)
+            // one token (the output head): the int8 matrix cores over x's planes
+            hipError_t e = launch_planes(dev, x, wt->cols, nullptr, 0.0f, nullptr, 0);
+            return e != hipSuccess ? e : launch_mv_q6k_mfma(dev, wt, out, 0);
+        }
+        return launch_fmt<DWIM_Q6_K>(s, w, x, out, n, add);
     case DWIM_Q4_0: return launch_fmt<DWIM_Q4_0>(s, w, x, out, n, add);
     case DWIM_Q8_0: return launch_fmt<DWIM_Q8_0>(s, w, x, out, n, add);
     default:

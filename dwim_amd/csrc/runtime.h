@@ -148,6 +148,9 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                                      int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
                                      float *xn_out);
+// A Q6_K weight times one token's planes in plane area `area` (the output
+// head; k_mv_q6k_mfma.hip).
+hipError_t launch_mv_q6k_mfma(dwim_dev *dev, const dwim_weight *w, float *out, int area);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
