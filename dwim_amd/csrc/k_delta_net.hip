@@ -159,13 +159,360 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
     for (int e = threadIdx.x; e < kD * kCols; e += kThreads) S[(e / kCols) * kD + c0 + e % kCols] = tile[e / kCols][e % kCols];
 }
 
+
+// ---- The chunked form, for batches of at least kC tokens -------------------
+//
+// Over a chunk of kC tokens with log decays lg_t and cumulative sums L_t (from
+// the chunk's start, so γ_t = exp(L_t) ≤ 1), the token loop above unrolls to
+// (the WY form of the delta rule):
+//   R = V − diag(γ)·K·S                  (kC × 128, per value column)
+//   U = X·R,   X = (I + A)⁻¹·diag(β),   A_ti = β_t·exp(L_t − L_i)·k_t·k_i (i < t)
+//   O = (diag(γ)·Q·S + M·U) / sqrt(d),  M_ti = exp(L_t − L_i)·q_t·k_i (i ≤ t)
+//   S ← γ_C·S + Kᵀ·diag(exp(L_C − L_t))·U
+// where S is the state at the chunk's start.  Padding tokens past the batch
+// have lg = 0, β = 0 and zero k, q, v, and change nothing.  Two kernels:
+// k_dn_prep builds X, M and the decays of every (value head, chunk) in
+// parallel (K·Kᵀ and Q·Kᵀ once per key head, on the fp32 matrix cores; X by
+// forward substitution, a column a lane), and k_dn_chunks walks the chunks of
+// a head in order with 16 of the state's value columns in registers, every
+// product on the fp32 matrix cores (v_mfma_f32_16x16x4_f32).  The algebra is
+// exact; the keys are unit vectors (the conv's l2 norm), so A's entries are
+// at most 1 in size and the substitution is well conditioned.
+constexpr int kC = 64;
+constexpr size_t kPrepLds = 4 * kC * sizeof(double) + (6 * kC * kC + 4 * kC) * sizeof(float);
+
+DEV v4f mfma4(float a, float b, v4f c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+// grid (chunks, key heads), 256 threads.  X, M: [n_v][chunks][kC][kC];
+// dec: [n_v][chunks][2][kC] (γ_t = exp(L_t), then exp(L_C − L_t))
+__global__ void __launch_bounds__(256) k_dn_prep(const float *__restrict__ q, const float *__restrict__ k,
+                                                 const float *__restrict__ gates, const float *__restrict__ decay,
+                                                 float *__restrict__ X, float *__restrict__ M, float *__restrict__ dec,
+                                                 size_t n, int n_k, int n_v) {
+    extern __shared__ double prep_lds[];
+    double(*Ls)[kC] = (double(*)[kC])prep_lds;
+    float(*kk)[kC] = (float(*)[kC])(prep_lds + 4 * kC);
+    float(*qk)[kC] = kk + kC;
+    float(*A)[kC][kC] = (float(*)[kC][kC])(qk + kC);
+    float(*bs)[kC] = (float(*)[kC])(A + 4);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r = lane & 15, kq = lane >> 4;
+    const size_t ch = blockIdx.x, nch = gridDim.x, t0 = ch * kC;
+    const int kh = blockIdx.y;
+    const size_t stride = (size_t)n_k * kD;
+    // K·Kᵀ (all sixteen 16×16 tiles: it is read by columns below) and Q·Kᵀ
+    // (the ten on and below the diagonal); lane (kq, r) feeds A[r][kq] and
+    // B[kq][r] with keys 4kq + j of each 16
+    for (int job = w; job < 26; job += 4) {
+        const int which = job >= 16;
+        int ti, tj;
+        if (!which) {
+            ti = job / 4;
+            tj = job % 4;
+        } else {
+            int jj = job - 16;
+            ti = 0;
+            while (jj > ti) jj -= ++ti;
+            tj = jj;
+        }
+        const size_t ta = t0 + 16 * ti + r, tb = t0 + 16 * tj + r;
+        const float za = ta < n ? 1.0f : 0.0f, zb = tb < n ? 1.0f : 0.0f;
+        const float *pa = (which ? q : k) + (ta < n ? ta : 0) * stride + kh * kD + 4 * kq;
+        const float *pb = k + (tb < n ? tb : 0) * stride + kh * kD + 4 * kq;
+        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < kD / 16; m++) {
+            const v4f a = *(const v4f *)(pa + 16 * m) * za, b = *(const v4f *)(pb + 16 * m) * zb;
+            acc = mfma4(a.x, b.x, acc);
+            acc = mfma4(a.y, b.y, acc);
+            acc = mfma4(a.z, b.z, acc);
+            acc = mfma4(a.w, b.w, acc);
+        }
+        float(*dst)[kC] = which ? qk : kk;
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[16 * ti + 4 * kq + i][16 * tj + r] = acc[i];
+    }
+    __syncthreads();
+    const int ratio = n_v / n_k;
+    for (int rr = w; rr < ratio; rr += 4) {
+        const int h = kh * ratio + rr;
+        const size_t t = t0 + lane;
+        float lg = 0.0f, beta = 0.0f;
+        if (t < n) {
+            lg = decay[h] * softplusf_(gates[t * 2 * n_v + h] + decay[n_v + h]);
+            beta = sigmoidf_(gates[t * 2 * n_v + n_v + h]);
+        }
+        // the cumulative log decay, in double: differences of sums of up to
+        // 64 terms are taken below
+        double L = lg;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const double u = __shfl_up(L, o, 64);
+            if (lane >= o) L += u;
+        }
+        const double LC = __shfl(L, 63, 64);
+        const size_t base = (size_t)h * nch + ch;
+        dec[base * 2 * kC + lane] = expf((float)L);
+        dec[base * 2 * kC + kC + lane] = expf((float)(LC - L));
+        Ls[w][lane] = L;
+        bs[w][lane] = beta;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // A by columns (At[i][t] = A_ti, lane t) and M by rows (M_it, lane t);
+        // L falls with t, so each decay below is exp of a value ≤ 0
+        float *Mg = M + base * kC * kC;
+#pragma unroll 2
+        for (int i = 0; i < kC; i++) {
+            const double Li = Ls[w][i];
+            const float e = expf((float)(lane > i ? L - Li : Li - L));
+            A[w][i][lane] = lane > i ? beta * e * kk[i][lane] : 0.0f;
+            Mg[i * kC + lane] = i >= lane ? e * qk[i][lane] : 0.0f;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // (I + A)·X = diag(β), right-looking: once row i of X is known, its
+        // terms join every later row's sum; lane j holds column j (its rows
+        // go out through LDS: 64 stores from registers would hold 64 addresses)
+        float *Xg = X + base * kC * kC;
+        float acc[kC];
+#pragma unroll
+        for (int t = 0; t < kC; t++) acc[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kC; i++) {
+            const float xi = (i == lane ? bs[w][i] : 0.0f) - acc[i];
+#pragma unroll
+            for (int t = (i + 4) & ~3; t < kC; t += 4) {
+                const v4f a = *(const v4f *)&A[w][i][t];
+                acc[t] += a.x * xi;
+                acc[t + 1] += a.y * xi;
+                acc[t + 2] += a.z * xi;
+                acc[t + 3] += a.w * xi;
+            }
+#pragma unroll
+            for (int t = i + 1; t < ((i + 4) & ~3); t++) acc[t] += A[w][i][t] * xi;
+            A[w][i][lane] = xi;  // column i of A is spent: row i of X takes its place
+            // the sums are brought up to date row by row (left to itself the
+            // compiler defers them and keeps all of A in registers)
+#pragma unroll
+            for (int t = i + 1; t < kC; t++) asm volatile("" : "+v"(acc[t]));
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll 4
+        for (int i = 0; i < kC; i++) Xg[i * kC + lane] = A[w][i][lane];
+    }
+}
+
+// grid: 8 column blocks × n_v heads (all the blocks of a key head on one XCD
+// when n_k is a multiple of 8), 256 threads.  Wave w holds keys 32w..32w+31
+// of the block's 16 columns, as two 16×16 accumulator tiles.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_dn_chunks(float *__restrict__ out, const float *__restrict__ q,
+                                                   const float *__restrict__ k, const float *__restrict__ v,
+                                                   const float *__restrict__ X, const float *__restrict__ M,
+                                                   const float *__restrict__ dec, float *__restrict__ state,
+                                                   size_t n, int n_k, int n_v) {
+    __shared__ float part[4][2][kC][kCols];
+    __shared__ float Rs[kC][kCols], Us[kC][kCols], Ud[kC][kCols];
+    // each wave's keys of the chunk, transposed ([key][token], rows padded
+    // to stay 16-byte aligned without bank conflicts)
+    __shared__ float KT[4][32][kC + 4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r = lane & 15, kq = lane >> 4;
+    const int ratio = n_v / n_k;
+    const unsigned b = blockIdx.x;
+    int h, cb;
+    if (n_k % 8 == 0) {
+        const unsigned idx = b / 8, per = (unsigned)(ratio * 8);
+        const int kh = (int)(b % 8) * (n_k / 8) + (int)(idx / per);
+        h = kh * ratio + (int)((idx % per) / 8);
+        cb = (int)(idx % 8);
+    } else {
+        h = (int)(b / 8);
+        cb = (int)(b % 8);
+    }
+    const int kh = h / ratio, c0 = cb * kCols;
+    const size_t stride = (size_t)n_k * kD, vstride = (size_t)n_v * kD;
+    float *S = state + (size_t)h * kD * kD;
+    v4f s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[kt][i] = S[(32 * w + 16 * kt + 4 * kq + i) * kD + c0 + r];
+    const size_t nch = (n + kC - 1) / kC;
+    const float scale = 1.0f / sqrtf((float)kD);
+    // every global load is issued a step or more before its use: the keys
+    // and queries of K·S and Q·S a chunk ahead (right after the last use),
+    // the rest at the start of the chunk that uses it
+    v4f kf[4][2], qf[4][2];
+    auto fetch_kq = [&](size_t t0) {
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+            const size_t t = t0 + 16 * tt + r;
+            const float z = t < n ? 1.0f : 0.0f;
+            const size_t off = (t < n ? t : 0) * stride + kh * kD + 32 * w + 4 * kq;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+                kf[tt][kt] = *(const v4f *)(k + off + 16 * kt) * z;
+                qf[tt][kt] = *(const v4f *)(q + off + 16 * kt) * z;
+            }
+        }
+    };
+    // X's and M's rows of token tile w, the values and decays of its tokens,
+    // loaded a chunk ahead too (right after their last use)
+    v4f xr[4], mr[4];
+    float vv[4], gg[4], ee[4], gC;
+    auto fetch_rows = [&](size_t ch) {
+        const size_t t0 = ch * kC, base = (size_t)h * nch + ch;
+        const float *Lc = dec + base * 2 * kC;
+        const float *Xc = X + base * kC * kC + (16 * w + r) * kC + 4 * kq;
+        const float *Mc = M + base * kC * kC + (16 * w + r) * kC + 4 * kq;
+#pragma unroll
+        for (int ut = 0; ut < 4; ut++) {
+            xr[ut] = *(const v4f *)(Xc + 16 * ut);
+            mr[ut] = *(const v4f *)(Mc + 16 * ut);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 16 * w + 4 * kq + i;
+            const size_t tg = t0 + t;
+            vv[i] = v[(tg < n ? tg : 0) * vstride + h * kD + c0 + r] * (tg < n ? 1.0f : 0.0f);
+            gg[i] = Lc[t];
+            ee[i] = Lc[kC + t];
+        }
+        gC = Lc[kC - 1];
+    };
+    if (nch) {
+        fetch_kq(0);
+        fetch_rows(0);
+    }
+    for (size_t ch = 0; ch < nch; ch++) {
+        const size_t t0 = ch * kC;
+        // K·S and Q·S over this wave's keys, every token
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+            v4f pk = {0.0f, 0.0f, 0.0f, 0.0f}, pq = pk;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+                const v4f a = kf[tt][kt], aq = qf[tt][kt];
+                pk = mfma4(a.x, s[kt].x, pk);
+                pk = mfma4(a.y, s[kt].y, pk);
+                pk = mfma4(a.z, s[kt].z, pk);
+                pk = mfma4(a.w, s[kt].w, pk);
+                pq = mfma4(aq.x, s[kt].x, pq);
+                pq = mfma4(aq.y, s[kt].y, pq);
+                pq = mfma4(aq.z, s[kt].z, pq);
+                pq = mfma4(aq.w, s[kt].w, pq);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                part[w][0][16 * tt + 4 * kq + i][r] = pk[i];
+                part[w][1][16 * tt + 4 * kq + i][r] = pq[i];
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) KT[w][16 * kt + 4 * kq + j][16 * tt + r] = kf[tt][kt][j];
+        if (ch + 1 < nch) fetch_kq(t0 + kC);
+        __syncthreads();
+        // token tile w: R = V − γ·K·S, and O starts as γ·Q·S
+        v4f o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 16 * w + 4 * kq + i;
+            const float ks = part[0][0][t][r] + part[1][0][t][r] + part[2][0][t][r] + part[3][0][t][r];
+            const float qs = part[0][1][t][r] + part[1][1][t][r] + part[2][1][t][r] + part[3][1][t][r];
+            Rs[t][r] = vv[i] - gg[i] * ks;
+            o[i] = gg[i] * qs;
+        }
+        __syncthreads();
+        // U = X·R, X lower triangular
+        v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ut = 0; ut < 4; ut++) {
+            if (ut > w) break;
+            const v4f a = xr[ut];
+            u = mfma4(a.x, Rs[16 * ut + 4 * kq][r], u);
+            u = mfma4(a.y, Rs[16 * ut + 4 * kq + 1][r], u);
+            u = mfma4(a.z, Rs[16 * ut + 4 * kq + 2][r], u);
+            u = mfma4(a.w, Rs[16 * ut + 4 * kq + 3][r], u);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 16 * w + 4 * kq + i;
+            Us[t][r] = u[i];
+            Ud[t][r] = u[i] * ee[i];
+        }
+        __syncthreads();
+        // O += M·U, M lower triangular
+#pragma unroll
+        for (int ut = 0; ut < 4; ut++) {
+            if (ut > w) break;
+            const v4f a = mr[ut];
+            o = mfma4(a.x, Us[16 * ut + 4 * kq][r], o);
+            o = mfma4(a.y, Us[16 * ut + 4 * kq + 1][r], o);
+            o = mfma4(a.z, Us[16 * ut + 4 * kq + 2][r], o);
+            o = mfma4(a.w, Us[16 * ut + 4 * kq + 3][r], o);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const size_t tg = t0 + 16 * w + 4 * kq + i;
+            if (tg < n) out[tg * vstride + h * kD + c0 + r] = o[i] * scale;
+        }
+        const float gCc = gC;
+        if (ch + 1 < nch) fetch_rows(ch + 1);
+        // S = γ_C·S + Kᵀ·diag(exp(L_C − L_t))·U
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            s[kt] *= gCc;
+#pragma unroll
+            for (int ut = 0; ut < 4; ut++) {
+                const v4f a = *(const v4f *)&KT[w][16 * kt + r][16 * ut + 4 * kq];
+                s[kt] = mfma4(a.x, Ud[16 * ut + 4 * kq][r], s[kt]);
+                s[kt] = mfma4(a.y, Ud[16 * ut + 4 * kq + 1][r], s[kt]);
+                s[kt] = mfma4(a.z, Ud[16 * ut + 4 * kq + 2][r], s[kt]);
+                s[kt] = mfma4(a.w, Ud[16 * ut + 4 * kq + 3][r], s[kt]);
+            }
+        }
+    }
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) S[(32 * w + 16 * kt + 4 * kq + i) * kD + c0 + r] = s[kt][i];
+}
+
 }  // namespace
 
-hipError_t launch_delta_net(hipStream_t s, float *out, const float *q, const float *k, const float *v,
+hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k, const float *v,
                             const float *gates, const float *decay, float *state, size_t n, size_t n_k_heads,
                             size_t n_v_heads, size_t head_dim, const Rms *rms) {
+    if (n >= (size_t)kC && !(rms && rms->ss)) {
+        const size_t nch = (n + kC - 1) / kC;
+        const size_t need = n_v_heads * nch * (2 * kC * kC + 2 * kC);
+        if (dev->dn_work_cap < need) {
+            if (dev->dn_work) hipFree(dev->dn_work);
+            dev->dn_work = nullptr;
+            dev->dn_work_cap = 0;
+            hipError_t e = hipMalloc(&dev->dn_work, need * sizeof(float));
+            if (e != hipSuccess) return e;
+            dev->dn_work_cap = need;
+        }
+        float *X = dev->dn_work, *M = X + n_v_heads * nch * kC * kC, *dec = M + n_v_heads * nch * kC * kC;
+        static bool lds_set = false;
+        if (!lds_set) {
+            hipError_t e = hipFuncSetAttribute((const void *)k_dn_prep, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)kPrepLds);
+            if (e != hipSuccess) return e;
+            lds_set = true;
+        }
+        k_dn_prep<<<dim3((unsigned)nch, (unsigned)n_k_heads), 256, kPrepLds, dev->stream>>>(q, k, gates, decay, X, M, dec, n,
+                                                                                   (int)n_k_heads, (int)n_v_heads);
+        k_dn_chunks<<<(unsigned)(8 * n_v_heads), 256, 0, dev->stream>>>(out, q, k, v, X, M, dec, state, n,
+                                                                         (int)n_k_heads, (int)n_v_heads);
+        return hipGetLastError();
+    }
     dim3 grid(kD / kCols, (unsigned)n_v_heads);
-    k_delta_net<<<grid, kThreads, 0, s>>>(out, q, k, v, gates, decay, state, n, (int)n_k_heads, (int)n_v_heads,
-                                          rms ? *rms : Rms{});
+    k_delta_net<<<grid, kThreads, 0, dev->stream>>>(out, q, k, v, gates, decay, state, n, (int)n_k_heads,
+                                                    (int)n_v_heads, rms ? *rms : Rms{});
     return hipGetLastError();
 }

@@ -33,6 +33,8 @@ struct dwim_dev {
     size_t work_cap = 0;     // floats
     float *gemm_parts = nullptr;  // a k-split batch product's partial results (k_gemm_q4k)
     size_t gemm_parts_cap = 0;    // floats
+    float *dn_work = nullptr;     // a batch delta rule's per-chunk matrices (k_delta_net.hip)
+    size_t dn_work_cap = 0;       // floats
     // Split one-token Q4_K products (k_mv_q4k_mfma.hip): the partial sums of
     // up to mv_tiles_cap 16-row tiles (4 parts × 32 floats each) and a counter
     // per tile, zero between launches.
@@ -168,7 +170,7 @@ struct Rms {
     float eps = 0.0f;
 };
 // with rms, the gate logits (alpha, beta) are scaled by it first
-hipError_t launch_delta_net(hipStream_t s, float *out, const float *q, const float *k,
+hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k,
                             const float *v, const float *gates, const float *decay, float *state,
                             size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim, const Rms *rms = nullptr);
 hipError_t launch_embed(hipStream_t s, float *out, const dwim_weight *w, const uint32_t *tokens,

@@ -92,6 +92,7 @@ void dwim_dev_release_resources(dwim_dev *dev) {
     if (dev->split) hipFree(dev->split);
     if (dev->work) hipFree(dev->work);
     if (dev->gemm_parts) hipFree(dev->gemm_parts);
+    if (dev->dn_work) hipFree(dev->dn_work);
     hipStreamDestroy(dev->stream);
     delete dev;
 }
@@ -531,7 +532,7 @@ extern "C" int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, c
     DWIM_CHECK(gates->len == n * 2 * n_v_heads && decay->len == 2 * n_v_heads, "delta_net: gates or decay");
     DWIM_CHECK(state->len == n_v_heads * head_dim * head_dim, "delta_net: the state");
     if (n)
-        LAUNCH(launch_delta_net(dev->stream, out->data, q->data, k->data, v->data, gates->data, decay->data,
+        LAUNCH(launch_delta_net(dev, out->data, q->data, k->data, v->data, gates->data, decay->data,
                                 state->data, n, n_k_heads, n_v_heads, head_dim));
     return 0;
 }

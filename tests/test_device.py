@@ -498,6 +498,28 @@ def test_delta_net_matches_cpu(gpu):
         close(gpu.read(st), want_state, 1e-4)
 
 
+def test_delta_net_in_chunks_matches_cpu(gpu):
+    """Batches of 64 tokens and more take the chunked form of the delta rule
+    (k_dn_prep + k_dn_chunks): the same outputs and final state as the
+    token loop, with the conv's unit keys and queries (gpu/cpu.rs:298-363).
+    63 tokens stay on the token loop; 100 ends in a partial chunk; 16/48 heads
+    is the 27B shape (its blocks grouped by key head)."""
+    rng = O.Rng(13)
+    for nk, nv, n in ((2, 6, 63), (2, 6, 64), (2, 6, 100), (1, 4, 200), (16, 48, 300)):
+        q, k, v, gates, decay, state = _delta_inputs(rng, n, nk, nv)
+        for a in (q, k):
+            r = a.reshape(n * nk, 128)
+            r /= np.sqrt((r.astype(np.float64) ** 2).sum(1, keepdims=True)).astype(np.float32)
+        want, want_state = O.delta_net(q, k, v, gates, decay, state, nk, nv, 128)
+        out = gpu.alloc(v.size)
+        st = gpu.buffer(state)
+        gpu.delta_net(out, gpu.buffer(q), gpu.buffer(k), gpu.buffer(v), gpu.buffer(gates), gpu.buffer(decay),
+                      st, nk, nv, 128)
+        print(f"heads {nk}/{nv}, {n} tokens", flush=True)
+        close(gpu.read(out), want, 1e-4)
+        close(gpu.read(st), want_state, 1e-4)
+
+
 def test_argmax_takes_the_first_maximum(gpu):
     rng = O.Rng(30)
     rows, cols = 5, 248_320
