@@ -426,17 +426,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             o[i] = gg[i] * qs;
         }
         __syncthreads();
-        // U = X·R, X lower triangular
-        v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
+        // U = X·R, X lower triangular (two accumulator chains: the longest
+        // chain, wave 3's, holds every wave at the next barrier)
+        v4f u = {0.0f, 0.0f, 0.0f, 0.0f}, u2 = u;
 #pragma unroll
         for (int ut = 0; ut < 4; ut++) {
             if (ut > w) break;
             const v4f a = xr[ut];
             u = mfma4(a.x, Rs[16 * ut + 4 * kq][r], u);
-            u = mfma4(a.y, Rs[16 * ut + 4 * kq + 1][r], u);
+            u2 = mfma4(a.y, Rs[16 * ut + 4 * kq + 1][r], u2);
             u = mfma4(a.z, Rs[16 * ut + 4 * kq + 2][r], u);
-            u = mfma4(a.w, Rs[16 * ut + 4 * kq + 3][r], u);
+            u2 = mfma4(a.w, Rs[16 * ut + 4 * kq + 3][r], u2);
         }
+        u += u2;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int t = 16 * w + 4 * kq + i;
@@ -445,15 +447,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
         __syncthreads();
         // O += M·U, M lower triangular
+        v4f o2 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ut = 0; ut < 4; ut++) {
             if (ut > w) break;
             const v4f a = mr[ut];
             o = mfma4(a.x, Us[16 * ut + 4 * kq][r], o);
-            o = mfma4(a.y, Us[16 * ut + 4 * kq + 1][r], o);
+            o2 = mfma4(a.y, Us[16 * ut + 4 * kq + 1][r], o2);
             o = mfma4(a.z, Us[16 * ut + 4 * kq + 2][r], o);
-            o = mfma4(a.w, Us[16 * ut + 4 * kq + 3][r], o);
+            o2 = mfma4(a.w, Us[16 * ut + 4 * kq + 3][r], o2);
         }
+        o += o2;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const size_t tg = t0 + 16 * w + 4 * kq + i;
@@ -464,15 +468,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         // S = γ_C·S + Kᵀ·diag(exp(L_C − L_t))·U
 #pragma unroll
         for (int kt = 0; kt < 2; kt++) {
+            v4f d = {0.0f, 0.0f, 0.0f, 0.0f};
             s[kt] *= gCc;
 #pragma unroll
             for (int ut = 0; ut < 4; ut++) {
                 const v4f a = *(const v4f *)&KT[w][16 * kt + r][16 * ut + 4 * kq];
                 s[kt] = mfma4(a.x, Ud[16 * ut + 4 * kq][r], s[kt]);
-                s[kt] = mfma4(a.y, Ud[16 * ut + 4 * kq + 1][r], s[kt]);
+                d = mfma4(a.y, Ud[16 * ut + 4 * kq + 1][r], d);
                 s[kt] = mfma4(a.z, Ud[16 * ut + 4 * kq + 2][r], s[kt]);
-                s[kt] = mfma4(a.w, Ud[16 * ut + 4 * kq + 3][r], s[kt]);
+                d = mfma4(a.w, Ud[16 * ut + 4 * kq + 3][r], d);
             }
+            s[kt] += d;
         }
     }
 #pragma unroll
