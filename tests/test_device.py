@@ -520,6 +520,33 @@ def test_delta_net_in_chunks_matches_cpu(gpu):
         close(gpu.read(st), want_state, 1e-4)
 
 
+def test_delta_net_chunks_agree_with_the_token_loop_at_full_size(gpu):
+    """4096 tokens at the 27B shape (16/48 heads): one call takes the chunked
+    form; the same tokens in calls of 63 take the token loop, the state
+    carried between calls.  Outputs and final state agree to 1e-4 (the
+    oracle at this size would take minutes; the two paths share no code)."""
+    rng = O.Rng(14)
+    nk, nv, n, step = 16, 48, 4096, 63
+    q, k, v, gates, decay, state = _delta_inputs(rng, n, nk, nv)
+    for a in (q, k):
+        r = a.reshape(n * nk, 128)
+        r /= np.sqrt((r.astype(np.float64) ** 2).sum(1, keepdims=True)).astype(np.float32)
+    out = gpu.alloc(v.size)
+    st = gpu.buffer(state)
+    gpu.delta_net(out, gpu.buffer(q), gpu.buffer(k), gpu.buffer(v), gpu.buffer(gates), gpu.buffer(decay),
+                  st, nk, nv, 128)
+    want_state, parts = gpu.buffer(state), []
+    for t0 in range(0, n, step):
+        t1 = min(n, t0 + step)
+        o = gpu.alloc((t1 - t0) * nv * 128)
+        gpu.delta_net(o, gpu.buffer(q[t0 * nk * 128:t1 * nk * 128]), gpu.buffer(k[t0 * nk * 128:t1 * nk * 128]),
+                      gpu.buffer(v[t0 * nv * 128:t1 * nv * 128]), gpu.buffer(gates[t0 * 2 * nv:t1 * 2 * nv]),
+                      gpu.buffer(decay), want_state, nk, nv, 128)
+        parts.append(gpu.read(o))
+    close(gpu.read(out), np.concatenate(parts), 1e-4)
+    close(gpu.read(st), gpu.read(want_state), 1e-4)
+
+
 def test_argmax_takes_the_first_maximum(gpu):
     rng = O.Rng(30)
     rows, cols = 5, 248_320
