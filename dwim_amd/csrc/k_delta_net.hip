@@ -179,7 +179,10 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
 // exact; the keys are unit vectors (the conv's l2 norm), so A's entries are
 // at most 1 in size and the substitution is well conditioned.
 constexpr int kC = 64;
-constexpr size_t kPrepLds = 4 * kC * sizeof(double) + (6 * kC * kC + 4 * kC) * sizeof(float);
+// k_dn_prep's LDS for `ratio` value heads a key head
+size_t prep_lds_bytes(int ratio) {
+    return (size_t)ratio * kC * sizeof(double) + ((size_t)ratio * kC + (1 + (ratio < 4 ? ratio : 4)) * kC * kC) * sizeof(float);
+}
 
 DEV v4f mfma4(float a, float b, v4f c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
@@ -189,16 +192,46 @@ __global__ void __launch_bounds__(256) k_dn_prep(const float *__restrict__ q, co
                                                  const float *__restrict__ gates, const float *__restrict__ decay,
                                                  float *__restrict__ X, float *__restrict__ M, float *__restrict__ dec,
                                                  size_t n, int n_k, int n_v) {
+    // LDS: each value head's cumulative log decays (double) and betas, K·Kᵀ,
+    // and an A matrix for each of up to 4 heads solved at once
     extern __shared__ double prep_lds[];
+    const int ratio = n_v / n_k;
     double(*Ls)[kC] = (double(*)[kC])prep_lds;
-    float(*kk)[kC] = (float(*)[kC])(prep_lds + 4 * kC);
-    float(*qk)[kC] = kk + kC;
-    float(*A)[kC][kC] = (float(*)[kC][kC])(qk + kC);
-    float(*bs)[kC] = (float(*)[kC])(A + 4);
+    float(*bs)[kC] = (float(*)[kC])(prep_lds + ratio * kC);
+    float(*kk)[kC] = (float(*)[kC])(bs + ratio);
+    float(*A)[kC][kC] = (float(*)[kC][kC])(kk + kC);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r = lane & 15, kq = lane >> 4;
     const size_t ch = blockIdx.x, nch = gridDim.x, t0 = ch * kC;
     const int kh = blockIdx.y;
     const size_t stride = (size_t)n_k * kD;
+    // K·Kᵀ (all sixteen 16×16 tiles: it is read by columns below) and Q·Kᵀ
+    // (the ten on and below the diagonal); lane (kq, r) feeds A[r][kq] and
+    // B[kq][r] with keys 4kq + j of each 16
+    // every value head's decays: g_t = exp(lg_t), lg_t = a·softplus(alpha +
+    // dt_bias), beta_t = sigmoid(beta logit); L_t = Σ lg up to t, in double:
+    // differences of sums of up to 64 terms are taken below
+    for (int rr = w; rr < ratio; rr += 4) {
+        const int h = kh * ratio + rr;
+        const size_t t = t0 + lane;
+        float lg = 0.0f, beta = 0.0f;
+        if (t < n) {
+            lg = decay[h] * softplusf_(gates[t * 2 * n_v + h] + decay[n_v + h]);
+            beta = sigmoidf_(gates[t * 2 * n_v + n_v + h]);
+        }
+        double L = lg;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const double u = __shfl_up(L, o, 64);
+            if (lane >= o) L += u;
+        }
+        const double LC = __shfl(L, 63, 64);
+        const size_t base = (size_t)h * nch + ch;
+        dec[base * 2 * kC + lane] = expf((float)L);
+        dec[base * 2 * kC + kC + lane] = expf((float)(LC - L));
+        Ls[rr][lane] = L;
+        bs[rr][lane] = beta;
+    }
+    __syncthreads();
     // K·Kᵀ (all sixteen 16×16 tiles: it is read by columns below) and Q·Kᵀ
     // (the ten on and below the diagonal); lane (kq, r) feeds A[r][kq] and
     // B[kq][r] with keys 4kq + j of each 16
@@ -227,45 +260,39 @@ __global__ void __launch_bounds__(256) k_dn_prep(const float *__restrict__ q, co
             acc = mfma4(a.z, b.z, acc);
             acc = mfma4(a.w, b.w, acc);
         }
-        float(*dst)[kC] = which ? qk : kk;
+        if (!which) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) dst[16 * ti + 4 * kq + i][16 * tj + r] = acc[i];
+            for (int i = 0; i < 4; i++) kk[16 * ti + 4 * kq + i][16 * tj + r] = acc[i];
+        } else {
+            // M_tc = exp(L_t − L_c)·q_t·k_c for c ≤ t, of every value head
+            // (the tiles above the diagonal are never read)
+            const int c = 16 * tj + r;
+            for (int rr = 0; rr < ratio; rr++) {
+                float *Mg = M + ((size_t)(kh * ratio + rr) * nch + ch) * kC * kC;
+                const double Lc = Ls[rr][c];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = 16 * ti + 4 * kq + i;
+                    const float e = expf((float)(t >= c ? Ls[rr][t] - Lc : 0.0));
+                    Mg[t * kC + c] = t >= c ? e * acc[i] : 0.0f;
+                }
+            }
+        }
     }
     __syncthreads();
-    const int ratio = n_v / n_k;
+    // each value head: A, then X by forward substitution (A[w]: wave w)
     for (int rr = w; rr < ratio; rr += 4) {
         const int h = kh * ratio + rr;
-        const size_t t = t0 + lane;
-        float lg = 0.0f, beta = 0.0f;
-        if (t < n) {
-            lg = decay[h] * softplusf_(gates[t * 2 * n_v + h] + decay[n_v + h]);
-            beta = sigmoidf_(gates[t * 2 * n_v + n_v + h]);
-        }
-        // the cumulative log decay, in double: differences of sums of up to
-        // 64 terms are taken below
-        double L = lg;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const double u = __shfl_up(L, o, 64);
-            if (lane >= o) L += u;
-        }
-        const double LC = __shfl(L, 63, 64);
         const size_t base = (size_t)h * nch + ch;
-        dec[base * 2 * kC + lane] = expf((float)L);
-        dec[base * 2 * kC + kC + lane] = expf((float)(LC - L));
-        Ls[w][lane] = L;
-        bs[w][lane] = beta;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // A by columns (At[i][t] = A_ti, lane t) and M by rows (M_it, lane t);
-        // L falls with t, so each decay below is exp of a value ≤ 0
-        float *Mg = M + base * kC * kC;
+        const double L = Ls[rr][lane];
+        const float beta = bs[rr][lane];
+        // A by columns (At[i][t] = A_ti, lane t); L falls with t, so each
+        // decay below is exp of a value ≤ 0
 #pragma unroll 2
         for (int i = 0; i < kC; i++) {
-            const double Li = Ls[w][i];
-            const float e = expf((float)(lane > i ? L - Li : Li - L));
+            const double Li = Ls[rr][i];
+            const float e = expf((float)(lane > i ? L - Li : 0.0));
             A[w][i][lane] = lane > i ? beta * e * kk[i][lane] : 0.0f;
-            Mg[i * kC + lane] = i >= lane ? e * qk[i][lane] : 0.0f;
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -278,7 +305,7 @@ __global__ void __launch_bounds__(256) k_dn_prep(const float *__restrict__ q, co
         for (int t = 0; t < kC; t++) acc[t] = 0.0f;
 #pragma unroll
         for (int i = 0; i < kC; i++) {
-            const float xi = (i == lane ? bs[w][i] : 0.0f) - acc[i];
+            const float xi = (i == lane ? bs[rr][i] : 0.0f) - acc[i];
 #pragma unroll
             for (int t = (i + 4) & ~3; t < kC; t += 4) {
                 const v4f a = *(const v4f *)&A[w][i][t];
@@ -504,14 +531,15 @@ hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const flo
             dev->dn_work_cap = need;
         }
         float *X = dev->dn_work, *M = X + n_v_heads * nch * kC * kC, *dec = M + n_v_heads * nch * kC * kC;
-        static bool lds_set = false;
-        if (!lds_set) {
+        const size_t lds = prep_lds_bytes((int)(n_v_heads / n_k_heads));
+        static size_t lds_set = 0;
+        if (lds > lds_set) {
             hipError_t e = hipFuncSetAttribute((const void *)k_dn_prep, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)kPrepLds);
+                                               (int)lds);
             if (e != hipSuccess) return e;
-            lds_set = true;
+            lds_set = lds;
         }
-        k_dn_prep<<<dim3((unsigned)nch, (unsigned)n_k_heads), 256, kPrepLds, dev->stream>>>(q, k, gates, decay, X, M, dec, n,
+        k_dn_prep<<<dim3((unsigned)nch, (unsigned)n_k_heads), 256, lds, dev->stream>>>(q, k, gates, decay, X, M, dec, n,
                                                                                    (int)n_k_heads, (int)n_v_heads);
         k_dn_chunks<<<(unsigned)(8 * n_v_heads), 256, 0, dev->stream>>>(out, q, k, v, X, M, dec, state, n,
                                                                          (int)n_k_heads, (int)n_v_heads);
