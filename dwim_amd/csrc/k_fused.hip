@@ -103,6 +103,75 @@ __global__ void __launch_bounds__(256) k_conv_l2_batch(float *__restrict__ q, fl
     }
 }
 
+// The same for kConvT tokens a block: the block's `dim` channels read each
+// input row once (the window of 4 slides in registers), the weights once as
+// a float4, and each token's l2 sum is a wave sum plus one exchange of the
+// waves' partials.
+constexpr int kConvT = 16;
+
+__global__ void __launch_bounds__(256) k_conv_l2_tokens(float *__restrict__ q, float *__restrict__ k,
+                                                        float *__restrict__ v, float *__restrict__ state_out,
+                                                        const float *__restrict__ x, const float *__restrict__ state,
+                                                        const float *__restrict__ w, size_t n, size_t qd, size_t kd,
+                                                        size_t vd, float eps) {
+    __shared__ float red[kConvT][4];
+    const size_t ch = qd + kd + vd;
+    const size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x, t0 = (size_t)blockIdx.y * kConvT;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const float4 wc = *(const float4 *)(w + c * 4);
+    // inputs t0 − 3 .. t0 − 1: x rows, or the state's rows before the batch
+    float win[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const long tp = (long)t0 + j - 3;
+        win[j] = tp >= 0 ? x[(size_t)tp * ch + c] : state[(size_t)(3 + tp) * ch + c];
+    }
+    float y[kConvT];
+#pragma unroll
+    for (int i = 0; i < kConvT; i++) {
+        const size_t t = t0 + i;
+        const float xi = t < n ? x[t * ch + c] : 0.0f;
+        float acc = 0.0f;
+        acc += wc.x * win[0];
+        acc += wc.y * win[1];
+        acc += wc.z * win[2];
+        acc += wc.w * xi;
+        y[i] = acc * sigmoidf_(acc);
+        if (t == n - 1) {
+            // the last three inputs carry over
+            state_out[c] = win[1];
+            state_out[ch + c] = win[2];
+            state_out[2 * ch + c] = xi;
+        }
+        win[0] = win[1];
+        win[1] = win[2];
+        win[2] = xi;
+    }
+    float *dst;
+    size_t stride, col;
+    bool norm = true;
+    if (c < qd) { dst = q; stride = qd; col = c; }
+    else if (c < qd + kd) { dst = k; stride = kd; col = c - qd; }
+    else { dst = v; stride = vd; col = c - qd - kd; norm = false; }
+    if (norm) {  // uniform over the block
+#pragma unroll
+        for (int i = 0; i < kConvT; i++) {
+            const float ss = group_sum<64>(y[i] * y[i]);
+            if (lane == 0) red[i][wave] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kConvT; i++) {
+            float ss = 0.0f;
+            for (int u = 0; u < waves; u++) ss += red[i][u];
+            y[i] *= 1.0f / sqrtf(ss + eps);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kConvT; i++)
+        if (t0 + i < n) dst[(t0 + i) * stride + col] = y[i];
+}
+
 // z = silu(z) · (att · (1/rms(att) · w)) per `dim`-row (rmsnorm, gpu/cpu.rs:
 // 157-166, then silu_mul, :238-242), four values a thread; with one token,
 // the result's planes too.
@@ -196,9 +265,12 @@ hipError_t launch_conv_l2(hipStream_t s, float *q, float *k, float *v, float *st
     if (n == 1)
         k_conv_l2<<<(unsigned)((qd + kd + vd) / dim), (unsigned)dim, 0, s>>>(q, k, v, state_out, x, state, w, n, qd,
                                                                              kd, vd, eps);
-    else
+    else if (n < (size_t)kConvT)
         k_conv_l2_batch<<<dim3((unsigned)((qd + kd + vd) / dim), (unsigned)n), (unsigned)dim, 0, s>>>(
             q, k, v, state_out, x, state, w, n, qd, kd, vd, eps);
+    else
+        k_conv_l2_tokens<<<dim3((unsigned)((qd + kd + vd) / dim), (unsigned)((n + kConvT - 1) / kConvT)),
+                           (unsigned)dim, 0, s>>>(q, k, v, state_out, x, state, w, n, qd, kd, vd, eps);
     return hipGetLastError();
 }
 

@@ -461,7 +461,7 @@ def test_conv_matches_cpu(gpu):
     rng = O.Rng(11)
     qd, kd, vd = 16, 16, 48
     ch = qd + kd + vd
-    for n in (1, 2, 7):
+    for n in (1, 2, 7, 16, 37):  # 16 and 37: the 16-token blocks, whole and ragged
         x = rng.floats(n * ch)
         state = rng.floats(3 * ch)
         w = rng.floats(ch * 4)
