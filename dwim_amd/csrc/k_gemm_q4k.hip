@@ -41,38 +41,30 @@ constexpr int kThreads = 512;
 
 // x [n][cols] f32 -> xh, xl [n][cols] f16 (hi and lo parts), and per
 // (token, block) xm [n][nb][16] f16: the 8 sub-block sums' hi parts, then
-// their lo parts.  A thread per (token, sub-block).
+// their lo parts.  A thread per float4, eight lanes per 32-value sub-block,
+// so that a wave's loads and stores are contiguous; the sub-block's sum is
+// an 8-lane DPP sum.
 __global__ void k_split(const float *__restrict__ x, _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
                         _Float16 *__restrict__ xm, size_t n, size_t cols) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // sub-block index over [n][cols/32]
-    if (i >= n * (cols / 32)) return;
-    const float4 *src = (const float4 *)(x + i * 32);
-    float s = 0.0f;
-    uint32_t hh[16], ll[16];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const float4 v = src[k];
-        const float e[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; q += 2) {
-            const _Float16 h0 = (_Float16)e[q], h1 = (_Float16)e[q + 1];
-            const _Float16 l0 = (_Float16)(e[q] - (float)h0), l1 = (_Float16)(e[q + 1] - (float)h1);
-            hh[2 * k + q / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16;
-            ll[2 * k + q / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | (uint32_t)__builtin_bit_cast(uint16_t, l1) << 16;
-        }
-        s += (v.x + v.y) + (v.z + v.w);
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // float4 index over [n][cols/4]
+    if (i >= n * (cols / 4)) return;  // whole sub-blocks: cols is a multiple of 32
+    const float4 v = ((const float4 *)x)[i];
+    const _Float16 h0 = (_Float16)v.x, h1 = (_Float16)v.y, h2 = (_Float16)v.z, h3 = (_Float16)v.w;
+    const _Float16 l0 = (_Float16)(v.x - (float)h0), l1 = (_Float16)(v.y - (float)h1);
+    const _Float16 l2 = (_Float16)(v.z - (float)h2), l3 = (_Float16)(v.w - (float)h3);
+    auto pk = [](_Float16 a, _Float16 b) {
+        return (uint32_t)__builtin_bit_cast(uint16_t, a) | (uint32_t)__builtin_bit_cast(uint16_t, b) << 16;
+    };
+    ((uint2 *)xh)[i] = make_uint2(pk(h0, h1), pk(h2, h3));
+    ((uint2 *)xl)[i] = make_uint2(pk(l0, l1), pk(l2, l3));
+    const float s = group_sum<8>((v.x + v.y) + (v.z + v.w));
+    if ((i & 7) == 0) {
+        const size_t sbi = i / 8, t = sbi / (cols / 32), sb = sbi % (cols / 32), b = sb / 8, j = sb % 8;
+        _Float16 *m = xm + (t * (cols / 256) + b) * 16;
+        const _Float16 sh = (_Float16)s;
+        m[j] = sh;
+        m[8 + j] = (_Float16)(s - (float)sh);
     }
-    uint4 *dh = (uint4 *)(xh + i * 32), *dl = (uint4 *)(xl + i * 32);
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        dh[k] = make_uint4(hh[4 * k], hh[4 * k + 1], hh[4 * k + 2], hh[4 * k + 3]);
-        dl[k] = make_uint4(ll[4 * k], ll[4 * k + 1], ll[4 * k + 2], ll[4 * k + 3]);
-    }
-    const size_t t = i / (cols / 32), sb = i % (cols / 32), b = sb / 8, j = sb % 8;
-    _Float16 *m = xm + (t * (cols / 256) + b) * 16;
-    const _Float16 sh = (_Float16)s;
-    m[j] = sh;
-    m[8 + j] = (_Float16)(s - (float)sh);
 }
 
 // what a product does with its result r and the output's old value o
@@ -494,7 +486,7 @@ hipError_t gemm_prepare(dwim_dev *dev, const float *x, size_t n, size_t cols) {
     }
     _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * cols, *xm = xl + n * cols;
     const size_t subs = n * (cols / 32);
-    k_split<<<(unsigned)((subs + 255) / 256), 256, 0, dev->stream>>>(x, xh, xl, xm, n, cols);
+    k_split<<<(unsigned)((subs * 8 + 255) / 256), 256, 0, dev->stream>>>(x, xh, xl, xm, n, cols);
     dev->split_n = n;
     dev->split_cols = cols;
     return hipGetLastError();
