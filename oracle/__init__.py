@@ -465,6 +465,8 @@ def _declare_model(L):
     L.or_model_draft.argtypes = [vp, ctypes.c_uint32, _sz, _sz, u32p]
     L.or_model_reset.restype = None
     L.or_model_reset.argtypes = [vp]
+    L.or_model_zero_residual_writes.restype = None
+    L.or_model_zero_residual_writes.argtypes = [vp]
     L.or_model_verify.restype = None
     L.or_model_verify.argtypes = [vp, u32p, _sz, _sz, _f32p]
     L.or_model_rewind.restype = None
@@ -529,6 +531,10 @@ class Model:
 
     def reset(self):
         self.L.or_model_reset(self.h)
+
+    def zero_residual_writes(self):
+        """Test hook: every ffn_down, attn_output and ssm_out becomes zero."""
+        self.L.or_model_zero_residual_writes(self.h)
 
     def __del__(self):
         if getattr(self, "h", None):

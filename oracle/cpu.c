@@ -7,6 +7,7 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <immintrin.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
@@ -49,9 +50,107 @@ static float row_dot(const or_weight *w, size_t r, const float *x) {
     abort();
 }
 
+/* or_dot_q4_k for many tokens at once, with the same arithmetic for every
+ * (row, token) pair: the row's nibbles are converted to floats once per tile
+ * of tokens, and each sub-block's Σx, which does not depend on the row, once
+ * per token.  The 8 lanes of a sub-block's Σq·x are one vector, summed in the
+ * same order (4 steps of 8 from zero, then sum8 from -0.0), and the total
+ * folds in d1·Σqx − m1·Σx sub-block after sub-block as or_dot_q4_k does. */
+
+static void matmul_q4_k(float *out, const or_weight *w, const float *x, size_t n) {
+    size_t rows = w->rows, cols = w->cols, subs = cols / 32;
+    const uint8_t *quants = (const uint8_t *)w->quants;
+    float *sx = (float *)malloc(n * subs * sizeof(float));
+#pragma omp parallel for schedule(static)
+    for (size_t t = 0; t < n; t++)
+        for (size_t s = 0; s < subs; s++) {
+            const float *xs = x + t * cols + 32 * s;
+            float l[8] = {0};
+            for (int c = 0; c < 4; c++)
+                for (int i = 0; i < 8; i++) l[i] += xs[8 * c + i];
+            float v = -0.0f;
+            for (int i = 0; i < 8; i++) v += l[i];
+            sx[t * subs + s] = v;
+        }
+    const size_t tile = 16;
+    for (size_t t0 = 0; t0 < n; t0 += tile) {
+        size_t t1 = t0 + tile < n ? t0 + tile : n;
+#pragma omp parallel
+        {
+            float *qf = (float *)aligned_alloc(32, cols * sizeof(float));
+            float *d1 = (float *)malloc(subs * sizeof(float)), *m1 = (float *)malloc(subs * sizeof(float));
+#pragma omp for schedule(static)
+            for (size_t r = 0; r < rows; r++) {
+                const uint8_t *row = quants + r * (cols / 256) * 144;
+                for (size_t b = 0; b < cols / 256; b++) {
+                    const uint8_t *blk = row + 144 * b;
+                    float d = or_from_f16((uint16_t)(blk[0] | blk[1] << 8));
+                    float dmin = or_from_f16((uint16_t)(blk[2] | blk[3] << 8));
+                    for (int j = 0; j < 8; j++) {
+                        uint8_t sc, m;
+                        or_q4_k_scale_min(j, blk + 4, &sc, &m);
+                        d1[8 * b + j] = d * (float)sc;
+                        m1[8 * b + j] = dmin * (float)m;
+                        for (int l = 0; l < 32; l++) {
+                            uint8_t byte = blk[16 + 32 * (j / 2) + l];
+                            qf[256 * b + 32 * j + l] = (float)((j % 2) ? (byte >> 4) : (byte & 0xf));
+                        }
+                    }
+                }
+                for (size_t t = t0; t < t1; t++) {
+                    const float *xt = x + t * cols;
+                    const float *st = sx + t * subs;
+                    float acc = 0.0f;
+                    for (size_t s0 = 0; s0 < subs; s0 += 8) {
+                        __m256 sq[8];
+                        for (int k = 0; k < 8; k++) {
+                            const float *qs = qf + 32 * (s0 + k), *xs = xt + 32 * (s0 + k);
+                            __m256 v = _mm256_setzero_ps();
+                            for (int c = 0; c < 4; c++)
+                                v = _mm256_add_ps(v, _mm256_mul_ps(_mm256_load_ps(qs + 8 * c), _mm256_loadu_ps(xs + 8 * c)));
+                            sq[k] = v;
+                        }
+                        /* transpose: lane i of sq[k] to lane k of tr[i], so that
+                         * -0.0 + tr[0] + ... + tr[7] is sum8 of each sub-block in order */
+                        __m256 a0 = _mm256_unpacklo_ps(sq[0], sq[1]), a1 = _mm256_unpackhi_ps(sq[0], sq[1]);
+                        __m256 a2 = _mm256_unpacklo_ps(sq[2], sq[3]), a3 = _mm256_unpackhi_ps(sq[2], sq[3]);
+                        __m256 a4 = _mm256_unpacklo_ps(sq[4], sq[5]), a5 = _mm256_unpackhi_ps(sq[4], sq[5]);
+                        __m256 a6 = _mm256_unpacklo_ps(sq[6], sq[7]), a7 = _mm256_unpackhi_ps(sq[6], sq[7]);
+                        __m256 b0 = _mm256_shuffle_ps(a0, a2, 0x44), b1 = _mm256_shuffle_ps(a0, a2, 0xee);
+                        __m256 b2 = _mm256_shuffle_ps(a1, a3, 0x44), b3 = _mm256_shuffle_ps(a1, a3, 0xee);
+                        __m256 b4 = _mm256_shuffle_ps(a4, a6, 0x44), b5 = _mm256_shuffle_ps(a4, a6, 0xee);
+                        __m256 b6 = _mm256_shuffle_ps(a5, a7, 0x44), b7 = _mm256_shuffle_ps(a5, a7, 0xee);
+                        __m256 tr[8] = {
+                            _mm256_permute2f128_ps(b0, b4, 0x20), _mm256_permute2f128_ps(b1, b5, 0x20),
+                            _mm256_permute2f128_ps(b2, b6, 0x20), _mm256_permute2f128_ps(b3, b7, 0x20),
+                            _mm256_permute2f128_ps(b0, b4, 0x31), _mm256_permute2f128_ps(b1, b5, 0x31),
+                            _mm256_permute2f128_ps(b2, b6, 0x31), _mm256_permute2f128_ps(b3, b7, 0x31)};
+                        __m256 sum = _mm256_set1_ps(-0.0f);
+                        for (int i = 0; i < 8; i++) sum = _mm256_add_ps(sum, tr[i]);
+                        __m256 term = _mm256_sub_ps(_mm256_mul_ps(_mm256_loadu_ps(d1 + s0), sum),
+                                                    _mm256_mul_ps(_mm256_loadu_ps(m1 + s0), _mm256_loadu_ps(st + s0)));
+                        float tv[8];
+                        _mm256_storeu_ps(tv, term);
+                        for (int k = 0; k < 8; k++) acc += tv[k];
+                    }
+                    out[t * rows + r] = acc;
+                }
+            }
+            free(qf);
+            free(d1);
+            free(m1);
+        }
+    }
+    free(sx);
+}
+
 /* gpu/cpu.rs:110-149: out[t][r] = w[r]·x[t], rows in parallel. */
 void or_matmul(float *out, const or_weight *w, const float *x, size_t n) {
     size_t rows = w->rows, cols = w->cols;
+    if (w->fmt == OR_Q4_K) {
+        matmul_q4_k(out, w, x, n);
+        return;
+    }
 #pragma omp parallel for schedule(static)
     for (size_t r = 0; r < rows; r++)
         for (size_t t = 0; t < n; t++) out[t * rows + r] = row_dot(w, r, x + t * cols);

@@ -123,33 +123,35 @@ static owned_weight mat(struct or_model *m, const char *name, int fmt, size_t ro
     o.w.rows = rows;
     o.w.cols = cols;
     uint64_t s = tensor_seed(m->seed, name);
-    float *row = malloc(cols * sizeof(float));
-    if (fmt == OR_BF16) {
-        uint16_t *q = malloc(rows * cols * 2);
-        for (size_t r = 0; r < rows; r++) {
-            or_synthetic_values(s, r * cols, cols, sigma, row);
-            for (size_t i = 0; i < cols; i++) q[r * cols + i] = or_to_bf16(row[i]);
-        }
-        o.quants = q;
-    } else if (fmt == OR_Q4_K || fmt == OR_Q6_K) {
-        size_t per = fmt == OR_Q4_K ? 144 : 210;
-        uint8_t *q = malloc(rows * (cols / 256) * per);
-        for (size_t r = 0; r < rows; r++) {
-            or_synthetic_values(s, r * cols, cols, sigma, row);
-            if (fmt == OR_Q4_K) or_quantize_q4_k_row(row, cols, q + r * (cols / 256) * per);
-            else or_quantize_q6_k_row(row, cols, q + r * (cols / 256) * per);
-        }
-        o.quants = q;
-    } else if (fmt == OR_Q4_0 || fmt == OR_Q8_0) {
+    if (fmt == OR_BF16) o.quants = malloc(rows * cols * 2);
+    else if (fmt == OR_Q4_K || fmt == OR_Q6_K) o.quants = malloc(rows * (cols / 256) * (fmt == OR_Q4_K ? 144 : 210));
+    else if (fmt == OR_Q4_0 || fmt == OR_Q8_0) {
         o.scales = malloc(rows * (cols / 32) * 2);
         o.quants = malloc(fmt == OR_Q4_0 ? rows * cols / 2 : rows * cols);
+    }
+    /* rows are independent streams of values: generated and quantized in parallel */
+#pragma omp parallel
+    {
+        float *row = malloc(cols * sizeof(float));
+#pragma omp for schedule(static)
         for (size_t r = 0; r < rows; r++) {
             or_synthetic_values(s, r * cols, cols, sigma, row);
-            if (fmt == OR_Q4_0) or_quantize_q4_0_row(row, cols, o.scales + r * (cols / 32), (uint8_t *)o.quants + r * cols / 2);
-            else or_quantize_q8_0_row(row, cols, o.scales + r * (cols / 32), (int8_t *)o.quants + r * cols);
+            switch (fmt) {
+            case OR_BF16:
+                for (size_t i = 0; i < cols; i++) ((uint16_t *)o.quants)[r * cols + i] = or_to_bf16(row[i]);
+                break;
+            case OR_Q4_K: or_quantize_q4_k_row(row, cols, (uint8_t *)o.quants + r * (cols / 256) * 144); break;
+            case OR_Q6_K: or_quantize_q6_k_row(row, cols, (uint8_t *)o.quants + r * (cols / 256) * 210); break;
+            case OR_Q4_0:
+                or_quantize_q4_0_row(row, cols, o.scales + r * (cols / 32), (uint8_t *)o.quants + r * cols / 2);
+                break;
+            case OR_Q8_0:
+                or_quantize_q8_0_row(row, cols, o.scales + r * (cols / 32), (int8_t *)o.quants + r * cols);
+                break;
+            }
         }
+        free(row);
     }
-    free(row);
     o.w.quants = o.quants;
     o.w.scales = o.scales;
     return o;
@@ -573,4 +575,29 @@ void or_model_reset(or_model *m) {
     m->carry = 0;
     m->n_verified = 0;
     m->marked = 0;
+}
+
+/* Test hook: zeroes every product that writes into the residual stream (each
+ * layer's ffn_down, attn_output and ssm_out), so that the logits reduce to the
+ * head applied to the normalized embedding of the last token. */
+static void zero_weight(owned_weight *o) {
+    const or_weight *w = &o->w;
+    size_t bytes = 0;
+    switch (w->fmt) {
+    case OR_BF16: bytes = w->rows * w->cols * 2; break;
+    case OR_Q4_K: bytes = w->rows * (w->cols / 256) * 144; break;
+    case OR_Q6_K: bytes = w->rows * (w->cols / 256) * 210; break;
+    case OR_Q4_0: bytes = w->rows * w->cols / 2; break;
+    case OR_Q8_0: bytes = w->rows * w->cols; break;
+    }
+    memset(o->quants, 0, bytes);
+    if (o->scales) memset(o->scales, 0, w->rows * (w->cols / 32) * 2);
+}
+
+void or_model_zero_residual_writes(or_model *m) {
+    for (size_t i = 0; i < m->c.layers; i++) {
+        layer_t *l = &m->layers[i];
+        zero_weight(&l->down);
+        zero_weight(l->attention ? &l->o : &l->out);
+    }
 }

@@ -124,6 +124,7 @@ void or_model_rewind(or_model *m, size_t keep);
 void or_model_mark(or_model *m);
 int or_model_rewind_to_mark(or_model *m);
 void or_model_reset(or_model *m);
+void or_model_zero_residual_writes(or_model *m);
 
 #ifdef __cplusplus
 }

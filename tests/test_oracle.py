@@ -455,3 +455,45 @@ def test_argmax_takes_the_first_maximum():
     assert O.argmax([1.0, 3.0, 3.0, 2.0]) == 1
     assert O.argmax([-1.0]) == 0
     assert O.argmax([0.0, -0.0, 0.0]) == 0
+
+
+def test_elementwise_closed_forms():
+    """cpu.rs:151-155 (add), :238-242 (silu_mul: gate·σ(gate)·up, the gate
+    overwritten) and :244-248 (sigmoid_mul: x·σ(gate)), against float64.  The
+    operands are chosen so that exchanging them, or dropping the sigmoid,
+    fails."""
+    rng = O.Rng(21)
+    a, b = rng.floats(4096) * np.float32(8), rng.floats(4096) * np.float32(3)
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    assert np.allclose(O.add(a, b), a64 + b64, rtol=0, atol=1e-6)
+    sig = lambda v: 1 / (1 + np.exp(-v))  # noqa: E731
+    got = O.silu_mul(a, b)
+    want = a64 * sig(a64) * b64
+    assert np.abs(got - want).max() <= 2e-6 * np.abs(want).max()
+    assert np.abs(got - b64 * sig(b64) * a64).max() > 1e-2
+    got = O.sigmoid_mul(a, b)
+    want = a64 * sig(b64)
+    assert np.abs(got - want).max() <= 2e-6 * np.abs(want).max()
+    assert np.abs(got - b64 * sig(a64)).max() > 1e-2
+    # exact special cases: σ(0) = 1/2, silu(0) = 0, σ(±large) saturates
+    z = np.zeros(4, np.float32)
+    assert np.array_equal(O.sigmoid_mul(np.full(4, 6.0, np.float32), z), np.full(4, 3.0, np.float32))
+    assert np.array_equal(O.silu_mul(z, np.ones(4, np.float32)), z)
+    big = np.array([100.0, -100.0], np.float32)
+    assert np.array_equal(O.sigmoid_mul(np.array([5.0, 5.0], np.float32), big), np.array([5.0, 0.0], np.float32))
+
+
+@pytest.mark.parametrize("n", [1, 3, 17, 70])
+def test_q4_k_matmul_of_many_tokens_is_each_row_dot_bit_for_bit(n):
+    """or_matmul takes Q4_K through a tiled path (nibbles converted once per
+    row and tile of tokens, Σx per sub-block once per token); every element
+    must carry exactly the bits of or_dot_q4_k on that row and token."""
+    rows, cols = 24, 1280
+    vals = (O.Rng(31).floats(rows * cols) * np.float32(0.05)).reshape(rows, cols)
+    w = O.Weight.quantized(O.Q4_K, vals)
+    x = O.Rng(32).floats(n * cols).reshape(n, cols)
+    x[0, :7] = 0.0
+    got = O.matmul(w, x).reshape(n, rows)
+    q = w.quants.reshape(rows, -1)
+    want = np.array([[O.dot_q4_k(q[r], x[t]) for r in range(rows)] for t in range(n)], np.float32)
+    assert got.tobytes() == want.tobytes()
