@@ -539,6 +539,58 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
 
 }  // namespace
 
+// The decode path's partial results: [token][head][chunk][head_dim + 2] floats.
+size_t attention_partials_floats(size_t n, size_t pos, size_t n_heads, size_t head_dim) {
+    const size_t chunks = (pos + n + kPos - 1) / kPos;
+    return n * n_heads * chunks * (head_dim + 2);
+}
+
+// Grows the device's partials buffer to `floats` (a model reserves its
+// largest once, when it is built, so that no forward pass allocates).
+hipError_t attention_reserve(dwim_dev *dev, size_t floats) {
+    return dev_grow(dev, (void **)&dev->partials, &dev->partials_cap, floats, sizeof(float));
+}
+
+namespace {
+
+// Both entry points' launches: the batch path on the matrix cores (no
+// scratch), or the chunked decode path with its partial results in
+// `partials` (at least attention_partials_floats).
+hipError_t attention_run(dwim_dev *dev, float *partials, float *out, const float *q, const dwim_cache *k,
+                         const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
+                         size_t n_kv_heads, const float *gate, planes::View pv) {
+    if (n >= 16 && !pv.q && head_dim == (size_t)kFD && n_heads % n_kv_heads == 0) {
+        // a batch of tokens: flash attention on the matrix cores
+        PrefillArgs pa{out, q, gate, k->q, v->q, k->s, v->s, (unsigned)n, (unsigned)pos, (unsigned)n_heads,
+                       (unsigned)n_kv_heads};
+        dim3 grid((unsigned)((n + kFQ - 1) / kFQ), (unsigned)n_heads);
+        k_attn_prefill<<<grid, kFThreads, 0, dev->stream>>>(pa);
+        return hipGetLastError();
+    }
+    const size_t len = pos + n, ch = kPos, chunks = (len + ch - 1) / ch;
+    Shape sh{n, pos, n_heads, head_dim, n_kv_heads, ch, chunks};
+    dim3 g1((unsigned)chunks, (unsigned)n_kv_heads, (unsigned)n);
+    switch (n_heads / n_kv_heads) {
+#define DWIM_PARTIAL(G) \
+    case G: k_attn_partial<G><<<g1, kPThreads, 0, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh); break;
+        DWIM_PARTIAL(1) DWIM_PARTIAL(2) DWIM_PARTIAL(3) DWIM_PARTIAL(4) DWIM_PARTIAL(5) DWIM_PARTIAL(6)
+        DWIM_PARTIAL(7) DWIM_PARTIAL(8)
+#undef DWIM_PARTIAL
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    dim3 g2((unsigned)n_heads, (unsigned)n);
+    k_attn_combine<<<g2, kThreads, 0, dev->stream>>>(out, partials, sh, gate, pv);
+    return hipGetLastError();
+}
+
+bool attention_shape_ok(size_t n_heads, size_t head_dim, size_t n_kv_heads) {
+    return !(head_dim % 32 || head_dim > kMaxD || n_kv_heads == 0 || n_heads % n_kv_heads ||
+             n_heads / n_kv_heads > kMaxG);
+}
+
+}  // namespace
+
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k, const dwim_cache *v,
                             size_t n, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads) {
     return launch_attention_gated(dev, out, q, k, v, n, pos, n_heads, head_dim, n_kv_heads, nullptr, -1);
@@ -547,9 +599,7 @@ hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwi
 hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                                   const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
                                   size_t n_kv_heads, const float *gate, int area) {
-    if (head_dim % 32 || head_dim > kMaxD || n_kv_heads == 0 || n_heads % n_kv_heads ||
-        n_heads / n_kv_heads > kMaxG)
-        return hipErrorInvalidValue;
+    if (!attention_shape_ok(n_heads, head_dim, n_kv_heads)) return hipErrorInvalidValue;
     planes::View pv{};
     if (area >= 0) {
         if (n != 1 || head_dim % 32 || n_heads * head_dim > planes::kMaxCols || (n_heads * head_dim) % 256)
@@ -557,38 +607,10 @@ hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, con
         pv = planes_area(dev, area, n_heads * head_dim);
         dev->prepared = 0;
     }
-    if (n >= 16 && area < 0 && head_dim == (size_t)kFD && n_heads % n_kv_heads == 0) {
-        // a batch of tokens: flash attention on the matrix cores
-        PrefillArgs pa{out, q, gate, k->q, v->q, k->s, v->s, (unsigned)n, (unsigned)pos, (unsigned)n_heads,
-                       (unsigned)n_kv_heads};
-        dim3 grid((unsigned)((n + kFQ - 1) / kFQ), (unsigned)n_heads);
-        k_attn_prefill<<<grid, kFThreads, 0, dev->stream>>>(pa);
-        return hipGetLastError();
-    }
-    size_t len = pos + n;
-    const size_t ch = kPos;
-    size_t chunks = (len + ch - 1) / ch;
-    size_t need = n * n_heads * chunks * (head_dim + 2);
-    if (dev->partials_cap < need) {
-        if (dev->partials) hipFree(dev->partials);
-        dev->partials = nullptr;
-        dev->partials_cap = 0;
-        hipError_t e = hipMalloc(&dev->partials, need * sizeof(float));
+    const bool batch = n >= 16 && area < 0 && head_dim == (size_t)kFD;
+    if (!batch) {
+        hipError_t e = attention_reserve(dev, attention_partials_floats(n, pos, n_heads, head_dim));
         if (e != hipSuccess) return e;
-        dev->partials_cap = need;
     }
-    Shape sh{n, pos, n_heads, head_dim, n_kv_heads, ch, chunks};
-    dim3 g1((unsigned)chunks, (unsigned)n_kv_heads, (unsigned)n);
-    switch (n_heads / n_kv_heads) {
-#define DWIM_PARTIAL(G) \
-    case G: k_attn_partial<G><<<g1, kPThreads, 0, dev->stream>>>(dev->partials, q, k->q, k->s, v->q, v->s, sh); break;
-        DWIM_PARTIAL(1) DWIM_PARTIAL(2) DWIM_PARTIAL(3) DWIM_PARTIAL(4) DWIM_PARTIAL(5) DWIM_PARTIAL(6)
-        DWIM_PARTIAL(7) DWIM_PARTIAL(8)
-#undef DWIM_PARTIAL
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    dim3 g2((unsigned)n_heads, (unsigned)n);
-    k_attn_combine<<<g2, kThreads, 0, dev->stream>>>(out, dev->partials, sh, gate, pv);
-    return hipGetLastError();
+    return attention_run(dev, dev->partials, out, q, k, v, n, pos, n_heads, head_dim, n_kv_heads, gate, pv);
 }

@@ -516,20 +516,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 }  // namespace
 
+// The chunked form's per-chunk matrices (X, M and the decays) for n tokens.
+size_t delta_net_work_floats(size_t n, size_t n_v_heads) {
+    if (n < (size_t)kC) return 0;
+    const size_t nch = (n + kC - 1) / kC;
+    return n_v_heads * nch * (2 * kC * kC + 2 * kC);
+}
+
+hipError_t delta_net_reserve(dwim_dev *dev, size_t n, size_t n_v_heads) {
+    return dev_grow(dev, (void **)&dev->dn_work, &dev->dn_work_cap, delta_net_work_floats(n, n_v_heads),
+                    sizeof(float));
+}
+
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k, const float *v,
                             const float *gates, const float *decay, float *state, size_t n, size_t n_k_heads,
                             size_t n_v_heads, size_t head_dim, const Rms *rms) {
     if (n >= (size_t)kC && !(rms && rms->ss)) {
         const size_t nch = (n + kC - 1) / kC;
-        const size_t need = n_v_heads * nch * (2 * kC * kC + 2 * kC);
-        if (dev->dn_work_cap < need) {
-            if (dev->dn_work) hipFree(dev->dn_work);
-            dev->dn_work = nullptr;
-            dev->dn_work_cap = 0;
-            hipError_t e = hipMalloc(&dev->dn_work, need * sizeof(float));
-            if (e != hipSuccess) return e;
-            dev->dn_work_cap = need;
-        }
+        hipError_t e = delta_net_reserve(dev, n, n_v_heads);
+        if (e != hipSuccess) return e;
         float *X = dev->dn_work, *M = X + n_v_heads * nch * kC * kC, *dec = M + n_v_heads * nch * kC * kC;
         const size_t lds = prep_lds_bytes((int)(n_v_heads / n_k_heads));
         static size_t lds_set = 0;

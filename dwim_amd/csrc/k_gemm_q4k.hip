@@ -473,17 +473,24 @@ constexpr size_t kLds = (size_t)16 * (2 * kRows * 8 + 4 * kToks * 8 + 2 * kRows 
 
 size_t gemm_split_bytes(size_t n, size_t cols) { return 2 * n * cols * sizeof(_Float16) + n * (cols / 256) * 32; }
 
+// The partial results a k-split product of n tokens over a rows × cols
+// matrix keeps (0 when it does not split).
+size_t gemm_parts_floats(size_t n, size_t rows, size_t cols) {
+    const unsigned rtiles = (unsigned)((rows + kRows - 1) / kRows), ttiles = (unsigned)((n + kToks - 1) / kToks);
+    const unsigned p = gemm_parts(rtiles * ttiles, (unsigned)(cols / 256));
+    return p > 1 ? (size_t)p * n * rows : 0;
+}
+
+hipError_t gemm_reserve(dwim_dev *dev, size_t split_bytes, size_t parts_floats) {
+    hipError_t e = dev_grow(dev, &dev->split, &dev->split_cap, split_bytes, 1);
+    if (e != hipSuccess) return e;
+    return dev_grow(dev, (void **)&dev->gemm_parts, &dev->gemm_parts_cap, parts_floats, sizeof(float));
+}
+
 hipError_t gemm_prepare(dwim_dev *dev, const float *x, size_t n, size_t cols) {
     if (cols % 256 || n >= (1u << 31)) return hipErrorInvalidValue;
-    const size_t need = gemm_split_bytes(n, cols);
-    if (dev->split_cap < need) {
-        if (dev->split) hipFree(dev->split);
-        dev->split = nullptr;
-        dev->split_cap = 0;
-        hipError_t e = hipMalloc(&dev->split, need);
-        if (e != hipSuccess) return e;
-        dev->split_cap = need;
-    }
+    hipError_t e0 = dev_grow(dev, &dev->split, &dev->split_cap, gemm_split_bytes(n, cols), 1);
+    if (e0 != hipSuccess) return e0;
     _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * cols, *xm = xl + n * cols;
     const size_t subs = n * (cols / 32);
     k_split<<<(unsigned)((subs * 8 + 255) / 256), 256, 0, dev->stream>>>(x, xh, xl, xm, n, cols);
@@ -512,15 +519,9 @@ hipError_t gemm_run(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, i
     a.ttiles = (unsigned)((n + kToks - 1) / kToks);
     a.parts = gemm_parts(a.rtiles * a.ttiles, (unsigned)(w->cols / 256));
     if (a.parts > 1) {
-        const size_t need_parts = (size_t)a.parts * n * w->rows;
-        if (dev->gemm_parts_cap < need_parts) {
-            if (dev->gemm_parts) hipFree(dev->gemm_parts);
-            dev->gemm_parts = nullptr;
-            dev->gemm_parts_cap = 0;
-            e = hipMalloc(&dev->gemm_parts, need_parts * sizeof(float));
-            if (e != hipSuccess) return e;
-            dev->gemm_parts_cap = need_parts;
-        }
+        e = dev_grow(dev, (void **)&dev->gemm_parts, &dev->gemm_parts_cap, (size_t)a.parts * n * w->rows,
+                     sizeof(float));
+        if (e != hipSuccess) return e;
         a.part_out = dev->gemm_parts;
     }
     a.grid = (a.rtiles * a.ttiles * a.parts + 7) / 8 * 8;

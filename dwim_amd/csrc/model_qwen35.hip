@@ -661,6 +661,151 @@ struct dwim_model {
         return 0;
     }
 
+    // LanguageModel::save (qwen35/mod.rs:905-947): the "dwimstat" layout of
+    // version 3, all little-endian: magic, version u32, then seven u64 (len,
+    // attention caches, linear slots, kv_dim, conv width, ssm width, hidden
+    // or 0 without a drafter); every key cache's first len·kv_dim activations
+    // as read_cache gives them, then every value cache's; per linear slot its
+    // conv state (the buffer the next batch reads) and its recurrent state as
+    // f32; with a drafter, the hidden state carried over.  `bytes` is 0 when
+    // there is no state to save (a batch being verified, or a drafter with
+    // nothing carried over), as the reference returns None.
+    size_t state_bytes(size_t len) const {
+        size_t b = 8 + 4 + 7 * 8 + 2 * caches * (len * kv_dim() + len * kv_dim() / 32 * 2);
+        b += slots * (conv_width() + ssm_width()) * 4;
+        if (has_draft) b += c.hidden * 4;
+        return b;
+    }
+    int save(size_t len, uint8_t *out, size_t cap, size_t *bytes) {
+        *bytes = 0;
+        if (!seq.verified.empty() || (has_draft && !seq.carry)) return 0;
+        if (len > seq.max_len || (len * kv_dim()) % 32 != 0)
+            return dwim_fail("save: " + std::to_string(len) + " positions do not fit the context");
+        const size_t need = state_bytes(len);
+        if (!out) {
+            *bytes = need;
+            return 0;
+        }
+        if (cap < need) return dwim_fail("save: a buffer of " + std::to_string(cap) + " bytes can't hold " +
+                                         std::to_string(need));
+        uint8_t *p = out;
+        memcpy(p, "dwimstat", 8);
+        p += 8;
+        const uint32_t version = 3;
+        memcpy(p, &version, 4);
+        p += 4;
+        const uint64_t header[7] = {len, caches, slots, kv_dim(), conv_width(), ssm_width(),
+                                    has_draft ? c.hidden : 0};
+        memcpy(p, header, sizeof header);
+        p += sizeof header;
+        const size_t cache_len = len * kv_dim(), cache_bytes = cache_len + cache_len / 32 * 2;
+        for (int kv = 0; kv < 2; kv++)
+            for (size_t i = 0; i < caches; i++) {
+                TRY(dwim_read_cache(dev, kv ? seq.v_cache[i] : seq.k_cache[i], cache_len, p));
+                p += cache_bytes;
+            }
+        for (size_t slot = 0; slot < slots; slot++) {
+            TRY(dwim_read(dev, seq.conv_state[slot][seq.parity ? 0 : 1], (float *)p, conv_width()));
+            p += conv_width() * 4;
+            TRY(dwim_read(dev, seq.ssm_state[slot], (float *)p, ssm_width()));
+            p += ssm_width() * 4;
+        }
+        if (has_draft) {
+            // the carried row, through xb (the first c.hidden of seq.hidden)
+            TRY(dwim_resize(dev, xb, c.hidden));
+            TRY(dwim_copy(dev, xb, 0, seq.hidden, 0, c.hidden));
+            TRY(dwim_read(dev, xb, (float *)p, c.hidden));
+            p += c.hidden * 4;
+        }
+        *bytes = (size_t)(p - out);
+        return 0;
+    }
+
+    // LanguageModel::restore (qwen35/mod.rs:949-1017), with its checks and
+    // messages; the conv state goes to the first buffer of each pair, read
+    // next with the parity set.
+    int restore(const uint8_t *state, size_t bytes, size_t *len_out) {
+        size_t at = 0;
+        auto take = [&](size_t n, const uint8_t **ptr) -> int {
+            if (at + n > bytes) return dwim_fail("the saved state is cut short");
+            *ptr = state + at;
+            at += n;
+            return 0;
+        };
+        const uint8_t *ptr;
+        TRY(take(8, &ptr));
+        if (memcmp(ptr, "dwimstat", 8) != 0) return dwim_fail("not a saved state");
+        TRY(take(4, &ptr));
+        uint32_t version;
+        memcpy(&version, ptr, 4);
+        if (version != 3) return dwim_fail("a saved state of another version");
+        uint64_t header[7];
+        TRY(take(sizeof header, &ptr));
+        memcpy(header, ptr, sizeof header);
+        const uint64_t want[6] = {caches, slots, kv_dim(), conv_width(), ssm_width(), has_draft ? c.hidden : 0};
+        if (memcmp(header + 1, want, sizeof want) != 0) return dwim_fail("a saved state of another model");
+        const size_t len = header[0];
+        if (len > seq.max_len)
+            return dwim_fail("a saved state of " + std::to_string(len) + " tokens does not fit in the context");
+        if ((len * kv_dim()) % 32 != 0) return dwim_fail("a saved state of another model");
+        // every section is checked for length before any is written
+        const size_t cache_len = len * kv_dim(), cache_bytes = cache_len + cache_len / 32 * 2;
+        const size_t need = 2 * caches * cache_bytes + slots * (conv_width() + ssm_width()) * 4 +
+                            (has_draft ? c.hidden * 4 : 0);
+        if (bytes - at < need) return dwim_fail("the saved state is cut short");
+        for (int kv = 0; kv < 2; kv++)
+            for (size_t i = 0; i < caches; i++) {
+                TRY(take(cache_bytes, &ptr));
+                TRY(dwim_write_cache(dev, kv ? seq.v_cache[i] : seq.k_cache[i], ptr, cache_bytes));
+            }
+        for (size_t slot = 0; slot < slots; slot++) {
+            TRY(take(conv_width() * 4, &ptr));
+            TRY(dwim_write(dev, seq.conv_state[slot][0], (const float *)ptr, conv_width()));
+            TRY(take(ssm_width() * 4, &ptr));
+            TRY(dwim_write(dev, seq.ssm_state[slot], (const float *)ptr, ssm_width()));
+        }
+        seq.parity = true;
+        seq.verified.clear();
+        if (marked == (long)seq.id) marked = -1;
+        if (has_draft) {
+            TRY(take(c.hidden * 4, &ptr));
+            TRY(dwim_resize(dev, xb, c.hidden));
+            TRY(dwim_write(dev, xb, (const float *)ptr, c.hidden));
+            TRY(dwim_copy(dev, seq.hidden, 0, xb, 0, c.hidden));
+            seq.carry = true;
+        }
+        *len_out = len;
+        return dwim_sync(dev);
+    }
+
+    // Every device scratch buffer a forward pass can grow, at its largest for
+    // this model, now: a forward pass then never frees and allocates (which
+    // would wait for the device) in the middle of its launches.
+    int reserve(size_t max_len, int fmt) {
+        const size_t small = std::min(most, (size_t)15);  // the decode attention's most tokens
+        DWIM_HIP(attention_reserve(
+            dev, attention_partials_floats(small, max_len > small ? max_len - small : 0, c.heads, c.head_dim)));
+        DWIM_HIP(delta_net_reserve(dev, most, c.v_heads));
+        if (fmt == DWIM_Q4_K) {
+            const size_t H = c.hidden, I = c.intermediate;
+            const size_t shapes[][2] = {{q_dim(), H}, {kv_dim(), H}, {H, q_dim()}, {2 * k_dim() + v_dim(), H},
+                                        {v_dim(), H}, {H, v_dim()}, {I, H}, {H, I}, {H, H}};
+            size_t split = 0, parts = 0, cols_max = 0;
+            for (auto &rc : shapes) {
+                cols_max = std::max(cols_max, rc[1]);
+                for (size_t n = 16; n <= most; n++) {
+                    split = std::max(split, gemm_split_bytes(n, rc[1]));
+                    parts = std::max(parts, gemm_parts_floats(n, rc[0], rc[1]));
+                }
+            }
+            DWIM_HIP(gemm_reserve(dev, split, parts));
+            if (!dev_work(dev, most * cols_max)) return dwim_fail("reserving the normalized activations failed");
+        }
+        DWIM_HIP(dev_grow(dev, (void **)&dev->tokens, &dev->tokens_cap, most, 4));
+        DWIM_HIP(dev_grow(dev, (void **)&dev->argmax_buf, &dev->argmax_cap, argmax_scratch_words(kMaxDrafts + 1), 4));
+        return 0;
+    }
+
     // LanguageModel::reset (qwen35/mod.rs:1230-1246)
     int reset() {
         std::vector<float> zeros(std::max(conv_width(), ssm_width()), 0.0f);
@@ -765,6 +910,7 @@ extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg
     }
     if (m->buf(c.hidden, &m->mark_hidden)) return 1;
     if (m->new_sequence(m->seq, 0, max_len)) return 1;
+    if (m->reserve(max_len, body_format)) return 1;
     if (dwim_sync(dev)) return 1;
     *out = m.release();
     return 0;
@@ -804,3 +950,11 @@ extern "C" int dwim_model_rewind_to_mark(dwim_model *m) { return m->rewind_to_ma
 extern "C" int dwim_model_add_sequence(dwim_model *m, size_t *id) { return m->add_sequence(id); }
 
 extern "C" int dwim_model_select_sequence(dwim_model *m, size_t id) { return m->select_sequence(id); }
+
+extern "C" int dwim_model_save(dwim_model *m, size_t len, uint8_t *out, size_t cap, size_t *bytes) {
+    return m->save(len, out, cap, bytes);
+}
+
+extern "C" int dwim_model_restore(dwim_model *m, const uint8_t *state, size_t bytes, size_t *len) {
+    return m->restore(state, bytes, len);
+}

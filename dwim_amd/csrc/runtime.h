@@ -199,6 +199,18 @@ hipError_t launch_qk_prep(hipStream_t s, float *q, float *k, const float *v, con
                           size_t kv_heads, size_t head_dim, size_t rot, float eps, dwim_cache *kc, dwim_cache *vc);
 // attention, then out *= sigmoid(gate) when gate is given, and (one token,
 // area >= 0) out's planes into that plane area
+// Grows a device scratch buffer (cap in elements of `elem` bytes) to `need`,
+// after whatever is queued; a model reserves each buffer's largest size when
+// it is built, so that no forward pass allocates.
+hipError_t dev_grow(dwim_dev *dev, void **ptr, size_t *cap, size_t need, size_t elem);
+size_t delta_net_work_floats(size_t n, size_t n_v_heads);
+hipError_t delta_net_reserve(dwim_dev *dev, size_t n, size_t n_v_heads);
+size_t gemm_split_bytes(size_t n, size_t cols);
+size_t argmax_scratch_words(size_t rows);
+size_t gemm_parts_floats(size_t n, size_t rows, size_t cols);
+hipError_t gemm_reserve(dwim_dev *dev, size_t split_bytes, size_t parts_floats);
+size_t attention_partials_floats(size_t n, size_t pos, size_t n_heads, size_t head_dim);
+hipError_t attention_reserve(dwim_dev *dev, size_t floats);
 hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                                   const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
                                   size_t n_kv_heads, const float *gate, int area);

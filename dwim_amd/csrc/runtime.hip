@@ -69,14 +69,27 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
     return 0;
 }
 
-float *dev_work(dwim_dev *dev, size_t floats) {
-    if (dev->work_cap < floats) {
-        if (dev->work) hipFree(dev->work);
-        dev->work = nullptr;
-        dev->work_cap = 0;
-        if (hipMalloc(&dev->work, floats * sizeof(float)) != hipSuccess) return nullptr;
-        dev->work_cap = floats;
+hipError_t dev_grow(dwim_dev *dev, void **ptr, size_t *cap, size_t need, size_t elem) {
+    if (*cap >= need) return hipSuccess;
+    if (*ptr) {
+        // whatever is queued may still read the old buffer
+        hipError_t e = hipStreamSynchronize(dev->stream);
+        if (e != hipSuccess) return e;
+        hipFree(*ptr);
     }
+    *ptr = nullptr;
+    *cap = 0;
+    hipError_t e = hipMalloc(ptr, need * elem);
+    if (e != hipSuccess) {
+        *ptr = nullptr;
+        return e;
+    }
+    *cap = need;
+    return hipSuccess;
+}
+
+float *dev_work(dwim_dev *dev, size_t floats) {
+    if (dev_grow(dev, (void **)&dev->work, &dev->work_cap, floats, sizeof(float)) != hipSuccess) return nullptr;
     return dev->work;
 }
 
@@ -171,8 +184,12 @@ extern "C" int dwim_alloc_cache(dwim_dev *dev, size_t len, dwim_cache **out) {
         hipFree(q);
         return dwim_fail("allocating a cache failed");
     }
-    hipMemsetAsync(q, 0, std::max<size_t>(len, 32), dev->stream);
-    hipMemsetAsync(s, 0, std::max<size_t>(len / 32, 1) * 2, dev->stream);
+    if (hipMemsetAsync(q, 0, std::max<size_t>(len, 32), dev->stream) != hipSuccess ||
+        hipMemsetAsync(s, 0, std::max<size_t>(len / 32, 1) * 2, dev->stream) != hipSuccess) {
+        hipFree(q);
+        hipFree(s);
+        return dwim_fail("clearing a new cache failed");
+    }
     dev->refs++;
     *out = new dwim_cache{dev, q, s, len};
     return 0;
@@ -545,14 +562,7 @@ extern "C" int dwim_embed(dwim_dev *dev, dwim_buf *out, const dwim_weight *table
             return dwim_fail("embed: token " + std::to_string(tokens[i]) + " is past the table's " +
                              std::to_string(table->rows) + " rows");
     if (n == 0) return 0;
-    if (dev->tokens_cap < n) {
-        DWIM_HIP(hipStreamSynchronize(dev->stream));
-        if (dev->tokens) hipFree(dev->tokens);
-        dev->tokens = nullptr;
-        dev->tokens_cap = 0;
-        DWIM_HIP(hipMalloc(&dev->tokens, n * 4));
-        dev->tokens_cap = n;
-    }
+    DWIM_HIP(dev_grow(dev, (void **)&dev->tokens, &dev->tokens_cap, n, 4));
     // the ids go through the stream, after whatever still reads the previous ones
     DWIM_HIP(hipMemcpyAsync(dev->tokens, tokens, n * 4, hipMemcpyHostToDevice, dev->stream));
     DWIM_HIP(hipStreamSynchronize(dev->stream));
@@ -562,13 +572,7 @@ extern "C" int dwim_embed(dwim_dev *dev, dwim_buf *out, const dwim_weight *table
 
 extern "C" int dwim_argmax(dwim_dev *dev, const dwim_buf *logits, size_t rows, uint32_t *out) {
     DWIM_CHECK(rows > 0 && logits->len % rows == 0, "argmax: logits are not whole rows");
-    if (dev->argmax_cap < rows) {
-        if (dev->argmax_buf) hipFree(dev->argmax_buf);
-        dev->argmax_buf = nullptr;
-        dev->argmax_cap = 0;
-        DWIM_HIP(hipMalloc(&dev->argmax_buf, argmax_scratch_words(rows) * 4));
-        dev->argmax_cap = rows;
-    }
+    DWIM_HIP(dev_grow(dev, (void **)&dev->argmax_buf, &dev->argmax_cap, argmax_scratch_words(rows), 4));
     LAUNCH(launch_argmax(dev->stream, logits->data, rows, logits->len / rows, dev->argmax_buf));
     DWIM_HIP(hipMemcpyAsync(out, dev->argmax_buf, rows * 4, hipMemcpyDeviceToHost, dev->stream));
     DWIM_HIP(hipStreamSynchronize(dev->stream));

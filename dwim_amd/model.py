@@ -79,13 +79,17 @@ def _declare(L):
     L.dwim_model_add_sequence.argtypes = [vp, ctypes.POINTER(sz)]
     L.dwim_model_select_sequence.restype = ctypes.c_int
     L.dwim_model_select_sequence.argtypes = [vp, sz]
+    L.dwim_model_save.restype = ctypes.c_int
+    L.dwim_model_save.argtypes = [vp, sz, ctypes.c_void_p, sz, ctypes.POINTER(sz)]
+    L.dwim_model_restore.restype = ctypes.c_int
+    L.dwim_model_restore.argtypes = [vp, ctypes.c_char_p, sz, ctypes.POINTER(sz)]
     _sigs_done = True
 
 
 MODEL_SIGNATURES = ["dwim_model_synthetic", "dwim_model_free", "dwim_model_batch", "dwim_model_forward",
                     "dwim_model_forward_greedy", "dwim_model_reset", "dwim_model_draft", "dwim_model_verify",
                     "dwim_model_rewind", "dwim_model_mark", "dwim_model_rewind_to_mark", "dwim_model_add_sequence",
-                    "dwim_model_select_sequence"]
+                    "dwim_model_select_sequence", "dwim_model_save", "dwim_model_restore"]
 
 
 class Model:
@@ -158,6 +162,25 @@ class Model:
 
     def select_sequence(self, seq: int):
         D._check(self.L.dwim_model_select_sequence(self.h, seq))
+
+    def save(self, length: int) -> bytes | None:
+        """LanguageModel::save (qwen35/mod.rs:905-947): the state after
+        `length` positions as "dwimstat" v3 bytes, or None when there is
+        none to save."""
+        n = ctypes.c_size_t()
+        D._check(self.L.dwim_model_save(self.h, length, None, 0, ctypes.byref(n)))
+        if n.value == 0:
+            return None
+        out = ctypes.create_string_buffer(n.value)
+        D._check(self.L.dwim_model_save(self.h, length, out, n.value, ctypes.byref(n)))
+        return out.raw[:n.value]
+
+    def restore(self, state: bytes) -> int:
+        """LanguageModel::restore (qwen35/mod.rs:949-1017): the positions the
+        state holds; raises on another layout, version or model."""
+        n = ctypes.c_size_t()
+        D._check(self.L.dwim_model_restore(self.h, state, len(state), ctypes.byref(n)))
+        return n.value
 
     def close(self):
         if getattr(self, "h", None):

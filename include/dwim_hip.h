@@ -230,6 +230,18 @@ int dwim_model_rewind_to_mark(dwim_model *m);
  * switch of the running sequence (nothing copied; error while verifying). */
 int dwim_model_add_sequence(dwim_model *m, size_t *id);
 int dwim_model_select_sequence(dwim_model *m, size_t id);
+/* LanguageModel::save (inference/qwen35/mod.rs:905-947): the state after `len`
+ * positions in the reference's "dwimstat" layout, version 3 (header; each key
+ * cache then each value cache as read_cache gives it; per linear layer its conv
+ * and recurrent state as f32; the drafter's carried hidden state).  With
+ * `out` null, *bytes is the size needed; else up to `cap` bytes are written.
+ * *bytes = 0 means no state to save (the reference's None): a batch is being
+ * verified, or a drafter has nothing carried over. */
+int dwim_model_save(dwim_model *m, size_t len, uint8_t *out, size_t cap, size_t *bytes);
+/* LanguageModel::restore (inference/qwen35/mod.rs:949-1017): the current
+ * sequence from a saved state; *len = its positions.  Fails with the
+ * reference's messages on another layout, version or model. */
+int dwim_model_restore(dwim_model *m, const uint8_t *state, size_t bytes, size_t *len);
 
 /* Host-side quantizers, the product's own (gpu/quant.rs restated for the host
  * loader, plus the K formats).  `x` holds `cols` weights. */

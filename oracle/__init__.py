@@ -466,6 +466,10 @@ def _declare_model(L):
     L.or_model_reset.restype = None
     L.or_model_reset.argtypes = [vp]
     L.or_model_zero_residual_writes.restype = None
+    L.or_model_save.restype = _sz
+    L.or_model_save.argtypes = [vp, _sz, ctypes.c_void_p]
+    L.or_model_restore.restype = ctypes.c_int
+    L.or_model_restore.argtypes = [vp, ctypes.c_char_p, _sz, ctypes.POINTER(_sz)]
     L.or_model_zero_residual_writes.argtypes = [vp]
     L.or_model_verify.restype = None
     L.or_model_verify.argtypes = [vp, u32p, _sz, _sz, _f32p]
@@ -531,6 +535,26 @@ class Model:
 
     def reset(self):
         self.L.or_model_reset(self.h)
+
+    RESTORE_ERRORS = {1: "the saved state is cut short", 2: "not a saved state",
+                      3: "a saved state of another version", 4: "a saved state of another model",
+                      5: "does not fit in the context"}
+
+    def save(self, length):
+        """LanguageModel::save: the dwimstat v3 bytes, or None."""
+        n = self.L.or_model_save(self.h, length, None)
+        if n == 0:
+            return None
+        out = ctypes.create_string_buffer(n)
+        self.L.or_model_save(self.h, length, out)
+        return out.raw
+
+    def restore(self, state: bytes) -> int:
+        n = _sz()
+        err = self.L.or_model_restore(self.h, state, len(state), ctypes.byref(n))
+        if err:
+            raise ValueError(self.RESTORE_ERRORS[err])
+        return n.value
 
     def zero_residual_writes(self):
         """Test hook: every ffn_down, attn_output and ssm_out becomes zero."""

@@ -601,3 +601,84 @@ void or_model_zero_residual_writes(or_model *m) {
         zero_weight(l->attention ? &l->o : &l->out);
     }
 }
+
+/* LanguageModel::save (qwen35/mod.rs:905-947), "dwimstat" version 3.  Returns
+ * the bytes written (or needed, with out null); 0 for the reference's None. */
+size_t or_model_save(or_model *m, size_t len, uint8_t *out) {
+    if (m->n_verified || (m->has_draft && !m->carry)) return 0;
+    size_t kvd = kv_dim(m), cl = len * kvd, cb = cl + cl / 32 * 2;
+    size_t need = 8 + 4 + 56 + 2 * m->caches * cb + m->slots * (conv_width(m) + ssm_width(m)) * 4 +
+                  (m->has_draft ? m->c.hidden * 4 : 0);
+    if (!out) return need;
+    uint8_t *p = out;
+    memcpy(p, "dwimstat", 8);
+    p += 8;
+    uint32_t version = 3;
+    memcpy(p, &version, 4);
+    p += 4;
+    uint64_t header[7] = {len, m->caches, m->slots, kvd, conv_width(m), ssm_width(m), m->has_draft ? m->c.hidden : 0};
+    memcpy(p, header, sizeof header);
+    p += sizeof header;
+    for (int kv = 0; kv < 2; kv++)
+        for (size_t i = 0; i < m->caches; i++) {
+            memcpy(p, kv ? m->vq[i] : m->kq[i], cl);
+            memcpy(p + cl, kv ? m->vs[i] : m->ks[i], cl / 32 * 2);
+            p += cb;
+        }
+    for (size_t i = 0; i < m->slots; i++) {
+        memcpy(p, m->conv_state[m->parity ? 0 : 1][i], conv_width(m) * 4);
+        p += conv_width(m) * 4;
+        memcpy(p, m->ssm_state[i], ssm_width(m) * 4);
+        p += ssm_width(m) * 4;
+    }
+    if (m->has_draft) {
+        memcpy(p, m->hidden, m->c.hidden * 4);
+        p += m->c.hidden * 4;
+    }
+    return (size_t)(p - out);
+}
+
+/* LanguageModel::restore (qwen35/mod.rs:949-1017): returns 0 and *len, or an
+ * error code: 1 cut short, 2 not a state, 3 another version, 4 another model,
+ * 5 too long for the context. */
+int or_model_restore(or_model *m, const uint8_t *state, size_t bytes, size_t *len) {
+    if (bytes < 8) return 1;
+    if (memcmp(state, "dwimstat", 8) != 0) return 2;
+    if (bytes < 12) return 1;
+    uint32_t version;
+    memcpy(&version, state + 8, 4);
+    if (version != 3) return 3;
+    if (bytes < 68) return 1;
+    uint64_t header[7];
+    memcpy(header, state + 12, sizeof header);
+    uint64_t want[6] = {m->caches, m->slots, kv_dim(m), conv_width(m), ssm_width(m), m->has_draft ? m->c.hidden : 0};
+    if (memcmp(header + 1, want, sizeof want) != 0) return 4;
+    size_t n = header[0];
+    if (n > m->max_len) return 5;
+    size_t cl = n * kv_dim(m), cb = cl + cl / 32 * 2;
+    size_t need = 68 + 2 * m->caches * cb + m->slots * (conv_width(m) + ssm_width(m)) * 4 +
+                  (m->has_draft ? m->c.hidden * 4 : 0);
+    if (bytes < need) return 1;
+    const uint8_t *p = state + 68;
+    for (int kv = 0; kv < 2; kv++)
+        for (size_t i = 0; i < m->caches; i++) {
+            memcpy(kv ? m->vq[i] : m->kq[i], p, cl);
+            memcpy(kv ? m->vs[i] : m->ks[i], p + cl, cl / 32 * 2);
+            p += cb;
+        }
+    for (size_t i = 0; i < m->slots; i++) {
+        memcpy(m->conv_state[0][i], p, conv_width(m) * 4);
+        p += conv_width(m) * 4;
+        memcpy(m->ssm_state[i], p, ssm_width(m) * 4);
+        p += ssm_width(m) * 4;
+    }
+    m->parity = 1;
+    m->n_verified = 0;
+    m->marked = 0;
+    if (m->has_draft) {
+        memcpy(m->hidden, p, m->c.hidden * 4);
+        m->carry = 1;
+    }
+    *len = n;
+    return 0;
+}

@@ -125,6 +125,8 @@ void or_model_mark(or_model *m);
 int or_model_rewind_to_mark(or_model *m);
 void or_model_reset(or_model *m);
 void or_model_zero_residual_writes(or_model *m);
+size_t or_model_save(or_model *m, size_t len, uint8_t *out);
+int or_model_restore(or_model *m, const uint8_t *state, size_t bytes, size_t *len);
 
 #ifdef __cplusplus
 }
