@@ -614,3 +614,52 @@ hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, con
     }
     return attention_run(dev, dev->partials, out, q, k, v, n, pos, n_heads, head_dim, n_kv_heads, gate, pv);
 }
+
+// ---------------------------------------------------------------- without allocating
+//
+// dwim_attention_noalloc keeps the decode path's partial results in this
+// file-scope array instead of the device's grown buffer.  Every GPU holds its
+// own copy of it (64 MiB) until the process ends; its address on a device is
+// taken once, when the device is opened (attention_scratch_init), and used
+// wherever host code needs the array.  Calls on one GPU share it, so calls
+// that overlap on one device race.  Nothing in it needs to start at zero:
+// each chunk's partial row is written before the combine reads it.
+namespace {
+constexpr size_t kScratchFloats = (size_t)16 << 20;
+__device__ __align__(256) float scratch[kScratchFloats];
+}  // namespace
+
+hipError_t attention_scratch_init(dwim_dev *dev) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    dev->attn_scratch = (float *)ptr;
+    return hipSuccess;
+}
+
+extern "C" int dwim_attention_noalloc(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_cache *k_cache,
+                                      const dwim_cache *v_cache, size_t pos, size_t n_heads, size_t head_dim,
+                                      size_t n_kv_heads) {
+    DWIM_CHECK(head_dim % 32 == 0 && head_dim <= 256 && head_dim > 0,
+               "attention: heads are whole blocks of 32, at most 256");
+    DWIM_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8,
+               "attention: at most 8 query heads to a key/value head");
+    const size_t width = n_heads * head_dim;
+    DWIM_CHECK(q->len % width == 0 && out->len == q->len, "attention: q and out are whole tokens");
+    const size_t n = q->len / width, kv_dim = n_kv_heads * head_dim;
+    DWIM_CHECK((pos + n) * kv_dim <= k_cache->len && (pos + n) * kv_dim <= v_cache->len,
+               "attention: the caches do not hold the tokens' positions");
+    DWIM_CHECK(dev->attn_scratch != nullptr, "attention_noalloc: the device's scratch array has no address");
+    if (n == 0) return 0;
+    const bool batch = n >= 16 && head_dim == (size_t)kFD;
+    if (!batch) {
+        const size_t need = attention_partials_floats(n, pos, n_heads, head_dim);
+        DWIM_CHECK(need <= kScratchFloats,
+                   "attention_noalloc: " + std::to_string(n) + " tokens at position " + std::to_string(pos) +
+                       " need " + std::to_string(need * 4) + " bytes of partial results, more than the " +
+                       std::to_string(kScratchFloats * 4) + " bytes of its scratch array");
+    }
+    DWIM_HIP(attention_run(dev, dev->attn_scratch, out->data, q->data, k_cache, v_cache, n, pos, n_heads, head_dim,
+                           n_kv_heads, nullptr, planes::View{}));
+    return 0;
+}

@@ -20,6 +20,9 @@ struct dwim_dev {
     // results.  Grown on demand, freed with the device.
     float *partials = nullptr;
     size_t partials_cap = 0;  // floats
+    // the address on this device of k_attention.hip's file-scope scratch
+    // array (dwim_attention_noalloc), taken when the device is opened
+    float *attn_scratch = nullptr;
     uint32_t *argmax_buf = nullptr;
     size_t argmax_cap = 0;
     uint32_t *tokens = nullptr;  // token ids for the embedding lookup
@@ -211,6 +214,7 @@ size_t gemm_parts_floats(size_t n, size_t rows, size_t cols);
 hipError_t gemm_reserve(dwim_dev *dev, size_t split_bytes, size_t parts_floats);
 size_t attention_partials_floats(size_t n, size_t pos, size_t n_heads, size_t head_dim);
 hipError_t attention_reserve(dwim_dev *dev, size_t floats);
+hipError_t attention_scratch_init(dwim_dev *dev);
 hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                                   const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
                                   size_t n_kv_heads, const float *gate, int area);

@@ -65,6 +65,12 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
         dwim_dev_release_resources(dev);
         return dwim_fail("allocating the split-product scratch failed");
     }
+    // the address of the scratch array dwim_attention_noalloc uses, on this device
+    if (attention_scratch_init(dev) != hipSuccess) {
+        dev->refs = 0;
+        dwim_dev_release_resources(dev);
+        return dwim_fail("taking the address of the attention scratch array failed");
+    }
     *out = dev;
     return 0;
 }

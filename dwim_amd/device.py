@@ -73,6 +73,7 @@ SIGNATURES = {
     "dwim_l2norm": (_int, [_vp, _vp, _sz, ctypes.c_float]),
     "dwim_rope": (_int, [_vp, _vp, _vp, _sz, _sz, _sz, _sz]),
     "dwim_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz]),
+    "dwim_attention_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz]),
     "dwim_silu_mul": (_int, [_vp, _vp, _vp]),
     "dwim_sigmoid_mul": (_int, [_vp, _vp, _vp]),
     "dwim_conv": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -379,6 +380,12 @@ class Hip:
     def attention(self, out: Buffer, q: Buffer, k: Cache, v: Cache, pos: int, n_heads: int, head_dim: int,
                   n_kv_heads: int):
         _check(self.L.dwim_attention(self.h, out.h, q.h, k.h, v.h, pos, n_heads, head_dim, n_kv_heads))
+
+    def attention_noalloc(self, out: Buffer, q: Buffer, k: Cache, v: Cache, pos: int, n_heads: int,
+                          head_dim: int, n_kv_heads: int):
+        """dwim_attention without allocating: the partial results in the
+        library's fixed per-GPU scratch array (no counterpart in the reference)."""
+        _check(self.L.dwim_attention_noalloc(self.h, out.h, q.h, k.h, v.h, pos, n_heads, head_dim, n_kv_heads))
 
     def silu_mul(self, gate: Buffer, up: Buffer):
         _check(self.L.dwim_silu_mul(self.h, gate.h, up.h))

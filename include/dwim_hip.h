@@ -131,6 +131,18 @@ int dwim_rope(dwim_dev *dev, dwim_buf *x, const dwim_buf *table, size_t pos, siz
 int dwim_attention(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_cache *k_cache,
                    const dwim_cache *v_cache, size_t pos, size_t n_heads, size_t head_dim,
                    size_t n_kv_heads);
+/* No counterpart in the reference: dwim_attention for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The same kernels and results as
+ * dwim_attention, but the decode path's partial results live in a file-scope
+ * device array of 64 MiB per GPU (held until the process ends) instead of a
+ * buffer the library grows: no hipMalloc or hipFree is called.  Fails with a
+ * clear error when n·n_heads·ceil((pos + n)/64)·(head_dim + 2) floats exceed
+ * it (one token of 24 heads of 256 reaches past 170 000 positions).  Calls
+ * that overlap on one GPU share the array and race. */
+int dwim_attention_noalloc(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_cache *k_cache,
+                           const dwim_cache *v_cache, size_t pos, size_t n_heads, size_t head_dim,
+                           size_t n_kv_heads);
 /* gate = silu(gate) * up */
 int dwim_silu_mul(dwim_dev *dev, dwim_buf *gate, const dwim_buf *up);
 /* x *= sigmoid(gate) */
