@@ -530,8 +530,8 @@ hipError_t delta_net_reserve(dwim_dev *dev, size_t n, size_t n_v_heads) {
 
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k, const float *v,
                             const float *gates, const float *decay, float *state, size_t n, size_t n_k_heads,
-                            size_t n_v_heads, size_t head_dim, const Rms *rms) {
-    if (n >= (size_t)kC && !(rms && rms->ss)) {
+                            size_t n_v_heads, size_t head_dim, const Rms *rms, bool unit_keys) {
+    if (unit_keys && n >= (size_t)kC && !(rms && rms->ss)) {
         const size_t nch = (n + kC - 1) / kC;
         hipError_t e = delta_net_reserve(dev, n, n_v_heads);
         if (e != hipSuccess) return e;

@@ -399,9 +399,8 @@ struct dwim_model {
                 TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
                 TRY(dwim_matmul(dev, ab, l.ab, xh));
                 if (verify) TRY(save_inputs(l.slot, n));
-                DWIM_HIP(launch_conv_l2(dev->stream, q->data, k->data, v->data, state_out->data, qkv->data,
-                                        state->data, l.conv->data, n, k_dim(), k_dim(), v_dim(), c.state_dim, eps));
-                TRY(dwim_delta_net(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads, c.state_dim));
+                TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv, state, l.conv, c.state_dim, eps));
+                TRY(dwim_delta_net_unit_keys(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads, c.state_dim));
                 DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps, -1));
                 TRY(dwim_matmul_add(dev, x, l.out, z, xb));
             } else {

@@ -172,10 +172,12 @@ struct Rms {
     float cols = 1.0f;
     float eps = 0.0f;
 };
-// with rms, the gate logits (alpha, beta) are scaled by it first
+// with rms, the gate logits (alpha, beta) are scaled by it first; with
+// unit_keys (keys of unit length), 64 tokens and more take the chunked form
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k,
                             const float *v, const float *gates, const float *decay, float *state,
-                            size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim, const Rms *rms = nullptr);
+                            size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim, const Rms *rms = nullptr,
+                            bool unit_keys = false);
 hipError_t launch_embed(hipStream_t s, float *out, const dwim_weight *w, const uint32_t *tokens,
                         size_t n);
 // first index of each row's maximum, into the first `rows` words of scratch

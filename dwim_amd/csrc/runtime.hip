@@ -543,9 +543,9 @@ extern "C" int dwim_conv(dwim_dev *dev, dwim_buf *q, dwim_buf *k, dwim_buf *v, d
     return 0;
 }
 
-extern "C" int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_buf *k,
-                              const dwim_buf *v, const dwim_buf *gates, const dwim_buf *decay, dwim_buf *state,
-                              size_t n_k_heads, size_t n_v_heads, size_t head_dim) {
+static int delta_net_checked(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_buf *k, const dwim_buf *v,
+                             const dwim_buf *gates, const dwim_buf *decay, dwim_buf *state, size_t n_k_heads,
+                             size_t n_v_heads, size_t head_dim, bool unit_keys) {
     DWIM_CHECK(head_dim == 128, "delta_net: heads of 128");
     DWIM_CHECK(n_k_heads > 0 && n_v_heads % n_k_heads == 0, "delta_net: value heads a multiple of key heads");
     size_t n = v->len / (n_v_heads * head_dim);
@@ -556,7 +556,38 @@ extern "C" int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, c
     DWIM_CHECK(state->len == n_v_heads * head_dim * head_dim, "delta_net: the state");
     if (n)
         LAUNCH(launch_delta_net(dev, out->data, q->data, k->data, v->data, gates->data, decay->data,
-                                state->data, n, n_k_heads, n_v_heads, head_dim));
+                                state->data, n, n_k_heads, n_v_heads, head_dim, nullptr, unit_keys));
+    return 0;
+}
+
+extern "C" int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_buf *k,
+                              const dwim_buf *v, const dwim_buf *gates, const dwim_buf *decay, dwim_buf *state,
+                              size_t n_k_heads, size_t n_v_heads, size_t head_dim) {
+    return delta_net_checked(dev, out, q, k, v, gates, decay, state, n_k_heads, n_v_heads, head_dim, false);
+}
+
+extern "C" int dwim_delta_net_unit_keys(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_buf *k,
+                                        const dwim_buf *v, const dwim_buf *gates, const dwim_buf *decay,
+                                        dwim_buf *state, size_t n_k_heads, size_t n_v_heads, size_t head_dim) {
+    return delta_net_checked(dev, out, q, k, v, gates, decay, state, n_k_heads, n_v_heads, head_dim, true);
+}
+
+extern "C" int dwim_conv_l2norm(dwim_dev *dev, dwim_buf *q, dwim_buf *k, dwim_buf *v, dwim_buf *state_out,
+                                const dwim_buf *x, const dwim_buf *state, const dwim_buf *weight, size_t dim,
+                                float eps) {
+    DWIM_CHECK(weight->len % 4 == 0 && weight->len > 0, "conv: 4 taps per channel");
+    size_t ch = weight->len / 4;
+    size_t n = x->len / ch;
+    DWIM_CHECK(n * ch == x->len && n > 0, "conv: x is not whole rows of channels");
+    DWIM_CHECK(state->len == 3 * ch && state_out->len == state->len, "conv: states are 3 rows of channels");
+    size_t qd = q->len / n, kd = k->len / n, vd = v->len / n;
+    DWIM_CHECK(qd * n == q->len && kd * n == k->len && vd * n == v->len && qd + kd + vd == ch,
+               "conv: q, k and v do not split the channels");
+    DWIM_CHECK(state_out->data != state->data, "conv: state_out must be another buffer than state");
+    DWIM_CHECK(dim % 64 == 0 && dim > 0 && dim <= 256 && qd % dim == 0 && kd % dim == 0 && vd % dim == 0,
+               "conv_l2norm: rows of a multiple of 64 up to 256 that divide q, k and v");
+    LAUNCH(launch_conv_l2(dev->stream, q->data, k->data, v->data, state_out->data, x->data, state->data,
+                          weight->data, n, qd, kd, vd, dim, eps));
     return 0;
 }
 

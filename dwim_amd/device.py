@@ -78,6 +78,8 @@ SIGNATURES = {
     "dwim_sigmoid_mul": (_int, [_vp, _vp, _vp]),
     "dwim_conv": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "dwim_delta_net": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz]),
+    "dwim_delta_net_unit_keys": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz]),
+    "dwim_conv_l2norm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, ctypes.c_float]),
     "dwim_argmax": (_int, [_vp, _vp, _sz, _u32p]),
     "dwim_prepare": (_int, [_vp, _vp]),
     "dwim_matmul_prepared": (_int, [_vp, _vp, _vp]),
@@ -400,6 +402,17 @@ class Hip:
                   state: Buffer, n_k_heads: int, n_v_heads: int, head_dim: int):
         _check(self.L.dwim_delta_net(self.h, out.h, q.h, k.h, v.h, gates.h, decay.h, state.h,
                                      n_k_heads, n_v_heads, head_dim))
+
+    def delta_net_unit_keys(self, out: Buffer, q: Buffer, k: Buffer, v: Buffer, gates: Buffer, decay: Buffer,
+                            state: Buffer, n_k_heads: int, n_v_heads: int, head_dim: int):
+        """delta_net for unit keys: from 64 tokens on, the chunked form."""
+        _check(self.L.dwim_delta_net_unit_keys(self.h, out.h, q.h, k.h, v.h, gates.h, decay.h, state.h,
+                                               n_k_heads, n_v_heads, head_dim))
+
+    def conv_l2norm(self, q: Buffer, k: Buffer, v: Buffer, state_out: Buffer, x: Buffer, state: Buffer,
+                    weight: Buffer, dim: int, eps: float):
+        """conv, then l2norm of q and k in rows of `dim`, in one launch."""
+        _check(self.L.dwim_conv_l2norm(self.h, q.h, k.h, v.h, state_out.h, x.h, state.h, weight.h, dim, eps))
 
     def embed(self, out: Buffer, table: Weight, tokens):
         t = np.ascontiguousarray(tokens, np.uint32)

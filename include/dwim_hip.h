@@ -106,28 +106,30 @@ size_t dwim_cache_bytes(size_t len);
 
 /* ---- operations (gpu/mod.rs:251-400) ---- */
 
-/* out[t] = w · x[t] for each token row of x. */
+/* Device::matmul (gpu/mod.rs:254): out[t] = w · x[t] for each token row of x. */
 int dwim_matmul(dwim_dev *dev, dwim_buf *out, const dwim_weight *w, const dwim_buf *x);
-/* x += w · input (scratch as long as x, left undefined). */
+/* Device::matmul_add (gpu/mod.rs:259-268): x += w · input (scratch as long as x, left undefined). */
 int dwim_matmul_add(dwim_dev *dev, dwim_buf *x, const dwim_weight *w, const dwim_buf *input,
                     dwim_buf *scratch);
-/* out = silu(gate · x) * (up · x) (scratch as long as out, left undefined). */
+/* Device::swiglu (gpu/mod.rs:274-285): out = silu(gate · x) * (up · x) (scratch as long as out,
+ * left undefined). */
 int dwim_swiglu(dwim_dev *dev, dwim_buf *out, const dwim_weight *gate, const dwim_weight *up,
                 const dwim_buf *x, dwim_buf *scratch);
-/* x += y */
+/* Device::add (gpu/mod.rs:288): x += y */
 int dwim_add(dwim_dev *dev, dwim_buf *x, const dwim_buf *y);
-/* out = rmsnorm(x[..len]) * weight, rows of weight's length. */
+/* Device::normalize (gpu/mod.rs:295-305): out = rmsnorm(x[..len]) * weight, rows of weight's length. */
 int dwim_normalize(dwim_dev *dev, dwim_buf *out, const dwim_buf *x, const dwim_buf *weight,
                    size_t len, float eps);
-/* each weight-long row of x normalized by its root mean square, times weight. */
+/* Device::rmsnorm (gpu/mod.rs:309): each weight-long row of x normalized by its root mean square,
+ * times weight. */
 int dwim_rmsnorm(dwim_dev *dev, dwim_buf *x, const dwim_buf *weight, float eps);
-/* each dim-long row of x to unit length. */
+/* Device::l2norm (gpu/mod.rs:312): each dim-long row of x to unit length. */
 int dwim_l2norm(dwim_dev *dev, dwim_buf *x, size_t dim, float eps);
-/* rotary embeddings: pair (i, i + rot/2) of each head at position p rotated by
+/* Device::rope (gpu/mod.rs:321-336): rotary embeddings: pair (i, i + rot/2) of each head at position p rotated by
  * table[(p*rot/2 + i)*2 ..][..2] = (cos, sin); the first token at `pos`. */
 int dwim_rope(dwim_dev *dev, dwim_buf *x, const dwim_buf *table, size_t pos, size_t n_heads,
               size_t head_dim, size_t rot_dim);
-/* causal GQA over the caches, the first token at `pos`. */
+/* Device::attention (gpu/mod.rs:338-349): causal GQA over the caches, the first token at `pos`. */
 int dwim_attention(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_cache *k_cache,
                    const dwim_cache *v_cache, size_t pos, size_t n_heads, size_t head_dim,
                    size_t n_kv_heads);
@@ -143,19 +145,35 @@ int dwim_attention(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_c
 int dwim_attention_noalloc(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_cache *k_cache,
                            const dwim_cache *v_cache, size_t pos, size_t n_heads, size_t head_dim,
                            size_t n_kv_heads);
-/* gate = silu(gate) * up */
+/* Device::silu_mul (gpu/mod.rs:351): gate = silu(gate) * up */
 int dwim_silu_mul(dwim_dev *dev, dwim_buf *gate, const dwim_buf *up);
-/* x *= sigmoid(gate) */
+/* Device::sigmoid_mul (gpu/mod.rs:354): x *= sigmoid(gate) */
 int dwim_sigmoid_mul(dwim_dev *dev, dwim_buf *x, const dwim_buf *gate);
-/* the causal 4-tap convolution of linear attention, SiLU, split into q|k|v. */
+/* Device::conv (gpu/mod.rs:365-386): the causal 4-tap convolution of linear attention, SiLU,
+ * split into q|k|v. */
 int dwim_conv(dwim_dev *dev, dwim_buf *q, dwim_buf *k, dwim_buf *v, dwim_buf *state_out,
               const dwim_buf *x, const dwim_buf *state, const dwim_buf *weight);
-/* the gated delta rule, token after token, state [n_v_heads][head_dim][head_dim]. */
+/* Device::delta_net (gpu/mod.rs:388-400): the gated delta rule, token after token, state
+ * [n_v_heads][head_dim][head_dim]; any keys. */
 int dwim_delta_net(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_buf *k,
                    const dwim_buf *v, const dwim_buf *gates, const dwim_buf *decay,
                    dwim_buf *state, size_t n_k_heads, size_t n_v_heads, size_t head_dim);
 
 /* ---- beyond the trait ---- */
+
+/* Device::delta_net for keys of unit length, as qwen35's layer makes them
+ * (l2norm after the conv, inference/qwen35/mod.rs:612-617): from 64 tokens on,
+ * the chunked (WY) form on the fp32 matrix cores, whose triangular solve is
+ * well conditioned only for unit keys and decays below 1; fewer tokens, the
+ * token loop.  Other keys belong to dwim_delta_net. */
+int dwim_delta_net_unit_keys(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_buf *k,
+                             const dwim_buf *v, const dwim_buf *gates, const dwim_buf *decay,
+                             dwim_buf *state, size_t n_k_heads, size_t n_v_heads, size_t head_dim);
+/* Device::conv followed by Device::l2norm of q and of k, rows of `dim`, as
+ * qwen35's linear layer calls them (inference/qwen35/mod.rs:612-617), in one
+ * launch (16 tokens a block for batches); dim a multiple of 64, at most 256. */
+int dwim_conv_l2norm(dwim_dev *dev, dwim_buf *q, dwim_buf *k, dwim_buf *v, dwim_buf *state_out,
+                     const dwim_buf *x, const dwim_buf *state, const dwim_buf *weight, size_t dim, float eps);
 
 /* The greedy token of each of `rows` rows of logits: the first index of the
  * largest value (qwen35::argmax, inference/qwen35/mod.rs:702-710), on the

@@ -1,15 +1,17 @@
 """Parity at the shapes of the benchmark's configurations:
 
-* config 2, the gated-DeltaNet decode step: hidden 5120, 16 key heads and 48
-  value heads of 128, a causal conv of 4 over the q/k/v channels, fp32 state
-  48×128×128, Q4_K projections; 1024 consecutive one-token steps through the
-  model's fused decode path, the logits after each step against the oracle's
-  (the carried state is what they are computed from).  The layer's SwiGLU
-  width is cut to 1024, which the configuration does not specify, so that the
-  oracle runs the 1024 steps in seconds.
+* config 2, the gated-DeltaNet decode step, is in test_state.py (its carried
+  state, seeded N(0, 0.1), is read back through the saved state);
 * config 3, GQA attention over the Q8 cache: 24 query heads, 4 key/value
   heads of 256, decode at depths 4096, 32768 and 131072 for two sessions
   (separate caches), and a causal 2048-token prefill at depth 0.
+
+* config 5, the 27B shape with the MTP drafter: two sessions of
+  32768-token prompts sharing the weights; speculative decoding (3 drafts,
+  verified as a 4-token batch) yields exactly the plain greedy tokens
+  (qwen35/mod.rs:2100-2149, inference/local.rs:320-368), and verifying the
+  greedy continuation itself as the drafts commits whole batches (rewind with
+  keep = 4) and still yields them.
 
 Tolerances as the reference's device checks (gpu/tests.rs:132-140).
 """
@@ -26,23 +28,6 @@ pytestmark = pytest.mark.gpu
 def _err(got, want):
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     return float((np.abs(got - want) / (1 + np.abs(want))).max())
-
-
-def test_delta_net_decode_steps_carry_the_state():
-    cfg = M.config_27b(False)
-    cfg.layers, cfg.vocab, cfg.intermediate = 1, 256, 1024  # layer 0 is a DeltaNet layer
-    gpu = D.Hip(0)
-    g = M.Model(gpu, cfg, 77, max_len=1100)
-    o = O.Model(cfg.as_dict(), 77)
-    worst = 0.0
-    for step in range(1024):
-        token = (step * 37 + 11) % cfg.vocab
-        e = _err(g.forward([token], step), o.forward([token], step))
-        worst = max(worst, e)
-        if step + 1 in (1, 16, 256, 1024):
-            print(f"step {step + 1}: max err {e:.2e} (worst so far {worst:.2e})", flush=True)
-        assert e <= 2e-3, f"step {step + 1}: {e:.2e}"
-    g.close()
 
 
 @pytest.mark.parametrize("depth", [4096, 32768, 131072])
@@ -84,4 +69,67 @@ def test_attention_prefill_of_2048_tokens():
     e = _err(gpu.read(out), want)
     print(f"prefill 2048: max err {e:.2e}", flush=True)
     assert e <= 1e-4
+    gpu.close()
+
+
+def test_config5_speculative_decoding_equals_greedy_at_size():
+    cfg = M.config_27b(drafter=True)
+    prompt_len, tokens, k = 32768, 32, 3
+    gpu = D.Hip(0)
+    model = M.Model(gpu, cfg, seed=4321, max_len=prompt_len + 2 * tokens + 16)
+    rng = np.random.default_rng(55)
+    seqs = [0, model.add_sequence()]
+    firsts = []
+    for seq in seqs:  # both sessions prefilled first: their caches coexist
+        model.select_sequence(seq)
+        firsts.append(model.forward_greedy(rng.integers(0, cfg.vocab, prompt_len).astype(np.uint32), 0))
+    for seq, first in zip(seqs, firsts):
+        model.select_sequence(seq)
+        model.mark()
+        plain, token, pos = [], first, prompt_len
+        while len(plain) < tokens + k:
+            plain.append(token)
+            token = model.forward_greedy([token], pos)
+            pos += 1
+        # speculative, the drafter's own drafts (Local::step with a greedy sampler)
+        model.rewind_to_mark()
+        spec, token, pos, drafted = [], first, prompt_len, 0
+        while len(spec) < tokens:
+            spec.append(token)
+            drafts = model.draft(token, pos, k)
+            drafted += len(drafts)
+            _, picks = model.verify([token] + drafts, pos, want_logits=False)
+            keep = 1
+            for i, d in enumerate(drafts):
+                if picks[i] != d:
+                    break
+                spec.append(d)
+                keep += 1
+            model.rewind(keep)
+            pos += keep
+            token = picks[keep - 1]
+        print(f"session {seq}: {drafted} drafted, speculative == greedy: {spec[:tokens] == plain[:tokens]}",
+              flush=True)
+        assert spec[:tokens] == plain[:tokens]
+        # the greedy continuation verified as the drafts: every batch kept whole
+        model.rewind_to_mark()
+        got, token, pos, whole = [], first, prompt_len, 0
+        while len(got) < tokens:
+            got.append(token)
+            drafts = plain[len(got):len(got) + k]
+            _, picks = model.verify([token] + drafts, pos, want_logits=False)
+            keep = 1
+            for i, d in enumerate(drafts):
+                if picks[i] != d:
+                    break
+                got.append(d)
+                keep += 1
+            whole += keep == len(drafts) + 1
+            model.rewind(keep)
+            pos += keep
+            token = picks[keep - 1]
+        print(f"session {seq}: {whole} batches kept whole", flush=True)
+        assert got[:tokens] == plain[:tokens]
+        assert whole >= 7
+    model.close()
     gpu.close()

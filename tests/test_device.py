@@ -170,6 +170,24 @@ def test_q4_k_matvec_at_the_model_shapes(gpu, rows, cols):
     close(gpu.read(out)[::97], want, 1e-4)
 
 
+@pytest.mark.parametrize("rows,cols", [(17408, 5120), (5120, 17408)])
+def test_q4_k_gemm_at_the_prefill_batch(gpu, rows, cols):
+    """The batch product as the 4096-token prefill runs it (the f16 matrix-core
+    GEMM, k-split for the 5120-row product), on every 61st row and all 4096
+    tokens, against the oracle's dot of the same quantized rows: within the
+    batch tolerance of gpu/tests.rs:198-211 and 1e-4 of (1 + |y|) everywhere."""
+    n = 4096
+    w = gpu.upload_synthetic(D.Q4_K, rows, cols, seed=3, sigma=0.02)
+    x = D.synthetic_values(4, 0, n * cols, 1.0)
+    out = gpu.alloc(n * rows)
+    gpu.matmul(out, w, gpu.buffer(x))
+    got = gpu.read(out).reshape(n, rows)[:, ::61]
+    vals = np.stack([D.synthetic_values(3, r * cols, cols, 0.02) for r in range(0, rows, 61)])
+    want = O.matmul(O.Weight.quantized(O.Q4_K, vals), x).reshape(n, -1)
+    close_batch(got, want, f"{rows}x{cols} n={n}")
+    close(got, want, 1e-4)
+
+
 def test_q4_k_one_token_at_the_edges_of_its_activations(gpu):
     # one token runs on the int8 matrix cores with x held as 24-bit planes
     # scaled by max|x|: zeros, one outlier among tiny values, sign patterns
@@ -474,6 +492,46 @@ def test_conv_matches_cpu(gpu):
         close(gpu.read(so), ws, 1e-6)
 
 
+def test_conv_l2norm_matches_cpu(gpu):
+    """The model's fused conv + l2 norms (dwim_conv_l2norm): one token, a
+    batch under 16 tokens (a token a block), and 16-token blocks whole and
+    ragged, against the oracle's conv followed by its l2norm of q and k
+    (gpu/cpu.rs:250-296, :168-175), at the 27B shape's rows of 128."""
+    rng = O.Rng(15)
+    qd, kd, vd, dim = 256, 256, 768, 128
+    ch = qd + kd + vd
+    for n in (1, 15, 16, 37, 4096):
+        x = rng.floats(n * ch)
+        state = rng.floats(3 * ch)
+        w = rng.floats(ch * 4) * np.float32(0.5)
+        wq, wk, wv, ws = O.conv(x, state, w, qd, kd, vd)
+        wq, wk = O.l2norm(wq, dim, 1e-6), O.l2norm(wk, dim, 1e-6)
+        q, k, v, so = gpu.alloc(n * qd), gpu.alloc(n * kd), gpu.alloc(n * vd), gpu.alloc(3 * ch)
+        gpu.conv_l2norm(q, k, v, so, gpu.buffer(x), gpu.buffer(state), gpu.buffer(w), dim, 1e-6)
+        print(f"conv_l2norm n={n}", flush=True)
+        close(gpu.read(q), wq, 1e-5)
+        close(gpu.read(k), wk, 1e-5)
+        close(gpu.read(v), wv, 1e-5)
+        assert np.array_equal(gpu.read(so), ws)
+
+
+def test_delta_net_trait_op_keeps_the_token_loop_for_any_keys(gpu):
+    """Device::delta_net takes any keys (gpu/cpu.rs:298-363): 100 tokens of
+    keys that are not unit vectors, which the chunked form would not take,
+    agree with the oracle."""
+    rng = O.Rng(16)
+    nk, nv, n = 2, 6, 100
+    q, k, v, gates, decay, state = _delta_inputs(rng, n, nk, nv)
+    k = k * np.float32(0.3)
+    want, want_state = O.delta_net(q, k, v, gates, decay, state, nk, nv, 128)
+    out, st = gpu.alloc(v.size), gpu.buffer(state)
+    gpu.delta_net(out, gpu.buffer(q), gpu.buffer(k), gpu.buffer(v), gpu.buffer(gates), gpu.buffer(decay), st,
+                  nk, nv, 128)
+    scale = max(1.0, float(np.abs(want_state).max()))
+    assert np.abs(gpu.read(st) - want_state).max() <= 1e-4 * scale
+    assert np.abs(gpu.read(out) - want).max() <= 1e-4 * max(1.0, float(np.abs(want).max()))
+
+
 def _delta_inputs(rng, n, nk, nv, d=128):
     q, k = rng.floats(n * nk * d), rng.floats(n * nk * d)
     v = rng.floats(n * nv * d)
@@ -513,8 +571,8 @@ def test_delta_net_in_chunks_matches_cpu(gpu):
         want, want_state = O.delta_net(q, k, v, gates, decay, state, nk, nv, 128)
         out = gpu.alloc(v.size)
         st = gpu.buffer(state)
-        gpu.delta_net(out, gpu.buffer(q), gpu.buffer(k), gpu.buffer(v), gpu.buffer(gates), gpu.buffer(decay),
-                      st, nk, nv, 128)
+        gpu.delta_net_unit_keys(out, gpu.buffer(q), gpu.buffer(k), gpu.buffer(v), gpu.buffer(gates),
+                                gpu.buffer(decay), st, nk, nv, 128)
         print(f"heads {nk}/{nv}, {n} tokens", flush=True)
         close(gpu.read(out), want, 1e-4)
         close(gpu.read(st), want_state, 1e-4)
@@ -533,8 +591,8 @@ def test_delta_net_chunks_agree_with_the_token_loop_at_full_size(gpu):
         r /= np.sqrt((r.astype(np.float64) ** 2).sum(1, keepdims=True)).astype(np.float32)
     out = gpu.alloc(v.size)
     st = gpu.buffer(state)
-    gpu.delta_net(out, gpu.buffer(q), gpu.buffer(k), gpu.buffer(v), gpu.buffer(gates), gpu.buffer(decay),
-                  st, nk, nv, 128)
+    gpu.delta_net_unit_keys(out, gpu.buffer(q), gpu.buffer(k), gpu.buffer(v), gpu.buffer(gates),
+                            gpu.buffer(decay), st, nk, nv, 128)
     want_state, parts = gpu.buffer(state), []
     for t0 in range(0, n, step):
         t1 = min(n, t0 + step)
