@@ -1,6 +1,8 @@
-// Causal grouped-query attention over the Q8 key/value caches
-// (dwim gpu/cpu.rs:202-236), split over chunks of 64 positions so that a
-// single decode token still spreads its cache reads over the whole GPU.
+// Causal grouped-query attention over the key/value caches (dwim
+// gpu/cpu.rs:202-236), split over chunks of 64 positions so that a single
+// decode token still spreads its cache reads over the whole GPU.  A cache is
+// the reference's Q8 (int8 with an f16 scale per block of 32) or f16 (each
+// kernel a template on the format, F16; an f16 key or value is read as is).
 //
 // Pass 1, one block per (chunk, key/value head, token): the G query heads
 // sharing the key/value head score the chunk's positions (a Q8 block of 32 per
@@ -36,7 +38,12 @@ struct Shape {
 // head for all G query heads.  Values: wave w takes elements 32w..32w+31 (one
 // Q8 block: one scale per position), lane l elements 32w + 4(l % 8)..+3 of
 // positions l/8 + 8i; the 8 position groups meet by shuffles.
-template <int G>
+DEV float half_of(uint32_t word, int hi) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? word >> 16 : word & 0xffffu));
+}
+DEV uint32_t word_of(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+template <int G, bool F16>
 __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ partials, const float *__restrict__ q,
                                                             const int8_t *__restrict__ kq,
                                                             const uint16_t *__restrict__ ks,
@@ -78,24 +85,37 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
     // in flight before the first wait
     const int kp = threadIdx.x >> 3, b = threadIdx.x & 7, nblk = D / 32;
     const bool klive = kp < cnt && b < nblk;
-    uint4 ka, kc;
-    uint16_t kbits;
+    uint4 kr[F16 ? 4 : 2];
+    uint16_t kbits = 0;
     {
         const size_t off = (p0 + min(kp, cnt - 1)) * kv_dim + kvh * D + 32 * min(b, nblk - 1);
-        ka = ((const uint4 *)(kq + off))[0];
-        kc = ((const uint4 *)(kq + off))[1];
-        kbits = ks[off / 32];
+        if constexpr (F16) {
+            const uint4 *src = (const uint4 *)((const uint16_t *)kq + off);
+#pragma unroll
+            for (int i = 0; i < 4; i++) kr[i] = src[i];
+        } else {
+            kr[0] = ((const uint4 *)(kq + off))[0];
+            kr[1] = ((const uint4 *)(kq + off))[1];
+            kbits = ks[off / 32];
+        }
     }
-    // values: wave w < nblk takes Q8 block w of the head
+    // values: wave w < nblk takes block w of the head (4 values a lane)
     const bool vlive = wave < nblk;
-    uint32_t vw[kPos / 8];
+    uint32_t vw[kPos / 8][F16 ? 2 : 1];
     uint16_t vbits[kPos / 8];
 #pragma unroll
     for (int i = 0; i < kPos / 8; i++) {
         const int vp = min((lane >> 3) + 8 * i, cnt - 1);
         const size_t off = (p0 + vp) * kv_dim + kvh * D + 32 * min(wave, nblk - 1) + 4 * (lane & 7);
-        vw[i] = *(const uint32_t *)(vq + off);
-        vbits[i] = vs[off / 32];
+        if constexpr (F16) {
+            const uint2 x = *(const uint2 *)((const uint16_t *)vq + off);
+            vw[i][0] = x.x;
+            vw[i][F16 ? 1 : 0] = x.y;
+            vbits[i] = 0;
+        } else {
+            vw[i][0] = *(const uint32_t *)(vq + off);
+            vbits[i] = vs[off / 32];
+        }
     }
     // (the query loads were issued first, so this waits for them alone)
     for (int k = 0; k < kQPer; k++) {
@@ -106,14 +126,16 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
 
     const float scale = 1.0f / sqrtf((float)D);
     {
-        const float ksc = dq::from_f16(kbits);
+        const float ksc = F16 ? 1.0f : dq::from_f16(kbits);
         float kv[32];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t wa = i < 4 ? ka.x : i < 8 ? ka.y : i < 12 ? ka.z : ka.w;
-            const uint32_t wc = i < 4 ? kc.x : i < 8 ? kc.y : i < 12 ? kc.z : kc.w;
-            kv[i] = (float)(int8_t)((wa >> (8 * (i & 3))) & 0xff);
-            kv[16 + i] = (float)(int8_t)((wc >> (8 * (i & 3))) & 0xff);
+        for (int i = 0; i < 32; i++) {
+            if constexpr (F16) {
+                kv[i] = half_of(word_of(kr[i / 8], (i % 8) / 2), i % 2);
+            } else {
+                const uint32_t w = word_of(kr[i / 16], (i % 16) / 4);
+                kv[i] = (float)(int8_t)((w >> (8 * (i & 3))) & 0xff);
+            }
         }
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -150,10 +172,20 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
 #pragma unroll
         for (int i = 0; i < kPos / 8; i++) {
             const int vp = (lane >> 3) + 8 * i;
-            const uint32_t w = vw[i];
-            const float vsc = dq::from_f16(vbits[i]);
-            const float v0 = (float)(int8_t)(w & 0xff) * vsc, v1 = (float)(int8_t)((w >> 8) & 0xff) * vsc,
-                        v2 = (float)(int8_t)((w >> 16) & 0xff) * vsc, v3 = (float)(int8_t)(w >> 24) * vsc;
+            float v0, v1, v2, v3;
+            if constexpr (F16) {
+                v0 = half_of(vw[i][0], 0);
+                v1 = half_of(vw[i][0], 1);
+                v2 = half_of(vw[i][F16 ? 1 : 0], 0);
+                v3 = half_of(vw[i][F16 ? 1 : 0], 1);
+            } else {
+                const uint32_t w = vw[i][0];
+                const float vsc = dq::from_f16(vbits[i]);
+                v0 = (float)(int8_t)(w & 0xff) * vsc;
+                v1 = (float)(int8_t)((w >> 8) & 0xff) * vsc;
+                v2 = (float)(int8_t)((w >> 16) & 0xff) * vsc;
+                v3 = (float)(int8_t)(w >> 24) * vsc;
+            }
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 const float pr = vp < cnt ? p_s[g * kPos + vp] : 0.0f;
@@ -330,10 +362,11 @@ DEV ahalf8 lo8(const float *v, const ahalf8 &h) {
     return l;
 }
 
+template <bool F16>
 __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a) {
     __shared__ uint4 kf[kFP * kFD / 8];          // keys as f16, [pos][256], 16-byte chunks swizzled by pos
     __shared__ float ksc[kFP][kFD / 32];         // key scales
-    __shared__ uint32_t v8[kFP][kFD / 4];        // values, int8, [pos][256]
+    __shared__ uint32_t v8[kFP][F16 ? kFD / 2 : kFD / 4];  // values as stored (int8 or f16), [pos][256]
     __shared__ float vsc[kFP][kFD / 32];         // value scales
     __shared__ uint4 vt[2][kFD][kFP / 8];        // values hi / lo, [dim][pos]
     __shared__ uint4 pw[kFThreads / 64][2][16][kFP / 8];  // per wave: P hi / lo, [row][pos]
@@ -382,30 +415,56 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
     const bool skeys = tid < 256;
     const int8_t *const ssrc = skeys ? a.kq : a.vq;
     const uint16_t *const sscl = skeys ? a.ks : a.vs;
-    uint4 nx0, nx1;
+    uint4 nx[F16 ? 4 : 2];
     uint16_t nxs;
     auto fetch = [&](unsigned p0) {
         const unsigned p = p0 + sp;
         const bool live = p < len;
         const size_t row = (size_t)(live ? p : 0) * kv_dim + (size_t)kvh * kFD;
         const uint4 z = make_uint4(0, 0, 0, 0);
-        const uint4 v0 = *(const uint4 *)(ssrc + row + 32 * sc8), v1 = *(const uint4 *)(ssrc + row + 32 * sc8 + 16);
-        const uint16_t sv = sscl[row / 32 + sc8];
-        nx0 = live ? v0 : z;
-        nx1 = live ? v1 : z;
-        nxs = live ? sv : 0;
+        if constexpr (F16) {
+            const uint4 *src = (const uint4 *)((const uint16_t *)ssrc + row + 32 * sc8);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 v = src[i];
+                nx[i] = live ? v : z;
+            }
+            nxs = 0;
+        } else {
+            const uint4 v0 = *(const uint4 *)(ssrc + row + 32 * sc8), v1 = *(const uint4 *)(ssrc + row + 32 * sc8 + 16);
+            const uint16_t sv = sscl[row / 32 + sc8];
+            nx[0] = live ? v0 : z;
+            nx[F16 ? 1 : 1] = live ? v1 : z;
+            nxs = live ? sv : 0;
+        }
     };
     fetch(0);
     for (unsigned p0 = 0; p0 < len; p0 += kFP) {
         // ---- stage the 32 positions: keys to f16, values raw, scales
         __syncthreads();
         {
-            const uint4 x0 = nx0, x1 = nx1;
+            uint4 x[F16 ? 4 : 2];
+#pragma unroll
+            for (int i = 0; i < (F16 ? 4 : 2); i++) x[i] = nx[i];
             const uint16_t xs = nxs;
             if (p0 + kFP < len) fetch(p0 + kFP);
-            if (skeys) {
+            if constexpr (F16) {
+                // keys: as stored; values: raw words of two dims
+                if (skeys) {
+                    ksc[sp][sc8] = 1.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int chunk = 4 * sc8 + q;
+                        kf[sp * 32 + (chunk ^ (sp & 15))] = x[q];
+                    }
+                } else {
+                    vsc[sp][sc8] = 1.0f;
+#pragma unroll
+                    for (int q = 0; q < 16; q++) v8[sp][16 * sc8 + q] = word_of(x[q / 4], q % 4);
+                }
+            } else if (skeys) {
                 ksc[sp][sc8] = dq::from_f16(xs);
-                const uint32_t kw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const uint32_t kw[8] = {x[0].x, x[0].y, x[0].z, x[0].w, x[1].x, x[1].y, x[1].z, x[1].w};
 #pragma unroll
                 for (int q = 0; q < 4; q++) {  // 8 keys a 16-byte chunk of f16
                     uint32_t hw[4];
@@ -422,7 +481,7 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
                 }
             } else {
                 vsc[sp][sc8] = dq::from_f16(xs);
-                const uint32_t vw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const uint32_t vw[8] = {x[0].x, x[0].y, x[0].z, x[0].w, x[1].x, x[1].y, x[1].z, x[1].w};
 #pragma unroll
                 for (int q = 0; q < 8; q++) v8[sp][8 * sc8 + q] = vw[q];
             }
@@ -435,10 +494,16 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int p = 8 * j + i;
-                const uint32_t word = v8[p][dq4];
-                const float sc = vsc[p][dq4 / 8];
+                if constexpr (F16) {
+                    const uint32_t word = v8[p][2 * dq4 + hf];  // dims 4dq4 + 2hf, + 1
 #pragma unroll
-                for (int d = 0; d < 2; d++) vv[d][i] = (float)(int8_t)((word >> (8 * (2 * hf + d))) & 0xffu) * sc;
+                    for (int d = 0; d < 2; d++) vv[d][i] = half_of(word, d);
+                } else {
+                    const uint32_t word = v8[p][dq4];
+                    const float sc = vsc[p][dq4 / 8];
+#pragma unroll
+                    for (int d = 0; d < 2; d++) vv[d][i] = (float)(int8_t)((word >> (8 * (2 * hf + d))) & 0xffu) * sc;
+                }
             }
 #pragma unroll
             for (int d = 0; d < 2; d++) {
@@ -564,15 +629,19 @@ hipError_t attention_run(dwim_dev *dev, float *partials, float *out, const float
         PrefillArgs pa{out, q, gate, k->q, v->q, k->s, v->s, (unsigned)n, (unsigned)pos, (unsigned)n_heads,
                        (unsigned)n_kv_heads};
         dim3 grid((unsigned)((n + kFQ - 1) / kFQ), (unsigned)n_heads);
-        k_attn_prefill<<<grid, kFThreads, 0, dev->stream>>>(pa);
+        if (k->f16) k_attn_prefill<true><<<grid, kFThreads, 0, dev->stream>>>(pa);
+        else k_attn_prefill<false><<<grid, kFThreads, 0, dev->stream>>>(pa);
         return hipGetLastError();
     }
     const size_t len = pos + n, ch = kPos, chunks = (len + ch - 1) / ch;
     Shape sh{n, pos, n_heads, head_dim, n_kv_heads, ch, chunks};
     dim3 g1((unsigned)chunks, (unsigned)n_kv_heads, (unsigned)n);
     switch (n_heads / n_kv_heads) {
-#define DWIM_PARTIAL(G) \
-    case G: k_attn_partial<G><<<g1, kPThreads, 0, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh); break;
+#define DWIM_PARTIAL(G)                                                                                        \
+    case G:                                                                                                    \
+        if (k->f16) k_attn_partial<G, true><<<g1, kPThreads, 0, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh); \
+        else k_attn_partial<G, false><<<g1, kPThreads, 0, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh);      \
+        break;
         DWIM_PARTIAL(1) DWIM_PARTIAL(2) DWIM_PARTIAL(3) DWIM_PARTIAL(4) DWIM_PARTIAL(5) DWIM_PARTIAL(6)
         DWIM_PARTIAL(7) DWIM_PARTIAL(8)
 #undef DWIM_PARTIAL
@@ -649,6 +718,7 @@ extern "C" int dwim_attention_noalloc(dwim_dev *dev, dwim_buf *out, const dwim_b
     const size_t n = q->len / width, kv_dim = n_kv_heads * head_dim;
     DWIM_CHECK((pos + n) * kv_dim <= k_cache->len && (pos + n) * kv_dim <= v_cache->len,
                "attention: the caches do not hold the tokens' positions");
+    DWIM_CHECK(k_cache->f16 == v_cache->f16, "attention: the key and value caches are of different formats");
     DWIM_CHECK(dev->attn_scratch != nullptr, "attention_noalloc: the device's scratch array has no address");
     if (n == 0) return 0;
     const bool batch = n >= 16 && head_dim == (size_t)kFD;

@@ -189,6 +189,18 @@ __global__ void __launch_bounds__(256) k_store(int8_t *__restrict__ cq, uint16_t
     if (l == 0) cs[b] = bits;
 }
 
+// An f16 cache: each value rounded to the nearest f16 (ties to even, as the
+// host's to_f16), a thread a value.
+__global__ void __launch_bounds__(256) k_store_f16(uint16_t *__restrict__ c, const float *__restrict__ src, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) c[i] = dq::to_f16(src[i]);
+}
+
+hipError_t launch_store_f16(hipStream_t s, uint16_t *c, const float *src, size_t n) {
+    k_store_f16<<<blocks_for(n, 256), 256, 0, s>>>(c, src, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_store(hipStream_t s, int8_t *cq, uint16_t *cs, const float *src, size_t blocks) {
     k_store<<<blocks_for(blocks * 32, 256), 256, 0, s>>>(cq, cs, src, blocks);
     return hipGetLastError();

@@ -293,7 +293,8 @@ hipError_t launch_gated_norm(dwim_dev *dev, float *z, const float *att, const fl
 hipError_t launch_qk_prep(hipStream_t s, float *q, float *k, const float *v, const float *q_norm,
                           const float *k_norm, const float *table, size_t n, size_t pos, size_t heads,
                           size_t kv_heads, size_t head_dim, size_t rot, float eps, dwim_cache *kc, dwim_cache *vc) {
-    if (head_dim % 64 || head_dim > 256 || rot > head_dim || rot % 2) return hipErrorInvalidValue;
+    if (head_dim % 64 || head_dim > 256 || rot > head_dim || rot % 2 || kc->f16 || vc->f16)
+        return hipErrorInvalidValue;
     dim3 grid((unsigned)(heads + 2 * kv_heads), (unsigned)n);
     k_qk_prep<<<grid, (unsigned)head_dim, 0, s>>>(q, k, v, q_norm, k_norm, table, pos, heads, kv_heads, rot, eps,
                                                   kc->q, kc->s, vc->q, vc->s);

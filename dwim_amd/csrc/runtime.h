@@ -76,11 +76,15 @@ struct dwim_weight {
     void *q = nullptr, *s = nullptr, *s2 = nullptr, *s3 = nullptr;
 };
 
+// A key or value cache of `len` activations: the reference's Q8 (q: int8
+// values, s: an f16 scale per block of 32), or with f16 set, f16 values (q
+// holds their 2·len bytes, s is null).
 struct dwim_cache {
     dwim_dev *dev;
     int8_t *q;
     uint16_t *s;
     size_t len;
+    bool f16 = false;
 };
 
 // ---- errors ----
@@ -106,6 +110,7 @@ hipError_t launch_l2norm(hipStream_t s, float *x, size_t rows, size_t dim, float
 hipError_t launch_rope(hipStream_t s, float *x, const float *table, size_t n, size_t pos,
                        size_t n_heads, size_t head_dim, size_t rot_dim);
 hipError_t launch_store(hipStream_t s, int8_t *cq, uint16_t *cs, const float *src, size_t blocks);
+hipError_t launch_store_f16(hipStream_t s, uint16_t *c, const float *src, size_t n);
 hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n,
                          int add);
 hipError_t launch_matvec_q4k(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n,

@@ -201,6 +201,20 @@ extern "C" int dwim_alloc_cache(dwim_dev *dev, size_t len, dwim_cache **out) {
     return 0;
 }
 
+extern "C" int dwim_alloc_cache_f16(dwim_dev *dev, size_t len, dwim_cache **out) {
+    *out = nullptr;
+    DWIM_CHECK(len % 32 == 0, "a cache holds whole blocks of 32");
+    int8_t *q = nullptr;
+    DWIM_HIP(hipMalloc(&q, std::max<size_t>(len, 32) * 2));
+    if (hipMemsetAsync(q, 0, std::max<size_t>(len, 32) * 2, dev->stream) != hipSuccess) {
+        hipFree(q);
+        return dwim_fail("clearing a new cache failed");
+    }
+    dev->refs++;
+    *out = new dwim_cache{dev, q, nullptr, len, true};
+    return 0;
+}
+
 extern "C" void dwim_free_cache(dwim_cache *c) {
     if (!c) return;
     dwim_dev *dev = c->dev;
@@ -254,13 +268,18 @@ extern "C" int dwim_store(dwim_dev *dev, dwim_cache *cache, size_t offset, const
     DWIM_CHECK(offset % 32 == 0 && src->len % 32 == 0, "stores are whole blocks of 32");
     DWIM_CHECK(offset + src->len <= cache->len, "storing past the end of a cache");
     if (src->len == 0) return 0;
-    LAUNCH(launch_store(dev->stream, cache->q + offset, cache->s + offset / 32, src->data, src->len / 32));
+    if (cache->f16)
+        LAUNCH(launch_store_f16(dev->stream, (uint16_t *)cache->q + offset, src->data, src->len));
+    else
+        LAUNCH(launch_store(dev->stream, cache->q + offset, cache->s + offset / 32, src->data, src->len / 32));
     return 0;
 }
 
 extern "C" int dwim_read_cache(dwim_dev *dev, const dwim_cache *cache, size_t len, uint8_t *out) {
     DWIM_CHECK(len % 32 == 0 && len <= cache->len, "reading a cache past its end or mid-block");
-    if (len) {
+    if (len && cache->f16) {
+        DWIM_HIP(hipMemcpyAsync(out, cache->q, 2 * len, hipMemcpyDeviceToHost, dev->stream));
+    } else if (len) {
         DWIM_HIP(hipMemcpyAsync(out, cache->q, len, hipMemcpyDeviceToHost, dev->stream));
         DWIM_HIP(hipMemcpyAsync(out + len, cache->s, len / 32 * 2, hipMemcpyDeviceToHost, dev->stream));
     }
@@ -269,6 +288,13 @@ extern "C" int dwim_read_cache(dwim_dev *dev, const dwim_cache *cache, size_t le
 }
 
 extern "C" int dwim_write_cache(dwim_dev *dev, dwim_cache *cache, const uint8_t *data, size_t bytes) {
+    if (cache->f16) {
+        DWIM_CHECK(bytes % 64 == 0, "cache bytes are not whole blocks");
+        DWIM_CHECK(bytes / 2 <= cache->len, "writing past the end of a cache");
+        if (bytes) DWIM_HIP(hipMemcpyAsync(cache->q, data, bytes, hipMemcpyHostToDevice, dev->stream));
+        DWIM_HIP(hipStreamSynchronize(dev->stream));
+        return 0;
+    }
     size_t len = bytes / 34 * 32;
     DWIM_CHECK(bytes == dwim_cache_bytes(len), "cache bytes are not whole blocks");
     DWIM_CHECK(len <= cache->len, "writing past the end of a cache");
@@ -511,6 +537,7 @@ extern "C" int dwim_attention(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, c
     size_t kv_dim = n_kv_heads * head_dim;
     DWIM_CHECK((pos + n) * kv_dim <= k_cache->len && (pos + n) * kv_dim <= v_cache->len,
                "attention: the caches do not hold the tokens' positions");
+    DWIM_CHECK(k_cache->f16 == v_cache->f16, "attention: the key and value caches are of different formats");
     if (n) LAUNCH(launch_attention(dev, out->data, q->data, k_cache, v_cache, n, pos, n_heads, head_dim, n_kv_heads));
     return 0;
 }

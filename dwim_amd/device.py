@@ -54,6 +54,7 @@ SIGNATURES = {
     "dwim_alloc": (_int, [_vp, _sz, ctypes.POINTER(_vp)]),
     "dwim_free_buffer": (None, [_vp]),
     "dwim_alloc_cache": (_int, [_vp, _sz, ctypes.POINTER(_vp)]),
+    "dwim_alloc_cache_f16": (_int, [_vp, _sz, ctypes.POINTER(_vp)]),
     "dwim_free_cache": (None, [_vp]),
     "dwim_resize": (_int, [_vp, _vp, _sz]),
     "dwim_len": (_sz, [_vp]),
@@ -253,6 +254,7 @@ class Weight:
 class Cache:
     def __init__(self, dev: "Hip", handle: int, length: int):
         self.dev, self.h, self.len = dev, handle, length
+        self.f16 = False
 
     def __del__(self):
         if getattr(self, "h", None) and _lib is not None:
@@ -314,6 +316,14 @@ class Hip:
         _check(self.L.dwim_alloc(self.h, length, ctypes.byref(h)))
         return Buffer(self, h.value)
 
+    def alloc_cache_f16(self, length: int) -> Cache:
+        """An f16 key/value cache (the f16 KV-cache mode)."""
+        h = _vp()
+        _check(self.L.dwim_alloc_cache_f16(self.h, length, ctypes.byref(h)))
+        c = Cache(self, h.value, length)
+        c.f16 = True
+        return c
+
     def alloc_cache(self, length: int) -> Cache:
         h = _vp()
         _check(self.L.dwim_alloc_cache(self.h, length, ctypes.byref(h)))
@@ -346,7 +356,7 @@ class Hip:
         _check(self.L.dwim_store(self.h, cache.h, offset, src.h))
 
     def read_cache(self, cache: Cache, length: int) -> bytes:
-        out = np.empty(self.L.dwim_cache_bytes(length), np.uint8)
+        out = np.empty(2 * length if cache.f16 else self.L.dwim_cache_bytes(length), np.uint8)
         _check(self.L.dwim_read_cache(self.h, cache.h, length, _ptr(out, _u8p)))
         return out.tobytes()
 

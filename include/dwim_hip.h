@@ -103,6 +103,12 @@ int dwim_read_cache(dwim_dev *dev, const dwim_cache *cache, size_t len, uint8_t 
 int dwim_write_cache(dwim_dev *dev, dwim_cache *cache, const uint8_t *data, size_t bytes);
 /* gpu/mod.rs:404-407 */
 size_t dwim_cache_bytes(size_t len);
+/* An f16 key/value cache of `len` activations (the f16 KV-cache mode; the
+ * reference has only Q8, gpu/mod.rs:39-41,183-186): dwim_store rounds each
+ * value to the nearest f16 (ties to even), dwim_read_cache / dwim_write_cache
+ * move 2·len bytes of little-endian f16, and dwim_attention reads the values
+ * as they are.  Freed with dwim_free_cache. */
+int dwim_alloc_cache_f16(dwim_dev *dev, size_t len, dwim_cache **out);
 
 /* ---- operations (gpu/mod.rs:251-400) ---- */
 

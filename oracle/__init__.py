@@ -88,6 +88,8 @@ def _declare(L):
         "or_rope": (None, [_f32p, _sz, _f32p, _sz, _sz, _sz, _sz]),
         "or_store": (None, [_i8p, _u16p, _sz, _f32p, _sz]),
         "or_attention": (None, [_f32p, _f32p, _sz, _i8p, _u16p, _i8p, _u16p, _sz, _sz, _sz, _sz]),
+        "or_store_f16": (None, [_u16p, _sz, _f32p, _sz]),
+        "or_attention_f16": (None, [_f32p, _f32p, _sz, _u16p, _u16p, _sz, _sz, _sz, _sz]),
         "or_silu_mul": (None, [_f32p, _f32p, _sz]),
         "or_sigmoid_mul": (None, [_f32p, _f32p, _sz]),
         "or_conv": (None, [_f32p, _sz, _f32p, _sz, _f32p, _sz, _f32p, _f32p, _sz, _f32p, _f32p]),
@@ -387,6 +389,37 @@ def attention(q, k: Cache, v: Cache, pos, n_heads, head_dim, n_kv_heads):
     out = np.empty_like(q)
     lib().or_attention(_p(out, _f32p), _p(q, _f32p), n, _p(k.quants, _i8p), _p(k.scales, _u16p),
                        _p(v.quants, _i8p), _p(v.scales, _u16p), pos, n_heads, head_dim, n_kv_heads)
+    return out
+
+
+class CacheF16:
+    """The f16 KV-cache mode: f16 values (no reference; see or_store_f16)."""
+
+    def __init__(self, length: int):
+        assert length % 32 == 0
+        self.values = np.zeros(length, np.uint16)
+
+    def store(self, offset: int, src):
+        src = f32(src)
+        lib().or_store_f16(_p(self.values, _u16p), offset, _p(src, _f32p), src.size)
+
+    def read_cache(self, length: int) -> bytes:
+        return self.values[:length].astype("<u2").tobytes()
+
+
+def cache_f16_of(data) -> CacheF16:
+    data = f32(data)
+    c = CacheF16(data.size)
+    c.store(0, data)
+    return c
+
+
+def attention_f16(q, k: CacheF16, v: CacheF16, pos, n_heads, head_dim, n_kv_heads):
+    q = f32(q)
+    n = q.size // (n_heads * head_dim)
+    out = np.empty_like(q)
+    lib().or_attention_f16(_p(out, _f32p), _p(q, _f32p), n, _p(k.values, _u16p), _p(v.values, _u16p), pos,
+                           n_heads, head_dim, n_kv_heads)
     return out
 
 

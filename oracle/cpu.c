@@ -268,6 +268,53 @@ void or_attention(float *out, const float *q, size_t n, const int8_t *kq, const 
     }
 }
 
+/* The f16 KV-cache mode (no reference: the reference's caches are Q8): a
+ * cache of f16 values, each the nearest f16 of the value stored (ties to
+ * even), and Cpu::attention (gpu/cpu.rs:202-236) over it, the dot products
+ * and weighted sums in the same order as over the Q8 cache with every block
+ * scale 1 (dot_q8 and add_scaled_q8, :388-411). */
+void or_store_f16(uint16_t *cache, size_t offset, const float *src, size_t len) {
+    for (size_t i = 0; i < len; i++) cache[offset + i] = or_to_f16(src[i]);
+}
+
+static float dot_f16(const float *a, size_t len, const uint16_t *c, size_t offset) {
+    float total = -0.0f;
+    for (size_t b = 0; b < len / 32; b++) {
+        float dot = -0.0f;
+        for (int i = 0; i < 32; i++) dot += a[32 * b + i] * or_from_f16(c[offset + 32 * b + i]);
+        total += dot;
+    }
+    return total;
+}
+
+static void add_scaled_f16(float *out, size_t len, float scale, const uint16_t *c, size_t offset) {
+    for (size_t i = 0; i < len; i++) out[i] += scale * or_from_f16(c[offset + i]);
+}
+
+void or_attention_f16(float *out, const float *q, size_t n, const uint16_t *kc, const uint16_t *vc, size_t pos,
+                      size_t n_heads, size_t head_dim, size_t n_kv_heads) {
+    size_t group = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim;
+    float scale = 1.0f / sqrtf((float)head_dim);
+    size_t items = n * n_heads;
+#pragma omp parallel
+    {
+        float *scores = (float *)malloc((pos + n) * sizeof(float));
+#pragma omp for schedule(dynamic, 1)
+        for (size_t i = 0; i < items; i++) {
+            size_t token = i / n_heads, head = i % n_heads;
+            size_t len = pos + token + 1;
+            size_t kv = head / group * head_dim;
+            const float *qh = q + i * head_dim;
+            float *o = out + i * head_dim;
+            for (size_t t = 0; t < len; t++) scores[t] = scale * dot_f16(qh, head_dim, kc, t * kv_dim + kv);
+            softmax(scores, len);
+            memset(o, 0, head_dim * sizeof(float));
+            for (size_t t = 0; t < len; t++) add_scaled_f16(o, head_dim, scores[t], vc, t * kv_dim + kv);
+        }
+        free(scores);
+    }
+}
+
 /* gpu/cpu.rs:238-242 */
 void or_silu_mul(float *gate, const float *up, size_t len) {
     for (size_t i = 0; i < len; i++) gate[i] = gate[i] * sigmoid(gate[i]) * up[i];

@@ -84,6 +84,9 @@ void or_l2norm(float *x, size_t len, size_t dim, float eps);
 void or_rope(float *x, size_t len, const float *table, size_t pos, size_t n_heads,
              size_t head_dim, size_t rot_dim);
 void or_store(int8_t *cache_q, uint16_t *cache_s, size_t offset, const float *src, size_t len);
+void or_store_f16(uint16_t *cache, size_t offset, const float *src, size_t len);
+void or_attention_f16(float *out, const float *q, size_t n, const uint16_t *kc, const uint16_t *vc, size_t pos,
+                      size_t n_heads, size_t head_dim, size_t n_kv_heads);
 void or_attention(float *out, const float *q, size_t n, const int8_t *kq, const uint16_t *ks,
                   const int8_t *vq, const uint16_t *vs, size_t pos, size_t n_heads,
                   size_t head_dim, size_t n_kv_heads);

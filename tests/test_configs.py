@@ -2,9 +2,11 @@
 
 * config 2, the gated-DeltaNet decode step, is in test_state.py (its carried
   state, seeded N(0, 0.1), is read back through the saved state);
-* config 3, GQA attention over the Q8 cache: 24 query heads, 4 key/value
-  heads of 256, decode at depths 4096, 32768 and 131072 for two sessions
-  (separate caches), and a causal 2048-token prefill at depth 0.
+* config 3, GQA attention: 24 query heads, 4 key/value heads of 256, decode
+  at depths 4096, 32768 and 131072 for two sessions (separate caches), and a
+  causal 2048-token prefill at depth 0; over the reference's Q8 cache and
+  over an f16 cache (the configuration's own wording), each against the
+  oracle's attention over the same cache format.
 
 * config 5, the 27B shape with the MTP drafter: two sessions of
   32768-token prompts sharing the weights; speculative decoding (3 drafts,
@@ -30,8 +32,25 @@ def _err(got, want):
     return float((np.abs(got - want) / (1 + np.abs(want))).max())
 
 
+def _caches(gpu, kd, vd, f16):
+    if f16:
+        kc, vc = gpu.alloc_cache_f16(kd.size), gpu.alloc_cache_f16(vd.size)
+        want = O.cache_f16_of(kd), O.cache_f16_of(vd)
+    else:
+        kc, vc = gpu.alloc_cache(kd.size), gpu.alloc_cache(vd.size)
+        want = O.cache_of(kd, 0), O.cache_of(vd, 0)
+    gpu.store(kc, 0, gpu.buffer(kd))
+    gpu.store(vc, 0, gpu.buffer(vd))
+    return kc, vc, want
+
+
+def _oracle_attention(f16, q, kc, vc, pos, heads, hd, kvh):
+    return (O.attention_f16 if f16 else O.attention)(q, kc, vc, pos, heads, hd, kvh)
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["q8", "f16"])
 @pytest.mark.parametrize("depth", [4096, 32768, 131072])
-def test_attention_decode_at_depth_for_two_sessions(depth):
+def test_attention_decode_at_depth_for_two_sessions(depth, f16):
     heads, hd, kvh = 24, 256, 4
     kv_dim = kvh * hd
     gpu = D.Hip(0)
@@ -40,35 +59,52 @@ def test_attention_decode_at_depth_for_two_sessions(depth):
         q = rng.floats(heads * hd)
         kd = rng.floats(depth * kv_dim)
         vd = rng.floats(depth * kv_dim)
-        want = O.attention(q, O.cache_of(kd, 0), O.cache_of(vd, 0), depth - 1, heads, hd, kvh)
-        kc, vc = gpu.alloc_cache(kd.size), gpu.alloc_cache(vd.size)
-        gpu.store(kc, 0, gpu.buffer(kd))
-        gpu.store(vc, 0, gpu.buffer(vd))
+        kc, vc, (ok, ov) = _caches(gpu, kd, vd, f16)
+        if f16:
+            assert gpu.read_cache(kc, 4096) == ok.read_cache(4096)  # f16 stores are exact
+        want = _oracle_attention(f16, q, ok, ov, depth - 1, heads, hd, kvh)
         out = gpu.alloc(heads * hd)
         gpu.attention(out, gpu.buffer(q), kc, vc, depth - 1, heads, hd, kvh)
         e = _err(gpu.read(out), want)
-        print(f"depth {depth} session {session}: max err {e:.2e}", flush=True)
+        print(f"depth {depth} session {session} {'f16' if f16 else 'q8'}: max err {e:.2e}", flush=True)
         assert e <= 1e-4
     gpu.close()
 
 
-def test_attention_prefill_of_2048_tokens():
+@pytest.mark.parametrize("f16", [False, True], ids=["q8", "f16"])
+def test_attention_prefill_of_2048_tokens(f16):
     heads, hd, kvh, n = 24, 256, 4, 2048
     kv_dim = kvh * hd
     rng = O.Rng(2048)
     q = rng.floats(n * heads * hd)
     kd = rng.floats(n * kv_dim)
     vd = rng.floats(n * kv_dim)
-    want = O.attention(q, O.cache_of(kd, 0), O.cache_of(vd, 0), 0, heads, hd, kvh)
     gpu = D.Hip(0)
-    kc, vc = gpu.alloc_cache(kd.size), gpu.alloc_cache(vd.size)
-    gpu.store(kc, 0, gpu.buffer(kd))
-    gpu.store(vc, 0, gpu.buffer(vd))
+    kc, vc, (ok, ov) = _caches(gpu, kd, vd, f16)
+    want = _oracle_attention(f16, q, ok, ov, 0, heads, hd, kvh)
     out = gpu.alloc(q.size)
     gpu.attention(out, gpu.buffer(q), kc, vc, 0, heads, hd, kvh)
     e = _err(gpu.read(out), want)
-    print(f"prefill 2048: max err {e:.2e}", flush=True)
+    print(f"prefill 2048 {'f16' if f16 else 'q8'}: max err {e:.2e}", flush=True)
     assert e <= 1e-4
+    gpu.close()
+
+
+def test_f16_cache_round_trips_and_refuses_mixed_formats():
+    gpu = D.Hip(0)
+    rng = O.Rng(7)
+    x = rng.floats(4 * 1024)
+    c = gpu.alloc_cache_f16(x.size)
+    gpu.store(c, 1024, gpu.buffer(x[1024:]))
+    gpu.store(c, 0, gpu.buffer(x[:1024]))
+    data = gpu.read_cache(c, x.size)
+    assert data == x.astype(np.float16).tobytes()
+    c2 = gpu.alloc_cache_f16(x.size)
+    gpu.write_cache(c2, data)
+    assert gpu.read_cache(c2, x.size) == data
+    q8 = gpu.alloc_cache(x.size)
+    with pytest.raises(D.DwimError, match="different formats"):
+        gpu.attention(gpu.alloc(256), gpu.buffer(rng.floats(256)), c, q8, 0, 1, 256, 1)
     gpu.close()
 
 

@@ -107,6 +107,22 @@ def test_full_width_layers_agree_with_cpu():
     g.close()
 
 
+@pytest.mark.gpu
+def test_one_token_path_with_value_heads_not_a_multiple_of_eight():
+    """The fused DeltaNet decode step places a value head's workgroups on one
+    XCD when the heads divide by 8, and in order otherwise: 6 value heads over
+    2 key heads take the second mapping (the 27B shape's 48 the first)."""
+    cfg = _tiny(False)
+    cfg.v_heads, cfg.k_heads = 6, 2
+    gpu = D.Hip(0)
+    g = M.Model(gpu, cfg, SEED + 5, max_len=32)
+    o = O.Model(cfg.as_dict(), SEED + 5)
+    _close(g.forward([3, 17, 42], 0), o.forward([3, 17, 42], 0), 2e-3, "3 tokens")
+    for i, t in enumerate([11, 40, 2, 63, 30]):
+        _close(g.forward([t], 3 + i), o.forward([t], 3 + i), 2e-3, f"token {i}")
+    g.close()
+
+
 # ---- drafting, verifying and rewinding (qwen35/mod.rs:1045-1290)
 
 PREFIX, BATCH = [3, 17, 42, 7, 9], [11, 2, 30, 5]

@@ -497,3 +497,29 @@ def test_q4_k_matmul_of_many_tokens_is_each_row_dot_bit_for_bit(n):
     q = w.quants.reshape(rows, -1)
     want = np.array([[O.dot_q4_k(q[r], x[t]) for r in range(rows)] for t in range(n)], np.float32)
     assert got.tobytes() == want.tobytes()
+
+
+def test_f16_cache_stores_nearest_f16_and_attends_as_softmax_over_it():
+    """The f16 KV-cache mode's oracle: stored values are numpy's float16 of
+    the input (nearest, ties to even) bit for bit; attention over the cache is
+    the float64 softmax of scaled dots over the f16 values."""
+    rng = O.Rng(8)
+    n_heads, head_dim, n_kv, n, pos = 6, 64, 2, 2, 40
+    kv_dim = n_kv * head_dim
+    kd = rng.floats((pos + n) * kv_dim) * np.float32(3)
+    vd = rng.floats((pos + n) * kv_dim)
+    kd[:3] = [65519.0, 1e-8, -2.5e-5]  # past the largest f16's halfway point, and subnormals
+    k, v = O.cache_f16_of(kd), O.cache_f16_of(vd)
+    assert k.read_cache(kd.size) == kd.astype(np.float16).tobytes()
+    q = rng.floats(n * n_heads * head_dim)
+    got = O.attention_f16(q, k, v, pos, n_heads, head_dim, n_kv).reshape(n, n_heads, head_dim)
+    K = kd.astype(np.float16).astype(np.float64).reshape(-1, n_kv, head_dim)
+    V = vd.astype(np.float16).astype(np.float64).reshape(-1, n_kv, head_dim)
+    qq = q.reshape(n, n_heads, head_dim).astype(np.float64)
+    for t in range(n):
+        for h in range(n_heads):
+            L = pos + t + 1
+            s = K[:L, h // (n_heads // n_kv)] @ qq[t, h] / math.sqrt(head_dim)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            assert np.allclose(got[t, h], p @ V[:L, h // (n_heads // n_kv)], atol=1e-5)
