@@ -1,0 +1,55 @@
+"""Workloads for counter runs of single kernels (rocprofv3 --pmc / --kernel-trace).
+
+    python -m dwim_amd.kernel_workloads attention [--reps N]
+
+`attention`: first a device copy of 256 MiB (four times), the calibration
+of the FETCH_SIZE / WRITE_SIZE counters; then one-token GQA decode (24 query heads, 4 key/value heads of 256,
+the 27B shape's attention layer) over Q8 caches filled with N(0, 1) keys and
+values at context depths 4096, 32768 and 131072, `reps` calls at each depth
+(k_attn_partial + k_attn_combine), each depth's caches distinct; then the
+same over f16 caches.  Every call goes through the C ABI (dwim_attention).
+"""
+from __future__ import annotations
+
+import argparse
+
+from . import device as D
+
+
+def attention(reps: int) -> None:
+    dev = D.Hip(0)
+    big = 64 << 20  # floats: 256 MiB
+    src, dst = dev.alloc(big), dev.alloc(big)
+    for _ in range(4):
+        dev.copy(dst, 0, src, 0, big)
+    dev.sync()
+    del src, dst
+    heads, hd, kvh = 24, 256, 4
+    kv_dim = kvh * hd
+    for f16 in (False, True):
+        for depth in (4096, 32768, 131072):
+            n = depth * kv_dim
+            kc = dev.alloc_cache_f16(n) if f16 else dev.alloc_cache(n)
+            vc = dev.alloc_cache_f16(n) if f16 else dev.alloc_cache(n)
+            dev.store(kc, 0, dev.buffer(D.synthetic_values(depth, 0, n, 1.0)))
+            dev.store(vc, 0, dev.buffer(D.synthetic_values(depth + 1, 0, n, 1.0)))
+            q = dev.buffer(D.synthetic_values(7, 0, heads * hd, 1.0))
+            out = dev.alloc(heads * hd)
+            for _ in range(reps):
+                dev.attention(out, q, kc, vc, depth - 1, heads, hd, kvh)
+            dev.sync()
+            print(f"attention {'f16' if f16 else 'q8'} depth {depth}: {reps} calls", flush=True)
+            del kc, vc
+    dev.close()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("workload", choices=["attention"])
+    ap.add_argument("--reps", type=int, default=20)
+    a = ap.parse_args()
+    attention(a.reps)
+
+
+if __name__ == "__main__":
+    main()
