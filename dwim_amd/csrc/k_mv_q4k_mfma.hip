@@ -31,6 +31,7 @@
 // take gate's rows of its tile, then up's.
 #include "device_util.h"
 #include "layout.h"
+#include "mv_common.h"
 #include "planes.h"
 #include "quant_math.h"
 #include "runtime.h"
@@ -39,6 +40,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 namespace {
+
+using namespace mvq;
 
 // One token's planes from f32 activations.  A workgroup of 256 writes 1024
 // activations (four lanes a group of 16, four each).  With a norm, either
@@ -91,37 +94,10 @@ __global__ void __launch_bounds__(kPlanesThreads) k_planes(const float *__restri
     planes::write4x4(out, i, v, pair != 0);
 }
 
-// The d·sc and dmin·m of sub-blocks 2k and 2k + 1 (k = 0..3) from the
-// block header words w1, w2, w3 (scale bytes 0-3, 4-7, 8-11), both at once
-// in the two bytes of a 16-bit lane, as ggml's get_scale_min_k4 defines them:
-// sub-block j < 4 keeps 6 bits of scale byte j and of byte j + 4; j >= 4 takes
-// the low / high nibble of byte j + 4 and the top two bits of byte j - 4 / j.
-DEV void scales_pair(uint32_t w1, uint32_t w2, uint32_t w3, int k, float &sc0, float &sc1, float &mn0, float &mn1) {
-    const int sh = 16 * (k & 1);
-    const uint32_t A = (w1 >> sh) & 0xffffu, B = (w2 >> sh) & 0xffffu, C = (w3 >> sh) & 0xffffu;
-    const uint32_t sc = k < 2 ? A & 0x3f3fu : (C & 0x0f0fu) | ((A >> 2) & 0x3030u);
-    const uint32_t mn = k < 2 ? B & 0x3f3fu : ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
-    sc0 = (float)(sc & 0xffu);
-    sc1 = (float)(sc >> 8);
-    mn0 = (float)(mn & 0xffu);
-    mn1 = (float)(mn >> 8);
-}
-
-DEV float f16_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
-
-// lane j of each quad of lanes, to all four
-template <int J>
-DEV uint32_t quad_bcast(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, J * 0x55, 0xf, 0xf, false);
-}
-
 constexpr int kMaxJobs = 4;
 constexpr int kMaxParts = 4;
 constexpr int kMaxTok = 4;     // tokens of a several-token launch (a verify batch: 1 + 3 drafts)
 constexpr int kBatchArea = 2;  // planes areas kBatchArea.. hold the tokens of such a launch
-// s_waitcnt immediate (gfx9 encoding) waiting for every vector memory
-// operation: vmcnt 0, expcnt and lgkmcnt at their maxima (no wait)
-constexpr int kWaitVm0 = 0x0f70;
 // RMS partial sums a lane loads up front: 6 · 64 groups of 16 cover 6144
 // columns (the rest, if any, are loaded at the end)
 constexpr int kRmsLoads = 6;

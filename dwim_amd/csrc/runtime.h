@@ -41,6 +41,14 @@ struct dwim_dev {
     // Split one-token Q4_K products (k_mv_q4k_mfma.hip): the partial sums of
     // up to mv_tiles_cap 16-row tiles (4 parts × 32 floats each) and a counter
     // per tile, zero between launches.
+    // The chain launches (k_mv_chain.hip): the error word, each workgroup's
+    // progress word, the parts' partial sums and a counter per split tile.
+    unsigned *chain_ctl = nullptr;                  // the error word
+    unsigned long long *chain_progress = nullptr;   // [kChainMaxGroups] progress words, zeroed once
+    unsigned long long chain_seq = 0;               // the last chain launch's sequence number
+    float *chain_partials = nullptr;
+    unsigned *chain_counters = nullptr;
+    unsigned chain_tiles_cap = 0;
     float *mv_partials = nullptr;
     unsigned *mv_counters = nullptr;
     unsigned mv_tiles_cap = 0;
@@ -219,6 +227,28 @@ size_t gemm_split_bytes(size_t n, size_t cols);
 size_t argmax_scratch_words(size_t rows);
 size_t gemm_parts_floats(size_t n, size_t rows, size_t cols);
 hipError_t gemm_reserve(dwim_dev *dev, size_t split_bytes, size_t parts_floats);
+// ---- a chain of one-token Q4_K products in one persistent launch (k_mv_chain.hip)
+constexpr int kMaxChain = 8;       // products a chain
+constexpr int kMaxChainParts = 4;  // parts a tile
+constexpr int kChainCtlWords = 4;
+constexpr size_t kChainMaxGroups = 1024;  // workgroups (CUs) a chain launch may have
+struct ChainStep {
+    const dwim_weight *w[2] = {nullptr, nullptr};  // w[1]: up of a SwiGLU pair (out = silu(w0·x)·(w1·x))
+    float *out = nullptr;
+    int in_area = 0;        // the planes area of the input
+    int dep = -1;           // the earlier step whose output the input is (-1: an earlier launch's)
+    int add = 0;            // out += W·in
+    int rms = 0;            // the input is x·w with per-group Σx²: results scale by 1/sqrt(Σ/cols + eps)
+    int coherent_out = 0;   // out is read by a later step of the chain
+    int emit_area = -1;     // the planes of out (of out·emit_norm with Σout², and that in f32 to emit_xw)
+    const float *emit_norm = nullptr;
+    float *emit_xw = nullptr;
+    float eps = 0.0f;
+};
+size_t chain_lds_bytes();
+hipError_t launch_mv_chain(dwim_dev *dev, const ChainStep *steps, int n);
+// nonzero when a chain launch gave up waiting (its results are then wrong)
+int chain_error(dwim_dev *dev);
 size_t attention_partials_floats(size_t n, size_t pos, size_t n_heads, size_t head_dim);
 hipError_t attention_reserve(dwim_dev *dev, size_t floats);
 hipError_t attention_scratch_init(dwim_dev *dev);
