@@ -137,59 +137,31 @@ def prefill_flops(cfg, tokens):
     return 2 * params * tokens + n_att * 4 * cfg.heads * cfg.head_dim * pairs + 2 * cfg.vocab * H
 
 
-def cpu_baseline():
-    """The oracle (C restatement of dwim's CPU path, OpenMP over rows/heads as
-    rayon does) timed per operation at the model's decode shapes, times the
-    calls per token — the reference's own per-op methodology
-    (gpu/tests.rs:429-609 kernel_speed) — giving CPU ms per decode token."""
+def cpu_baseline(cfg, seed, state, tokens, pos0, steps=4):
+    """The reference's CPU path on the same workload: the oracle (C
+    restatement of dwim gpu/cpu.rs and inference/qwen35, OpenMP over rows and
+    heads as rayon does) builds the same random-init model, restores the GPU
+    model's saved state after the 4096-token prefill (LanguageModel::restore,
+    the dwimstat layout), and decodes `steps` tokens of the same sequence at
+    4k context, timed as the reference's token loop would run them.  The
+    greedy token after each step is compared with the GPU's."""
     import oracle as O
-    rng = np.random.default_rng(0)
-    H, F, V = 5120, 17408, 248320
     t0 = time.time()
-
-    def q4k(rows, cols):
-        vals = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
-        return O.Weight.quantized(O.Q4_K, vals)
-
-    def timed(fn, reps):
-        fn()
-        s = time.perf_counter()
-        for _ in range(reps):
-            fn()
-        return (time.perf_counter() - s) / reps
-
-    per_token = 0.0
-    # matmuls: (rows, cols, calls per token) of the 64-layer body
-    shapes = [(17408, 5120, 128), (5120, 17408, 64), (10240, 5120, 48), (6144, 5120, 48 + 32), (5120, 6144, 64),
-              (1024, 5120, 32)]
-    for rows, cols, calls in shapes:
-        w = q4k(rows, cols)
-        x = rng.standard_normal(cols, dtype=np.float32)
-        per_token += calls * timed(lambda: O.matmul(w, x), 2)
-    # Q6_K head: time a 1/16 slice of its rows, scale up
-    vals = rng.standard_normal((V // 16, H), dtype=np.float32) * 0.02
-    head = O.Weight.quantized(O.Q6_K, vals)
-    x = rng.standard_normal(H, dtype=np.float32)
-    per_token += 16 * timed(lambda: O.matmul(head, x), 2)
-    # DeltaNet step (48 layers) and attention at 4k (16 layers)
-    nk, nv, d = 16, 48, 128
-    q = O.l2norm(rng.standard_normal(nk * d, dtype=np.float32), d, 1e-6)
-    k = O.l2norm(rng.standard_normal(nk * d, dtype=np.float32), d, 1e-6)
-    v = rng.standard_normal(nv * d, dtype=np.float32)
-    gates = rng.standard_normal(2 * nv, dtype=np.float32)
-    decay = np.concatenate([-rng.uniform(0.1, 1, nv), rng.uniform(-4, 4, nv)]).astype(np.float32)
-    state = rng.standard_normal(nv * d * d, dtype=np.float32) * 0.1
-    per_token += 48 * timed(lambda: O.delta_net(q, k, v, gates, decay, state, nk, nv, d), 2)
-    L = 4096
-    kd = rng.standard_normal(L * 1024, dtype=np.float32)
-    kc, vc = O.cache_of(kd, 0), O.cache_of(kd[::-1].copy(), 0)
-    qa = rng.standard_normal(24 * 256, dtype=np.float32)
-    per_token += 16 * timed(lambda: O.attention(qa, kc, vc, L - 1, 24, 256, 4), 2)
-    return {"value": 1.0 / per_token, "unit": "tok/s", "cores": O.threads(), "kind": "port",
-            "sample": "C restatement of dwim gpu/cpu.rs (OpenMP): each decode op of the 27B shape at 4k context "
-                      "timed once on the host (matmuls, Q6_K head on a 1/16 row slice, DeltaNet step, attention), "
-                      "times its calls per token; elementwise ops omitted",
-            "seconds": time.time() - t0}
+    o = O.Model(cfg.as_dict(), seed, O.Q4_K, O.Q6_K, max_len=pos0 + steps + 8, batch=1)
+    build_s = time.time() - t0
+    assert o.restore(state) == pos0
+    agree = 0
+    t0 = time.perf_counter()
+    for i in range(steps):
+        logits = o.forward([int(tokens[i])], pos0 + i)
+        agree += int(np.argmax(logits)) == int(tokens[i + 1])
+    dt = time.perf_counter() - t0
+    del o
+    return {"value": steps / dt, "unit": "tok/s", "cores": O.threads(), "kind": "port",
+            "sample": f"C restatement of dwim gpu/cpu.rs + inference/qwen35 (OpenMP), the same 27B-shape model "
+                      f"restored from the GPU's state after the 4096-token prefill, {steps} greedy decode tokens "
+                      f"at 4k context (model built in {build_s:.0f} s, not timed)",
+            "greedy_tokens_equal_to_gpu": f"{agree}/{steps}"}
 
 
 def mtp_leg(dev, D, M, prompt_len=32768, sessions=2, tokens=64, k=3):
@@ -308,13 +280,18 @@ def main():
     dev.sync()
     prefill_s = time.perf_counter() - t0
     pos = args.prompt
+    # the state after the prefill, for the CPU baseline (outside any timing)
+    state = None if args.no_cpu else model.save(pos)
+    decoded = [tok]
     for _ in range(args.warmup):
         tok = model.forward_greedy([tok], pos)
+        decoded.append(tok)
         pos += 1
     dev.sync()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         tok = model.forward_greedy([tok], pos)
+        decoded.append(tok)
         pos += 1
     dev.sync()
     decode_s = time.perf_counter() - t0
@@ -367,8 +344,8 @@ def main():
     model.close()
     if args.mtp:
         result["mtp"] = mtp_leg(dev, D, M, prompt_len=args.mtp_prompt)
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline()
+    if not args.no_cpu and len(decoded) > 4:
+        result["cpu_baseline"] = cpu_baseline(cfg, 1234, state, decoded, args.prompt)
     print(json.dumps(result), flush=True)
 
 
