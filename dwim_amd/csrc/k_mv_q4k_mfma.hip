@@ -36,6 +36,8 @@
 #include "quant_math.h"
 #include "runtime.h"
 
+#include <stdlib.h>
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
@@ -125,6 +127,12 @@ struct Args {
     float *emit_xw;
     float *partials;               // P > 1: [tile][part][token][2][16]
     unsigned *counters;            // P > 1: [tile], zero between launches
+    // given: the planes hold each head of head_dim columns unnormalized;
+    // its groups' scales and sums are multiplied by 1/sqrt(Σ head_ss[head]
+    // / head_dim + head_eps) (head_ss: [heads][4] partial sums of squares)
+    const float4 *head_ss;
+    unsigned head_dim;
+    float head_eps;
 };
 
 // Per wave LDS, in 16-byte chunks: the planes of its K blocks (chunk
@@ -183,7 +191,10 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
         const unsigned i = (unsigned)ci / 48u, p = ((unsigned)ci % 48u) / 16u, part16 = (unsigned)ci % 16u;
         xc[u] = *(const uint4 *)(a.xq + p * cols + (b0 + i) * 256u + 16u * part16);
     }
-    const float4 st = a.xstat[b0 * 8u + (lane < nblk * 8 ? (unsigned)lane : 0u)];
+    const unsigned sti = b0 * 8u + (lane < nblk * 8 ? (unsigned)lane : 0u);
+    float4 st = a.xstat[sti];
+    // (a 64-column run of the statistics: float4 sti / 2)
+    const float4 hss = a.head_ss ? a.head_ss[(sti / 2u) * 64u / a.head_dim] : float4{0.0f, 0.0f, 0.0f, 0.0f};
     // the RMS partial sums (up to kRmsLoads per lane) are loaded here too,
     // by every wave and without a branch, and added up at the end
     const unsigned ng = cols / (unsigned)planes::kGroup;
@@ -215,6 +226,13 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     // then overwrite the spares
 #pragma unroll
     for (int u = 0; u < kPlaneLoads; u++) my[lane + 64 * u] = xc[u];
+    if (a.head_ss) {
+        const float f = 1.0f / sqrtf(((hss.x + hss.y) + (hss.z + hss.w)) / (float)a.head_dim + a.head_eps);
+        st.x *= f;
+        st.y *= f;
+        st.z *= f;
+        st.w *= f;
+    }
     ((float4 *)(my + L::kStat))[lane] = st;
     if (lane < 2) my[L::kZero + lane] = make_uint4(0, 0, 0, 0);
     __builtin_amdgcn_wave_barrier();
@@ -769,6 +787,12 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
     if (swiglu && ws[0]->rows != ws[1]->rows) return hipErrorInvalidValue;
     a.swiglu = swiglu;
     if (extra) {
+        if (extra->head_ss) {
+            if (extra->head_dim % 64 || cols % extra->head_dim) return hipErrorInvalidValue;
+            a.head_ss = (const float4 *)extra->head_ss;
+            a.head_dim = (unsigned)extra->head_dim;
+            a.head_eps = extra->head_eps;
+        }
         if (extra->rms) {
             a.rms_ss = in.ss;
             a.eps = extra->eps;
@@ -785,6 +809,16 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
     }
     // a swiglu workgroup takes gate's tile and reads up's beside it
     return run(dev, a, swiglu ? 1 : (unsigned)count, rows);
+}
+
+// the stream-K kernel for 2..4 tokens unless DWIM_MV_STREAM=0 (the
+// tile-group kernel above, kept for comparison)
+static bool stream_tokens() {
+    static const bool on = [] {
+        const char *v = getenv("DWIM_MV_STREAM");
+        return !(v && v[0] == '0');
+    }();
+    return on;
 }
 
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
@@ -825,6 +859,17 @@ hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws
             }
             a.swiglu = swiglu;
             e = run(dev, a, njobs, rows);
+        } else if (stream_tokens()) {
+            const int8_t *xq[kMaxTok];
+            const float *xs[kMaxTok];
+            float *o[kMaxJobs];
+            for (size_t t = 0; t < nt; t++) {
+                const planes::View v = planes_area(dev, kBatchArea + (int)t, cols);
+                xq[t] = v.q;
+                xs[t] = v.stat;
+            }
+            for (int j = 0; j < count; j++) o[j] = outs[j] ? outs[j] + t0 * rows[j] : nullptr;
+            e = run_mv_stream(dev, ws, o, adds, count, swiglu, nt, xq, xs);
         } else {
             TokArgs a{};
             a.nb = (unsigned)(cols / 256);

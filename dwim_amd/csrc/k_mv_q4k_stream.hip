@@ -1,0 +1,497 @@
+// Q4_K products of two to four tokens at once (a speculative-decoding verify
+// batch, small batches) on the int8 matrix cores, reading every weight once
+// for all of them (dwim gpu/cpu.rs:110-149 computes each token's product in
+// f32; the arithmetic here is the one-token kernel's, exact in int32 and
+// scaled in f32).
+//
+// The MFMA layout is k_mv_q4k_mfma.hip's: v_mfma_i32_16x16x64_i8 with the 16
+// rows of a weight tile as A and B's columns (digit, sub-block) of one token's
+// planes, nonzero only in their sub-block's k-group; the planes are scaled per
+// 32 activations (k_planes' pair mode), so a sub-block's two MFMAs chain in
+// int32 and take one scale.
+//
+// The work is split so that every CU streams the same number of weight
+// bytes in one round ("stream-K"):
+//   * an item is up to K (k_of) consecutive 256-blocks of one tile (of gate's or of
+//     up's rows for a SwiGLU pair); the items of a tile are its blocks in
+//     order, gate's then up's;
+//   * the row's blocks split into P parts only when the planes of NT tokens
+//     of a whole row would not fit in LDS; items are numbered part by part,
+//     tile by tile;
+//   * one workgroup of 16 waves a CU takes a contiguous run of a part's items
+//     (the runs as even as integer division makes them), stages the planes of
+//     its part once, and its waves take every 16th item of the run, the next
+//     item's weights in flight while the current one is computed;
+//   * each item's partial sums (per token, its 16 rows) go to LDS; after one
+//     barrier a wave per tile sums them in item order.  A tile that lies in
+//     one workgroup's run (and P = 1) is finished there; otherwise the
+//     workgroups that share it write their sums with device-coherent stores,
+//     count in on the tile's counter, and the last to arrive sums them in
+//     (part, workgroup) order, so the result has the same bits whichever
+//     finishes last, and clears the counter.
+#include "device_util.h"
+#include "layout.h"
+#include "mv_common.h"
+#include "planes.h"
+#include "runtime.h"
+
+#include <algorithm>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+// global-memory pointers, so that the loads through them are global loads
+// (counted in order by vmcnt) rather than flat ones
+#define GMEM __attribute__((address_space(1)))
+
+namespace {
+
+using namespace mvq;
+
+constexpr int kW = 16;           // waves a workgroup
+// blocks an item: 3, or 2 for four tokens (whose accumulators take the
+// registers of a third block in both of the wave's two item buffers)
+constexpr int k_of(int nt) { return nt >= 4 ? 2 : 3; }
+constexpr int kJobs = 4;
+constexpr int kTok = 4;
+constexpr int kParts = 4;
+constexpr int kHdrChunks = 32;   // per wave: d·sc of the 8 sub-blocks × 16 rows (floats)
+// LDS for one part's planes and statistics: at most this many bytes
+constexpr size_t kPlaneBudget = 96 * 1024;
+
+struct StreamArgs {
+    const uint8_t *w[kJobs];     // SwiGLU: w[0] gate, w[1] up
+    float *out[kJobs];           // [NT][rows_j]
+    unsigned rows[kJobs];
+    unsigned tile0[kJobs + 1];   // first tile of each matrix in the launch's numbering; [njobs] = all tiles
+    unsigned add_mask;
+    int swiglu;
+    unsigned nb;                 // 256-blocks per row
+    unsigned P;                  // parts
+    unsigned pb0[kParts + 1];    // part p: blocks [pb0[p], pb0[p + 1])
+    unsigned ih[kParts];         // items per tile and matrix in part p: ceil(blocks / K)
+    unsigned g0[kParts + 1];     // first workgroup of part p; [P] = the grid
+    unsigned cmax;               // partial-sum slots per (tile, part)
+    unsigned plane_cap;          // LDS layout: blocks of planes reserved (the largest part)
+    unsigned items_cap;          // LDS layout: item slots reserved
+    const int8_t *xq[kTok];      // each token's planes [3][cols]
+    const float *xstat[kTok];    // [cols/64][8]
+    float *partials;             // [tile][part][cmax][NT][32]
+    unsigned *counters;          // [tile], zero between launches
+};
+
+// Kernel-argument arrays are copied once, with constant indices, each
+// element through readfirstlane into scalar registers, and selected from
+// there by value: a select among loads of the argument block would otherwise
+// become one vector load at a selected address, or a copy to scratch memory,
+// and a wait on it.
+DEV uint32_t sload(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+template <typename T>
+DEV T sload(T v) {
+    if constexpr (sizeof(T) == 8) {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        return __builtin_bit_cast(T, (uint64_t)sload((uint32_t)u) | (uint64_t)sload((uint32_t)(u >> 32)) << 32);
+    } else {
+        return __builtin_bit_cast(T, sload(__builtin_bit_cast(uint32_t, v)));
+    }
+}
+// an opaque copy in scalar registers (the empty asm keeps the selects below
+// from being folded back into an indexed load)
+template <typename T>
+DEV T sreg(T v) {
+    T r = sload(v);
+    asm volatile("" : "+s"(r));
+    return r;
+}
+template <typename T>
+DEV T sel(unsigned i, T v0, T v1, T v2, T v3, T v4 = T()) {
+    return i == 1 ? v1 : i == 2 ? v2 : i == 3 ? v3 : i == 4 ? v4 : v0;
+}
+
+struct Item {
+    const GMEM uint8_t *units;  // the item's first unit
+    unsigned tile;         // in the launch's numbering
+    unsigned bl;           // its first block, counted from the part's first
+    int nblk;
+    int half;              // SwiGLU: 0 gate, 1 up
+};
+
+template <int K>
+struct Regs {
+    v4u q[K][2];
+    uint32_t h[K];
+};
+
+template <int NT>
+__global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
+    constexpr int kK = k_of(NT);
+    extern __shared__ uint4 lds[];
+    // (the wave index through readfirstlane: the compiler then knows it,
+    // and all that follows from it, to be the same across the wave)
+    const int lane = threadIdx.x & 63, wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kq = lane >> 4, c = lane & 15;
+    const unsigned P = a.P, nb = a.nb, J = a.swiglu ? 2u : 1u;
+    const unsigned g01 = sreg(a.g0[1]), g02 = sreg(a.g0[2]), g03 = sreg(a.g0[3]), g04 = sreg(a.g0[4]);
+    const unsigned pb01 = sreg(a.pb0[1]), pb02 = sreg(a.pb0[2]), pb03 = sreg(a.pb0[3]), pb04 = sreg(a.pb0[4]);
+    const unsigned ih0 = sreg(a.ih[0]), ih1 = sreg(a.ih[1]), ih2 = sreg(a.ih[2]), ih3 = sreg(a.ih[3]);
+    const unsigned t01 = sreg(a.tile0[1]), t02 = sreg(a.tile0[2]), t03 = sreg(a.tile0[3]);
+    const GMEM uint8_t *w0 = (const GMEM uint8_t *)sreg(a.w[0]), *w1 = (const GMEM uint8_t *)sreg(a.w[1]),
+                       *w2 = (const GMEM uint8_t *)sreg(a.w[2]), *w3 = (const GMEM uint8_t *)sreg(a.w[3]);
+    const unsigned g = blockIdx.x;
+    const unsigned p = (unsigned)(1u < P && g >= g01) + (unsigned)(2u < P && g >= g02) + (unsigned)(3u < P && g >= g03);
+    const unsigned gfirst = sel(p, 0u, g01, g02, g03), G = sel(p + 1, 0u, g01, g02, g03, g04) - gfirst, gp = g - gfirst;
+    const unsigned pb = sel(p, 0u, pb01, pb02, pb03), PB = sel(p + 1, 0u, pb01, pb02, pb03, pb04) - pb;
+    const unsigned ih = sel(p, ih0, ih1, ih2, ih3), ip = J * ih;
+    const unsigned TT = a.tile0[kJobs];
+    const unsigned long long Ip = (unsigned long long)TT * ip;
+    const unsigned i0 = (unsigned)((unsigned long long)gp * Ip / G);
+    const unsigned i1 = (unsigned)((unsigned long long)(gp + 1) * Ip / G);
+    const unsigned cols = nb * 256;
+
+    // LDS: planes [block][token][48 chunks], statistics [block][token][8],
+    // the zero region, per wave the decoded scales, the items' sums
+    const unsigned kStat = a.plane_cap * NT * 48;
+    const unsigned kZero = kStat + a.plane_cap * NT * 8;
+    const unsigned kHdr = kZero + kK * NT * 48;
+    const unsigned kSlots = kHdr + kW * kHdrChunks;
+    v4i *lv = (v4i *)lds;
+    const float4 *stl = (const float4 *)(lds + kStat);
+    float *hdr = (float *)(lds + kHdr + wave * kHdrChunks);
+    float *slots = (float *)(lds + kSlots);  // [item - i0][NT][16]
+
+    auto item_of = [=](unsigned i) {
+        Item it;
+        const unsigned T = i / ip, rem = i - T * ip, half = rem / ih, r = rem - half * ih;
+        const unsigned j = (unsigned)(T >= t01) + (unsigned)(T >= t02) + (unsigned)(T >= t03);
+        const unsigned tl = T - sel(j, 0u, t01, t02, t03);
+        const GMEM uint8_t *wbase = sel(a.swiglu ? half : j, w0, w1, w2, w3);
+        it.tile = T;
+        it.bl = r * kK;
+        it.nblk = (int)min((unsigned)kK, PB - r * kK);
+        it.half = (int)half;
+        it.units = wbase + ((size_t)tl * nb + pb + it.bl) * q4kt::kUnit;
+        return it;
+    };
+    auto load = [=](Regs<kK> &R, const Item &it) {
+#pragma unroll
+        for (int u = 0; u < kK; u++) {
+            const unsigned off = (unsigned)(u < it.nblk ? u : 0) * (unsigned)q4kt::kUnit;
+            R.q[u][0] = *(const GMEM v4u *)(it.units + off + q4kt::qs_off(kq, c));
+            R.q[u][1] = *(const GMEM v4u *)(it.units + off + q4kt::qs_off(kq, c) + 16);
+            R.h[u] = *(const GMEM uint32_t *)(it.units + off + 4 * lane);
+        }
+    };
+
+    // B: lane (k-group kq, column c) reads digit c % 3 of sub-block 2kq + h
+    // when c / 3 == kq, else the zero region
+    const bool active = c < 12 && c / 3 == kq;
+    const int gcol = c < 12 ? c / 3 : 0;
+    const int k4 = lane & 3, R4 = lane >> 2;
+    const float f = c < 12 ? (c % 3 == 0 ? 1.0f : c % 3 == 1 ? 256.0f : 65536.0f) : 0.0f;
+
+    auto compute = [=](const Regs<kK> &R, const Item &it, unsigned slot) {
+        float acc[NT][4], macc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            acc[t][0] = acc[t][1] = acc[t][2] = acc[t][3] = 0.0f;
+            macc[t] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kK; u++) {
+            if (u >= it.nblk) break;
+            const unsigned bl = it.bl + (unsigned)u;
+            {
+                const uint32_t w0 = quad_bcast<0>(R.h[u]), w1 = quad_bcast<1>(R.h[u]), w2 = quad_bcast<2>(R.h[u]),
+                               w3 = quad_bcast<3>(R.h[u]);
+                const float d = f16_bits(w0 & 0xffffu), dmin = f16_bits(w0 >> 16);
+                float sc0, sc1, mn0, mn1;
+                scales_pair(w1, w2, w3, k4, sc0, sc1, mn0, mn1);
+                const float D0 = d * sc0, D1 = d * sc1;
+                // the high nibble arrives as 16·(q − 8): scale d·sc/16, and
+                // 8·d·sc joins the min term
+                const float mA = dmin * mn0, mB = dmin * mn1 - 8.0f * D1;
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const float4 xm = stl[(bl * NT + t) * 8 + 2 * k4 + 1];
+                    macc[t] += mA * (xm.x + xm.y) + mB * (xm.z + xm.w);
+                }
+                hdr[(2 * k4) * 16 + R4] = D0;
+                hdr[(2 * k4 + 1) * 16 + R4] = D1 * 0.0625f;
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const v4i *bbase = lv + (active ? (int)(bl * NT * 48) + 16 * (c % 3) + 4 * kq : (int)kZero + u * NT * 48);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t mask = h ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+                const float4 Dsb = *(const float4 *)&hdr[(2 * gcol + h) * 16 + 4 * kq];
+                const v4u q0 = R.q[u][0], q1 = R.q[u][1];
+                const v4i a0 = {(int)(q0.x & mask), (int)(q0.y & mask), (int)(q0.z & mask), (int)(q0.w & mask)};
+                const v4i a1 = {(int)(q1.x & mask), (int)(q1.y & mask), (int)(q1.z & mask), (int)(q1.w & mask)};
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const v4i *bp = bbase + t * 48 + 2 * h;
+                    v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bp[1], C, 0, 0, 0);
+                    // token t's scale of sub-block 2·gcol + h
+                    const float sx = ((const float *)&stl[(bl * NT + t) * 8 + 2 * gcol])[2 * h];
+                    acc[t][0] += (Dsb.x * sx) * (float)C[0];
+                    acc[t][1] += (Dsb.y * sx) * (float)C[1];
+                    acc[t][2] += (Dsb.z * sx) * (float)C[2];
+                    acc[t][3] += (Dsb.w * sx) * (float)C[3];
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        // the columns meet, weighted by their digit: lanes 16kq..16kq+15 hold
+        // rows 4kq..4kq+3; the min terms of row R sit in lanes 4R..4R+3
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[t][e] = group_sum<16>(acc[t][e] * f);
+            const float mt = group_sum<4>(macc[t]);
+            const float mrow = __shfl(mt, 16 * kq + 4 * (c & 3), 64);
+            if (c < 4)
+                slots[(slot * NT + t) * 16 + 4 * kq + c] =
+                    (c == 0 ? acc[t][0] : c == 1 ? acc[t][1] : c == 2 ? acc[t][2] : acc[t][3]) - mrow;
+        }
+    };
+
+    // ---- the part's planes and statistics (from L2, every workgroup reads
+    // them), then the first item's weights, then the planes' stores: the
+    // barrier waits for the planes alone
+    const unsigned n_w = i1 - i0 > (unsigned)wave ? (i1 - i0 - (unsigned)wave + kW - 1) / kW : 0u;
+    Regs<kK> A, B;
+    Item ia{}, ib{};
+    {
+        // chunk gi of the planes, then of the statistics (past both: a
+        // reload of chunk 0, stored nowhere)
+        const unsigned nplane = PB * NT * 48, nstat = PB * NT * 8;
+        constexpr int kPL = (int)((kPlaneBudget / 16 + 1023) / 1024);
+        const GMEM int8_t *xqs[NT];
+        const GMEM float *xss[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            xqs[t] = (const GMEM int8_t *)sload(a.xq[t]);
+            xss[t] = (const GMEM float *)sload(a.xstat[t]);
+        }
+        v4i v[kPL];
+#pragma unroll
+        for (int u = 0; u < kPL; u++) {
+            const unsigned gi = threadIdx.x + 1024u * u;
+            const bool plane = gi < nplane;
+            const unsigned s = plane ? gi : gi - nplane < nstat ? gi - nplane : 0u;
+            const unsigned bt = plane ? s / 48u : s / 8u, bl = bt / NT, t = bt % NT;
+            const GMEM int8_t *qsrc = xqs[0];
+            const GMEM float *ssrc = xss[0];
+#pragma unroll
+            for (int q = 1; q < NT; q++) {
+                qsrc = t == (unsigned)q ? xqs[q] : qsrc;
+                ssrc = t == (unsigned)q ? xss[q] : ssrc;
+            }
+            const unsigned ch = s % 48u, k = s % 8u;
+            v[u] = plane ? *(const GMEM v4i *)(qsrc + (ch / 16u) * cols + (pb + bl) * 256u + 16u * (ch % 16u))
+                         : *(const GMEM v4i *)(ssrc + ((pb + bl) * 8u + k) * 4u);
+        }
+        // (unconditional, so that the waits count it: a wave without items
+        // reloads the run's first, which every run has)
+        ia = item_of(i0 + (n_w > 0 ? (unsigned)wave : 0u));
+        load(A, ia);
+#pragma unroll
+        for (int u = 0; u < kPL; u++) {
+            const unsigned gi = threadIdx.x + 1024u * u;
+            if (gi < nplane + nstat) lv[gi < nplane ? gi : kStat + (gi - nplane)] = v[u];
+        }
+        if (threadIdx.x < (unsigned)(kK * NT * 48)) lv[kZero + threadIdx.x] = v4i{0, 0, 0, 0};
+    }
+    __syncthreads();
+
+    // ---- the wave's items, the next one's weights in flight
+    // (the loads are unconditional, past the last item a reload of it, so
+    // that the waits before each item's arithmetic count only its own loads)
+    for (unsigned k = 0; k < n_w; k += 2) {
+        ib = item_of(i0 + wave + min(k + 1, n_w - 1) * kW);
+        load(B, ib);
+        compute(A, ia, wave + k * kW);
+        ia = item_of(i0 + wave + min(k + 2, n_w - 1) * kW);
+        load(A, ia);
+        if (k + 1 < n_w) compute(B, ib, wave + (k + 1) * kW);
+    }
+    __syncthreads();
+
+    // ---- each tile of the run: its items' sums in order, by one wave
+    // lane (half hf, token pair ts, row): tokens ts and ts + 2
+    const int hf = lane >> 5, ts = (lane >> 4) & 1, row = lane & 15;
+    const unsigned Tfirst = i0 / ip, Tlast = i1 > i0 ? (i1 - 1) / ip : Tfirst - 1;
+    for (unsigned T = Tfirst + (unsigned)wave; T <= Tlast && i1 > i0; T += kW) {
+        const unsigned lo = max(i0, T * ip), hi = min(i1, (T + 1) * ip);
+        float v0 = 0.0f, v1 = 0.0f;
+        for (unsigned i = lo; i < hi; i++) {
+            const int half = (int)((i - T * ip) / ih);
+            if (half != hf) continue;
+            const float *sl = slots + (size_t)(i - i0) * NT * 16;
+            v0 += sl[ts * 16 + row];
+            if (ts + 2 < NT) v1 += sl[(ts + 2) * 16 + row];
+        }
+        const bool whole = P == 1 && T * ip >= i0 && (T + 1) * ip <= i1;
+        if (!whole) {
+            // the workgroups sharing the tile meet: this one's slot is its
+            // index among the part's workgroups that hold a piece of the tile
+            auto wg_of = [=](unsigned long long item, unsigned long long I, unsigned Gq) {
+                return (unsigned)(((item + 1) * Gq - 1) / I);
+            };
+            const unsigned cl = gp - wg_of((unsigned long long)T * ip, Ip, G);
+            float *pp = a.partials + (((size_t)T * P + p) * a.cmax + cl) * NT * 32;
+            __hip_atomic_store(pp + ts * 32 + hf * 16 + row, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (ts + 2 < NT)
+                __hip_atomic_store(pp + (ts + 2) * 32 + hf * 16 + row, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
+            unsigned n_c = 0;
+            for (unsigned q = 0; q < P; q++) {
+                const unsigned ihq = sel(q, ih0, ih1, ih2, ih3), ipq = J * ihq;
+                const unsigned Gq = sel(q + 1, 0u, g01, g02, g03, g04) - sel(q, 0u, g01, g02, g03);
+                const unsigned long long Iq = (unsigned long long)TT * ipq;
+                n_c += wg_of((unsigned long long)(T + 1) * ipq - 1, Iq, Gq) - wg_of((unsigned long long)T * ipq, Iq, Gq) + 1;
+            }
+            unsigned old = 0;
+            if (lane == 0) old = __hip_atomic_fetch_add(&a.counters[T], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            old = __shfl(old, 0, 64);
+            if (old != n_c - 1) continue;
+            v0 = v1 = 0.0f;
+            for (unsigned q = 0; q < P; q++) {
+                const unsigned ihq = sel(q, ih0, ih1, ih2, ih3), ipq = J * ihq;
+                const unsigned Gq = sel(q + 1, 0u, g01, g02, g03, g04) - sel(q, 0u, g01, g02, g03);
+                const unsigned long long Iq = (unsigned long long)TT * ipq;
+                const unsigned nq = wg_of((unsigned long long)(T + 1) * ipq - 1, Iq, Gq) -
+                                    wg_of((unsigned long long)T * ipq, Iq, Gq) + 1;
+                const float *tp = a.partials + ((size_t)T * P + q) * a.cmax * NT * 32;
+                for (unsigned s = 0; s < nq; s++) {
+                    v0 += __hip_atomic_load(tp + s * NT * 32 + ts * 32 + hf * 16 + row, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+                    if (ts + 2 < NT)
+                        v1 += __hip_atomic_load(tp + s * NT * 32 + (ts + 2) * 32 + hf * 16 + row, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            if (lane == 0) __hip_atomic_store(&a.counters[T], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // the tile's results: lanes of half 0 hold gate (or the product),
+        // lanes of half 1 up
+        // (v_permlane32_swap of a value with itself: lanes < 32 get their
+        // own value first, then lane + 32's)
+        const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v0), false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v1), __float_as_uint(v1), false, false);
+        const float x0 = __uint_as_float(s0[0]), y0 = __uint_as_float(s0[1]);
+        const float x1 = __uint_as_float(s1[0]), y1 = __uint_as_float(s1[1]);
+        const unsigned j = (unsigned)(T >= t01) + (unsigned)(T >= t02) + (unsigned)(T >= t03);
+        const unsigned rj = sel(j, sreg(a.rows[0]), sreg(a.rows[1]), sreg(a.rows[2]), sreg(a.rows[3]));
+        const unsigned grow = (T - sel(j, 0u, t01, t02, t03)) * 16 + (unsigned)row;
+        float *oj = sel(j, sreg(a.out[0]), sreg(a.out[1]), sreg(a.out[2]), sreg(a.out[3]));
+        if (hf != 0 || grow >= rj) continue;
+        const bool adds = (a.add_mask >> j) & 1u;
+        float r0 = x0, r1 = x1;
+        if (a.swiglu) {
+            r0 = x0 * sigmoidf_(x0) * y0;  // silu(gate) · up (gpu/cpu.rs:238-242)
+            r1 = x1 * sigmoidf_(x1) * y1;
+        }
+        float *o0 = oj + (size_t)ts * rj + grow;
+        *o0 = adds ? *o0 + r0 : r0;
+        if (ts + 2 < NT) {
+            float *o1 = oj + (size_t)(ts + 2) * rj + grow;
+            *o1 = adds ? *o1 + r1 : r1;
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds, int count,
+                         int swiglu, size_t nt, const int8_t *const *xq, const float *const *xstat) {
+    if (nt < 2 || nt > (size_t)kTok || count < 1 || count > kJobs || (swiglu && count != 2)) return hipErrorInvalidValue;
+    const unsigned NT = (unsigned)nt, J = swiglu ? 2u : 1u, njobs = swiglu ? 1u : (unsigned)count;
+    const unsigned K = (unsigned)k_of((int)nt);
+    StreamArgs a{};
+    a.nb = (unsigned)(ws[0]->cols / 256);
+    a.swiglu = swiglu;
+    unsigned TT = 0;
+    for (unsigned j = 0; j < (unsigned)kJobs; j++) {
+        a.tile0[j] = j < njobs ? TT : 0xffffffffu;
+        if (j < njobs) TT += (unsigned)q4kt::tiles(ws[j]->rows);
+    }
+    a.tile0[0] = 0;
+    a.tile0[kJobs] = TT;
+    for (int j = 0; j < count; j++) {
+        a.w[j] = (const uint8_t *)ws[j]->q;
+        a.out[j] = outs[j];
+        a.rows[j] = (unsigned)ws[j]->rows;
+        if (adds && adds[j] && (unsigned)j < njobs) a.add_mask |= 1u << j;
+    }
+    if (TT > dev->mv_tiles_cap) return hipErrorInvalidValue;
+    // parts: as few as keep a part's planes within the LDS budget
+    const size_t per_block = (size_t)NT * (48 + 8) * 16;
+    const unsigned pb_max = (unsigned)(kPlaneBudget / per_block);
+    a.P = (a.nb + pb_max - 1) / pb_max;
+    if (a.P > (unsigned)kParts) return hipErrorInvalidValue;
+    unsigned long long I = 0, Ipart[kParts];
+    unsigned plane_cap = 0;
+    for (unsigned p = 0; p <= a.P; p++) a.pb0[p] = p * a.nb / a.P;
+    for (unsigned p = 0; p < a.P; p++) {
+        const unsigned PB = a.pb0[p + 1] - a.pb0[p];
+        plane_cap = std::max(plane_cap, PB);
+        a.ih[p] = (PB + K - 1) / K;
+        Ipart[p] = (unsigned long long)TT * J * a.ih[p];
+        I += Ipart[p];
+    }
+    // one workgroup a CU, shared out among the parts by their items
+    const unsigned G = (unsigned)std::min<unsigned long long>((unsigned long long)dev->cus, I);
+    unsigned given = 0;
+    unsigned Gp[kParts];
+    for (unsigned p = 0; p < a.P; p++) {
+        Gp[p] = (unsigned)std::max<unsigned long long>(1, std::min<unsigned long long>(Ipart[p], Ipart[p] * G / I));
+        given += Gp[p];
+    }
+    // the rounding's leftover to the part with the most items a workgroup
+    while (given < G) {
+        unsigned best = 0;
+        for (unsigned p = 1; p < a.P; p++)
+            if (Ipart[p] * Gp[best] > Ipart[best] * Gp[p]) best = p;
+        if (Gp[best] >= Ipart[best]) break;
+        Gp[best]++, given++;
+    }
+    unsigned items_cap = 0, cmax = 0;
+    a.g0[0] = 0;
+    for (unsigned p = 0; p < a.P; p++) {
+        a.g0[p + 1] = a.g0[p] + Gp[p];
+        items_cap = std::max(items_cap, (unsigned)((Ipart[p] + Gp[p] - 1) / Gp[p]));
+        const unsigned long long ip = (unsigned long long)J * a.ih[p];
+        auto wg_of = [=](unsigned long long item) { return (unsigned)(((item + 1) * Gp[p] - 1) / Ipart[p]); };
+        for (unsigned T = 0; T < TT; T++) cmax = std::max(cmax, wg_of((T + 1) * ip - 1) - wg_of(T * ip) + 1);
+    }
+    for (unsigned p = a.P + 1; p <= (unsigned)kParts; p++) a.g0[p] = a.g0[a.P];
+    a.cmax = cmax;
+    a.plane_cap = plane_cap;
+    a.items_cap = items_cap;
+    if ((size_t)TT * a.P * cmax * NT * 32 > dev->mv_stream_cap) return hipErrorInvalidValue;
+    a.partials = dev->mv_stream;
+    a.counters = dev->mv_counters;
+    for (unsigned t = 0; t < NT; t++) {
+        a.xq[t] = xq[t];
+        a.xstat[t] = xstat[t];
+    }
+    const size_t lds = ((size_t)plane_cap * NT * 56 + (size_t)K * NT * 48 + (size_t)kW * kHdrChunks) * 16 +
+                       (size_t)items_cap * NT * 16 * 4;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    static bool raised[kTok + 1] = {};
+    const void *fn = NT == 2 ? (const void *)k_mv_stream<2> : NT == 3 ? (const void *)k_mv_stream<3>
+                                                                       : (const void *)k_mv_stream<4>;
+    if (!raised[NT]) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        raised[NT] = true;
+    }
+    if (NT == 2) k_mv_stream<2><<<G, kW * 64, lds, dev->stream>>>(a);
+    else if (NT == 3) k_mv_stream<3><<<G, kW * 64, lds, dev->stream>>>(a);
+    else k_mv_stream<4><<<G, kW * 64, lds, dev->stream>>>(a);
+    return hipGetLastError();
+}

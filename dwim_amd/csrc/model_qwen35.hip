@@ -94,6 +94,8 @@ struct dwim_model {
     dwim_buf *x = nullptr, *xb = nullptr, *xh = nullptr, *q = nullptr, *gate = nullptr, *k = nullptr,
              *v = nullptr, *att = nullptr, *qkv = nullptr, *z = nullptr, *ab = nullptr;
     dwim_buf *up = nullptr, *gate_ffn = nullptr, *logits = nullptr, *rope = nullptr, *drafted = nullptr;
+    // the one-token DeltaNet step's Σo² per head quarter ([v_heads][4])
+    dwim_buf *head_ss = nullptr;
     Sequence seq;
     std::map<size_t, Sequence> parked;  // the sequences not running
     // verifying: the linear layers' states run through the batch, and their
@@ -331,14 +333,22 @@ struct dwim_model {
     }
     // x += w · (area `area`), handing the planes of x·norm (and x·norm in f32
     // to xw when given) on to area `to`
-    int add_handover(const dwim_weight *w, int area, int to, const dwim_buf *norm, dwim_buf *xw) {
+    // (head_ss given: the planes in `area` are DeltaNet heads whose RMS norm
+    // is applied here, from their Σo² per quarter)
+    int add_handover(const dwim_weight *w, int area, int to, const dwim_buf *norm, dwim_buf *xw,
+                     const dwim_buf *head_ss = nullptr) {
         float *o = x->data;
         const int add = 1;
         MvExtra e;
         e.emit_area = to;
         e.emit_norm = norm ? norm->data : nullptr;
         e.emit_xw = xw ? xw->data : nullptr;
-        DWIM_HIP(launch_mv_q4k_mfma(dev, &w, &o, &add, 1, 0, area, norm ? &e : nullptr));
+        if (head_ss) {
+            e.head_ss = head_ss->data;
+            e.head_dim = c.state_dim;
+            e.head_eps = c.eps;
+        }
+        DWIM_HIP(launch_mv_q4k_mfma(dev, &w, &o, &add, 1, 0, area, norm || head_ss ? &e : nullptr));
         return 0;
     }
     // products of the layer input (area 0, RMS-scaled)
@@ -391,12 +401,14 @@ struct dwim_model {
             const dwim_weight *ws[2] = {l.qkv, l.z};
             dwim_buf *outs[2] = {qkv, z};
             TRY(from_input(ws, outs, 2));
-            // the gate projection, conv, delta rule and gated norm in one
-            // launch, the gate logits from x·attn_norm (xh) RMS-scaled
-            DWIM_HIP(launch_gdn(dev, qkv->data, state->data, state_out->data, l.conv->data, l.ab, xh->data, rms0(),
-                                l.decay->data, seq.ssm_state[l.slot]->data, z->data, l.norm->data, eps, c.k_heads,
-                                c.v_heads, c.state_dim, 1));
-            TRY(add_handover(l.out, 1, 0, l.mlp_norm, nullptr));
+            // the gate projection, conv, delta rule and gated output in one
+            // launch of 4 workgroups a head, the gate logits from
+            // x·attn_norm (xh) RMS-scaled; the head's RMS norm of o is
+            // applied by the output product (its Σo² in head_ss)
+            DWIM_HIP(launch_gdn_split(dev, qkv->data, state->data, state_out->data, l.conv->data, l.ab, xh->data,
+                                      rms0(), l.decay->data, seq.ssm_state[l.slot]->data, z->data, l.norm->data, eps,
+                                      c.k_heads, c.v_heads, c.state_dim, head_ss->data, 1));
+            TRY(add_handover(l.out, 1, 0, l.mlp_norm, nullptr, head_ss));
         }
         // the FFN: gate/up pair from area 0 (RMS-scaled), its planes to area 1
         const dwim_weight *ws[2] = {l.gate, l.up};
@@ -999,7 +1011,8 @@ extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg
     for (int i = 0; i < 11; i++)
         if (m->buf(m->most * m->widths[i], b[i])) return 1;
     if (m->buf(m->most * c.intermediate, &m->up) || m->buf(m->most * c.intermediate, &m->gate_ffn) ||
-        m->buf((c.drafter ? kMaxDrafts + 1 : 1) * c.vocab, &m->logits) || m->buf(c.hidden, &m->drafted))
+        m->buf((c.drafter ? kMaxDrafts + 1 : 1) * c.vocab, &m->logits) || m->buf(c.hidden, &m->drafted) ||
+        m->buf(4 * c.v_heads, &m->head_ss))
         return 1;
     std::vector<float> table;
     rope_table(table, max_len, c.rot_dim, c.rope_theta);

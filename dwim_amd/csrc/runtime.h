@@ -52,6 +52,10 @@ struct dwim_dev {
     float *mv_partials = nullptr;
     unsigned *mv_counters = nullptr;
     unsigned mv_tiles_cap = 0;
+    // several-token products (k_mv_q4k_stream.hip): partial sums of the
+    // tiles that workgroups share, [tile][part][slot][token][32]
+    float *mv_stream = nullptr;
+    size_t mv_stream_cap = 0;  // floats
     // The open handle and every live buffer, weight and cache hold a
     // reference: the device (its stream) outlives whatever was made on it,
     // whichever order a binding frees them in.
@@ -155,6 +159,11 @@ struct MvExtra {
     int emit_area = -1;
     const float *emit_norm = nullptr;
     float *emit_xw = nullptr;
+    // the input planes hold heads of head_dim columns unnormalized, each
+    // scaled here by 1/sqrt(Σ head_ss[head][0..3] / head_dim + head_eps)
+    const float *head_ss = nullptr;
+    size_t head_dim = 0;
+    float head_eps = 0.0f;
 };
 hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                               int count, int swiglu, int area, const MvExtra *extra = nullptr);
@@ -163,6 +172,11 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
 // (RMS-normalized by `norm` when given, the normalized rows to xn_out when
 // that is given) in the batch areas, then outs[j] ([n][rows_j]) += or = W_j·x
 // by adds[j], or a SwiGLU pair into outs[0] as launch_mv_q4k_mfma.
+// 2..4 tokens whose planes (pair mode) are at xq[t], xstat[t]: outs[j]
+// ([nt][rows_j]) += or = W_j·x, or a SwiGLU pair into outs[0], every weight
+// read once (k_mv_q4k_stream.hip)
+hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds, int count,
+                         int swiglu, size_t nt, const int8_t *const *xq, const float *const *xstat);
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                                      int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
                                      float *xn_out);
@@ -264,6 +278,13 @@ hipError_t launch_gdn(dwim_dev *dev, const float *qkv, const float *conv_state, 
                       const float *conv_w, const dwim_weight *w_ab, const float *xw, const Rms &rms,
                       const float *decay, float *state, float *z, const float *norm_w, float eps, size_t nk,
                       size_t nv, size_t head_dim, int area);
+// The same step over 4 workgroups a head, the RMS norm of o left to the
+// product that reads the planes (area): each quarter's Σo² to head_ss
+// ([nv][4] floats), its columns' silu(z)·o·norm_w unnormalized as planes.
+hipError_t launch_gdn_split(dwim_dev *dev, const float *qkv, const float *conv_state, float *conv_state_out,
+                            const float *conv_w, const dwim_weight *w_ab, const float *xw, const Rms &rms,
+                            const float *decay, float *state, const float *z, const float *norm_w, float eps,
+                            size_t nk, size_t nv, size_t head_dim, float *head_ss, int area);
 
 // ---- batches of tokens (k_gemm_q4k.hip) ----
 // out (+)= w · x for n tokens on the f16 matrix cores (x's hi/lo parts are

@@ -60,7 +60,8 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
     dev->mv_tiles_cap = 4096;
     if (hipMalloc(&dev->mv_partials, (size_t)dev->mv_tiles_cap * 4 * 4 * 32 * sizeof(float)) != hipSuccess ||
         hipMalloc(&dev->mv_counters, (size_t)dev->mv_tiles_cap * sizeof(unsigned)) != hipSuccess ||
-        hipMemset(dev->mv_counters, 0, (size_t)dev->mv_tiles_cap * sizeof(unsigned)) != hipSuccess) {
+        hipMemset(dev->mv_counters, 0, (size_t)dev->mv_tiles_cap * sizeof(unsigned)) != hipSuccess ||
+        hipMalloc(&dev->mv_stream, (dev->mv_stream_cap = (size_t)4 << 20) * sizeof(float)) != hipSuccess) {
         dev->refs = 0;
         dwim_dev_release_resources(dev);
         return dwim_fail("allocating the split-product scratch failed");
@@ -118,6 +119,7 @@ void dwim_dev_release_resources(dwim_dev *dev) {
     hipStreamSynchronize(dev->stream);
     if (dev->mv_partials) hipFree(dev->mv_partials);
     if (dev->mv_counters) hipFree(dev->mv_counters);
+    if (dev->mv_stream) hipFree(dev->mv_stream);
     if (dev->chain_ctl) hipFree(dev->chain_ctl);
     if (dev->chain_progress) hipFree(dev->chain_progress);
     if (dev->chain_partials) hipFree(dev->chain_partials);
