@@ -260,8 +260,12 @@ DEV void argmax_merge(float &best, uint32_t &idx, float ov, uint32_t oi) {
     }
 }
 
-// Pass 1: block (part, row) scans its contiguous share of the row, each
-// thread its stride in increasing order, and leaves the part's first maximum.
+constexpr size_t kArgParts = 256;
+
+// Pass 1: block (part, row) scans its contiguous share of the row (a
+// multiple of 4 long when the row is), each thread four values at a time in
+// increasing order, every load of the block issued before the comparisons,
+// and leaves the part's first maximum.
 __global__ void __launch_bounds__(256) k_argmax_part(const float *__restrict__ logits, size_t cols, size_t per,
                                                      float *__restrict__ pv, uint32_t *__restrict__ pi) {
     __shared__ float bv[4];
@@ -271,12 +275,27 @@ __global__ void __launch_bounds__(256) k_argmax_part(const float *__restrict__ l
     const size_t lo = part * per, hi = lo + per < cols ? lo + per : cols;
     float best = -INFINITY;
     uint32_t idx = 0xffffffffu;
-    for (size_t i = lo + threadIdx.x; i < hi; i += 256) {
-        const float v = r[i];
-        if (idx == 0xffffffffu || v > best) {
-            best = v;
-            idx = (uint32_t)i;
+    if (cols % 4 == 0 && per % 4 == 0) {
+        constexpr int kU = 4;  // float4 loads a thread
+        for (size_t b = lo + 4 * threadIdx.x; b < hi; b += 4 * 256 * kU) {
+            float4 v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; u++) {
+                const size_t i = b + (size_t)u * 4 * 256;
+                v[u] = i < hi ? *(const float4 *)(r + i) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            }
+#pragma unroll
+            for (int u = 0; u < kU; u++) {
+                const size_t i = b + (size_t)u * 4 * 256;
+                if (i >= hi) continue;
+                argmax_merge(best, idx, v[u].x, (uint32_t)i);
+                argmax_merge(best, idx, v[u].y, (uint32_t)i + 1);
+                argmax_merge(best, idx, v[u].z, (uint32_t)i + 2);
+                argmax_merge(best, idx, v[u].w, (uint32_t)i + 3);
+            }
         }
+    } else {
+        for (size_t i = lo + threadIdx.x; i < hi; i += 256) argmax_merge(best, idx, r[i], (uint32_t)i);
     }
 #pragma unroll
     for (int m = 32; m > 0; m >>= 1) argmax_merge(best, idx, __shfl_xor(best, m, 64), __shfl_xor(idx, m, 64));
@@ -293,30 +312,41 @@ __global__ void __launch_bounds__(256) k_argmax_part(const float *__restrict__ l
     }
 }
 
-// Pass 2: a wave per row merges its parts (at most 64).
-__global__ void __launch_bounds__(64) k_argmax_merge(const float *__restrict__ pv, const uint32_t *__restrict__ pi,
-                                                     size_t parts, uint32_t *__restrict__ out) {
+// Pass 2: a block per row merges its parts (at most kArgParts).
+__global__ void __launch_bounds__(256) k_argmax_merge(const float *__restrict__ pv, const uint32_t *__restrict__ pi,
+                                                      size_t parts, uint32_t *__restrict__ out) {
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
     const size_t row = blockIdx.x;
-    const int lane = threadIdx.x;
-    float best = lane < (int)parts ? pv[row * parts + lane] : -INFINITY;
-    uint32_t idx = lane < (int)parts ? pi[row * parts + lane] : 0xffffffffu;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float best = threadIdx.x < parts ? pv[row * parts + threadIdx.x] : -INFINITY;
+    uint32_t idx = threadIdx.x < parts ? pi[row * parts + threadIdx.x] : 0xffffffffu;
 #pragma unroll
     for (int m = 32; m > 0; m >>= 1) argmax_merge(best, idx, __shfl_xor(best, m, 64), __shfl_xor(idx, m, 64));
-    if (lane == 0) out[row] = idx == 0xffffffffu ? 0u : idx;
+    if (lane == 0) {
+        bv[wave] = best;
+        bi[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) argmax_merge(best, idx, bv[w], bi[w]);
+        out[row] = idx == 0xffffffffu ? 0u : idx;
+    }
 }
 
-size_t argmax_scratch_words(size_t rows) { return rows * (1 + 2 * 64); }
+size_t argmax_scratch_words(size_t rows) { return rows * (1 + 2 * kArgParts); }
 
 // scratch: argmax_scratch_words(rows) words; the indices land in its first `rows`
 hipError_t launch_argmax(hipStream_t s, const float *logits, size_t rows, size_t cols, uint32_t *scratch) {
-    const size_t parts = cols >= 64 * 1024 ? 64 : (cols + 1023) / 1024;
-    const size_t per = (cols + parts - 1) / parts;
+    // parts of at least 1024 values, a multiple of 4 long
+    const size_t parts = cols >= kArgParts * 1024 ? kArgParts : (cols + 1023) / 1024;
+    const size_t per = ((cols + parts - 1) / parts + 3) / 4 * 4;
     float *pv = (float *)(scratch + rows);
-    uint32_t *pi = scratch + rows + rows * 64;
+    uint32_t *pi = scratch + rows + rows * kArgParts;
     k_argmax_part<<<dim3((unsigned)parts, (unsigned)rows), 256, 0, s>>>(logits, cols, per, pv, pi);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_argmax_merge<<<(unsigned)rows, 64, 0, s>>>(pv, pi, parts, scratch);
+    k_argmax_merge<<<(unsigned)rows, 256, 0, s>>>(pv, pi, parts, scratch);
     return hipGetLastError();
 }
 

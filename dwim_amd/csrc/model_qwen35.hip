@@ -601,6 +601,14 @@ struct dwim_model {
         const size_t h = c.hidden;
         if (!has_draft) {
             if (!wanted) return finish();
+            if (n == 1 && head->fmt == DWIM_Q6_K && h % 256 == 0 && h <= planes::kMaxCols) {
+                // the output norm inside the head's planes (one launch
+                // instead of a copy, an RMS norm and the planes)
+                DWIM_HIP(launch_planes(dev, x->data, h, norm->data, c.eps, nullptr, 0, 0));
+                TRY(dwim_resize(dev, logits, c.vocab));
+                DWIM_HIP(launch_mv_q6k_mfma(dev, head, logits->data, 0));
+                return read_logits(logits_out, greedy);
+            }
             TRY(dwim_resize(dev, xb, h));
             TRY(dwim_resize(dev, xh, h));
             TRY(dwim_copy(dev, xb, 0, x, (n - 1) * h, h));
