@@ -187,9 +187,10 @@ __global__ void __launch_bounds__(kT) k_gdn(const GdnArgs a) {
 // each workgroup writes silu(z)·o·norm_w of its columns, unnormalized, with
 // their planes, and its Σo² to head_ss[h][quarter]; the product that reads
 // the planes multiplies each group's scale and sum by the head's
-// 1/sqrt(Σ head_ss / 128 + eps), which is the same product.  Every workgroup
-// recomputes the head's gate logits, and the conv and l2 norms of its key
-// head's q and k (the v channels: only its own 32).
+// 1/sqrt(Σ head_ss / 128 + eps), which is the same product.  The gate
+// logits come from the qkv product's launch (W_ab · x·attn_norm) and are
+// RMS-scaled here; every workgroup recomputes the conv and l2 norms of its
+// key head's q and k (the v channels: only its own 32).
 constexpr int kQuarters = 4;
 constexpr int kCols = kD / kQuarters;     // value columns a workgroup
 constexpr int kST = 256;                  // threads: (column, key part) pairs
@@ -201,8 +202,7 @@ struct GdnSplitArgs {
     const float *conv_state;
     float *conv_state_out;
     const float *conv_w;
-    const uint16_t *w_ab;
-    const float *xw;
+    const float *ab;           // [2·nv]: W_ab · x·attn_norm, not yet RMS-scaled
     Rms rms;
     const float *decay;
     float *state;
@@ -210,14 +210,14 @@ struct GdnSplitArgs {
     const float *norm_w;       // [D]
     float *head_ss;            // [nv][4]: each quarter's Σo²
     float eps;
-    unsigned nk, nv, cols;
+    unsigned nk, nv;
     planes::View out;
 };
 
 __global__ void __launch_bounds__(kST) k_gdn_split(const GdnSplitArgs a) {
     __shared__ float part[2][kSParts][kCols];
     __shared__ float qs[kD], ks[kD], vs[kCols];
-    __shared__ float red[5][kST / 64];
+    __shared__ float red[4][kST / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const unsigned h = blockIdx.x / kQuarters, qd = blockIdx.x % kQuarters, c0 = qd * kCols;
     const unsigned kh = h / (a.nv / a.nk);
@@ -235,18 +235,7 @@ __global__ void __launch_bounds__(kST) k_gdn_split(const GdnSplitArgs a) {
     const float vx = a.qkv[vchan];
     const float v0s = a.conv_state[vchan], v1s = a.conv_state[ch + vchan], v2s = a.conv_state[2 * ch + vchan];
     const float4 vcw = ((const float4 *)a.conv_w)[vchan];
-    // gate rows: 8 columns of both rows a load, up to 3 loads a thread
-    const unsigned n8 = a.cols / 8;
-    uint4 wa[3], wb[3];
-    float4 xa[3], xb[3];
-#pragma unroll
-    for (int u = 0; u < 3; u++) {
-        const unsigned e = (unsigned)tid + kST * u, ec = e < n8 ? e : 0u;
-        wa[u] = ((const uint4 *)(a.w_ab + (size_t)h * a.cols))[ec];
-        wb[u] = ((const uint4 *)(a.w_ab + (size_t)(a.nv + h) * a.cols))[ec];
-        xa[u] = ((const float4 *)a.xw)[2 * ec];
-        xb[u] = ((const float4 *)a.xw)[2 * ec + 1];
-    }
+    const float la = a.ab[h], lb = a.ab[a.nv + h];
     float ssp = 0.0f;
     for (unsigned g = (unsigned)tid; g < a.rms.groups; g += kST) ssp += a.rms.ss[g];
     const int c = tid % kCols, p = tid / kCols;
@@ -275,33 +264,19 @@ __global__ void __launch_bounds__(kST) k_gdn_split(const GdnSplitArgs a) {
         a.conv_state_out[2 * ch + vchan] = vx;
     }
 
-    // ---- one block reduction: gate logits, RMS sum, |q|² (waves 0-1), |k|² (2-3)
-    float da = 0.0f, db = 0.0f;
-#pragma unroll
-    for (int u = 0; u < 3; u++) {
-        if ((unsigned)tid + kST * u >= n8) continue;
-        const uint32_t pa[4] = {wa[u].x, wa[u].y, wa[u].z, wa[u].w}, pb[4] = {wb[u].x, wb[u].y, wb[u].z, wb[u].w};
-        const float xs[8] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            da += bf16f((uint16_t)(pa[i] & 0xffffu)) * xs[2 * i] + bf16f((uint16_t)(pa[i] >> 16)) * xs[2 * i + 1];
-            db += bf16f((uint16_t)(pb[i] & 0xffffu)) * xs[2 * i] + bf16f((uint16_t)(pb[i] >> 16)) * xs[2 * i + 1];
-        }
-    }
+    // ---- one block reduction: the RMS sum, |q|² (waves 0-1), |k|² (2-3)
     {
-        const float v[4] = {da, db, ssp, y * y};
+        const float v[2] = {ssp, y * y};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 2; i++) {
             const float t = group_sum<64>(v[i]);
-            if (lane == 0) red[i][wave] = t;
+            if (lane == 0) red[2 + i][wave] = t;
         }
     }
     __syncthreads();
-    float sums[3];
-#pragma unroll
-    for (int i = 0; i < 3; i++) sums[i] = (red[i][0] + red[i][1]) + (red[i][2] + red[i][3]);
-    const float gs = 1.0f / sqrtf(sums[2] / a.rms.cols + a.rms.eps);
-    const float alpha = gs * sums[0], beta = sigmoidf_(gs * sums[1]);
+    const float ss = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
+    const float gs = 1.0f / sqrtf(ss / a.rms.cols + a.rms.eps);
+    const float alpha = gs * la, beta = sigmoidf_(gs * lb);
     const float g = expf(dec_a * softplusf_(alpha + dec_dt));
     if (tid < kD) qs[tid] = y * (1.0f / sqrtf((red[3][0] + red[3][1]) + a.eps));
     else ks[tid - kD] = y * (1.0f / sqrtf((red[3][2] + red[3][3]) + a.eps));
@@ -380,20 +355,17 @@ hipError_t launch_gdn(dwim_dev *dev, const float *qkv, const float *conv_state, 
 }
 
 hipError_t launch_gdn_split(dwim_dev *dev, const float *qkv, const float *conv_state, float *conv_state_out,
-                            const float *conv_w, const dwim_weight *w_ab, const float *xw, const Rms &rms,
-                            const float *decay, float *state, const float *z, const float *norm_w, float eps,
-                            size_t nk, size_t nv, size_t head_dim, float *head_ss, int area) {
-    if (head_dim != kD || nk == 0 || nv % nk || w_ab->fmt != DWIM_BF16 || w_ab->rows != 2 * nv ||
-        w_ab->cols % 8 || w_ab->cols / 8 > 3 * kST || !rms.ss || area < 0 || !head_ss)
-        return hipErrorInvalidValue;
+                            const float *conv_w, const float *ab, const Rms &rms, const float *decay, float *state,
+                            const float *z, const float *norm_w, float eps, size_t nk, size_t nv, size_t head_dim,
+                            float *head_ss, int area) {
+    if (head_dim != kD || nk == 0 || nv % nk || !rms.ss || area < 0 || !head_ss || !ab) return hipErrorInvalidValue;
     if (nv * kD > planes::kMaxCols || (nv * kD) % 256) return hipErrorInvalidValue;
     GdnSplitArgs a{};
     a.qkv = qkv;
     a.conv_state = conv_state;
     a.conv_state_out = conv_state_out;
     a.conv_w = conv_w;
-    a.w_ab = (const uint16_t *)w_ab->q;
-    a.xw = xw;
+    a.ab = ab;
     a.rms = rms;
     a.decay = decay;
     a.state = state;
@@ -403,7 +375,6 @@ hipError_t launch_gdn_split(dwim_dev *dev, const float *qkv, const float *conv_s
     a.eps = eps;
     a.nk = (unsigned)nk;
     a.nv = (unsigned)nv;
-    a.cols = (unsigned)w_ab->cols;
     a.out = planes_area(dev, area, nv * kD);
     dev->prepared = 0;
     k_gdn_split<<<(unsigned)(nv * kQuarters), kST, 0, dev->stream>>>(a);

@@ -133,7 +133,45 @@ struct Args {
     const float4 *head_ss;
     unsigned head_dim;
     float head_eps;
+    // given: the first bf_groups workgroups (dispatched first, so that they
+    // are done long before the matrices' last) compute out = W·x for a small
+    // bf16 matrix [bf_rows][bf_cols] and f32 x, a wave a row
+    const uint16_t *bf_w;
+    const float *bf_x;
+    float *bf_out;
+    unsigned bf_rows, bf_cols, bf_groups;
 };
+
+// A wave's row of a small bf16 matrix against f32 x (cols a multiple of 8):
+// 8 columns a lane a load, the loads of 5 such steps issued together.
+DEV void bf16_row(const Args &a, unsigned row, int lane) {
+    const uint4 *w = (const uint4 *)(a.bf_w + (size_t)row * a.bf_cols);
+    const float4 *x = (const float4 *)a.bf_x;
+    const unsigned n8 = a.bf_cols / 8;
+    float acc = 0.0f;
+    for (unsigned c0 = (unsigned)lane; c0 < n8; c0 += 5 * 64) {
+        uint4 wv[5];
+        float4 x0[5], x1[5];
+#pragma unroll
+        for (int u = 0; u < 5; u++) {
+            const unsigned c = c0 + 64u * u < n8 ? c0 + 64u * u : c0;
+            wv[u] = w[c];
+            x0[u] = x[2 * c];
+            x1[u] = x[2 * c + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 5; u++) {
+            if (c0 + 64u * u >= n8) continue;
+            const uint32_t pw[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+            const float xs[8] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w, x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                acc += __uint_as_float(pw[i] << 16) * xs[2 * i] + __uint_as_float(pw[i] & 0xffff0000u) * xs[2 * i + 1];
+        }
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) a.bf_out[row] = acc;
+}
 
 // Per wave LDS, in 16-byte chunks: the planes of its K blocks (chunk
 // 48i + 16p + c holds activations 16c..16c+15 of digit p of block i), the
@@ -158,10 +196,16 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     extern __shared__ uint4 lds_all[];
     __shared__ float red[16][16];
     const int lane = threadIdx.x & 63, wave_all = threadIdx.x >> 6, kq = lane >> 4, c = lane & 15;
+    if (blockIdx.x < a.bf_groups) {
+        // the small bf16 matrix's rows, a wave each
+        const unsigned row = blockIdx.x * (blockDim.x / 64) + (unsigned)wave_all;
+        if (row < a.bf_rows) bf16_row(a, row, lane);
+        return;
+    }
     // every argument is read up front and selected without branches, so that
     // the scalar loads of the kernel arguments issue together; a launch's
     // unused first[] entries are all ones
-    const unsigned S = a.S, P = a.P, nb = a.nb, bx = blockIdx.x;
+    const unsigned S = a.S, P = a.P, nb = a.nb, bx = blockIdx.x - a.bf_groups;
     const unsigned f1 = a.first[1], f2 = a.first[2], f3 = a.first[3];
     const int j = (int)(bx >= f1) + (int)(bx >= f2) + (int)(bx >= f3);
     const unsigned wg = bx - (j == 0 ? 0u : j == 1 ? f1 : j == 2 ? f2 : f3);
@@ -694,6 +738,8 @@ hipError_t run(dwim_dev *dev, Args a, unsigned njobs, const size_t *rows) {
     a.first[0] = 0;
     a.partials = dev->mv_partials;
     a.counters = dev->mv_counters;
+    a.bf_groups = a.bf_w ? (a.bf_rows + waves - 1) / waves : 0u;
+    total += a.bf_groups;
     switch (pl.K) {
         case 1: return go<1>(dev, a, total, waves);
         case 2: return go<2>(dev, a, total, waves);
@@ -787,6 +833,15 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
     if (swiglu && ws[0]->rows != ws[1]->rows) return hipErrorInvalidValue;
     a.swiglu = swiglu;
     if (extra) {
+        if (extra->bf16) {
+            const dwim_weight *b = extra->bf16;
+            if (b->fmt != DWIM_BF16 || b->cols % 8 || !extra->bf16_x || !extra->bf16_out) return hipErrorInvalidValue;
+            a.bf_w = (const uint16_t *)b->q;
+            a.bf_x = extra->bf16_x;
+            a.bf_out = extra->bf16_out;
+            a.bf_rows = (unsigned)b->rows;
+            a.bf_cols = (unsigned)b->cols;
+        }
         if (extra->head_ss) {
             if (extra->head_dim % 64 || cols % extra->head_dim) return hipErrorInvalidValue;
             a.head_ss = (const float4 *)extra->head_ss;

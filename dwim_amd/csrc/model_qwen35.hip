@@ -352,12 +352,20 @@ struct dwim_model {
         return 0;
     }
     // products of the layer input (area 0, RMS-scaled)
-    int from_input(const dwim_weight *const *ws, dwim_buf *const *outs, int count) {
+    // (bf16 given: the same launch also writes bf16_out = bf16 · xh, the
+    // DeltaNet gate logits from x·attn_norm, not yet RMS-scaled)
+    int from_input(const dwim_weight *const *ws, dwim_buf *const *outs, int count, const dwim_weight *bf16 = nullptr,
+                   dwim_buf *bf16_out = nullptr) {
         float *o[4];
         for (int i = 0; i < count; i++) o[i] = outs[i]->data;
         MvExtra e;
         e.rms = 1;
         e.eps = c.eps;
+        if (bf16) {
+            e.bf16 = bf16;
+            e.bf16_x = xh->data;
+            e.bf16_out = bf16_out->data;
+        }
         DWIM_HIP(launch_mv_q4k_mfma(dev, ws, o, nullptr, count, 0, 0, &e));
         return 0;
     }
@@ -400,13 +408,14 @@ struct dwim_model {
             dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
             const dwim_weight *ws[2] = {l.qkv, l.z};
             dwim_buf *outs[2] = {qkv, z};
-            TRY(from_input(ws, outs, 2));
-            // the gate projection, conv, delta rule and gated output in one
-            // launch of 4 workgroups a head, the gate logits from
-            // x·attn_norm (xh) RMS-scaled; the head's RMS norm of o is
-            // applied by the output product (its Σo² in head_ss)
-            DWIM_HIP(launch_gdn_split(dev, qkv->data, state->data, state_out->data, l.conv->data, l.ab, xh->data,
-                                      rms0(), l.decay->data, seq.ssm_state[l.slot]->data, z->data, l.norm->data, eps,
+            TRY(dwim_resize(dev, ab, 2 * c.v_heads));
+            TRY(from_input(ws, outs, 2, l.ab, ab));
+            // conv, delta rule and gated output in one launch of 4
+            // workgroups a head, the gate logits (ab) RMS-scaled there; the
+            // head's RMS norm of o is applied by the output product (its Σo²
+            // in head_ss)
+            DWIM_HIP(launch_gdn_split(dev, qkv->data, state->data, state_out->data, l.conv->data, ab->data, rms0(),
+                                      l.decay->data, seq.ssm_state[l.slot]->data, z->data, l.norm->data, eps,
                                       c.k_heads, c.v_heads, c.state_dim, head_ss->data, 1));
             TRY(add_handover(l.out, 1, 0, l.mlp_norm, nullptr, head_ss));
         }

@@ -164,6 +164,11 @@ struct MvExtra {
     const float *head_ss = nullptr;
     size_t head_dim = 0;
     float head_eps = 0.0f;
+    // given: the same launch also computes bf16_out = bf16 · bf16_x (a small
+    // bf16 matrix against f32 x, in workgroups of its own)
+    const dwim_weight *bf16 = nullptr;
+    const float *bf16_x = nullptr;
+    float *bf16_out = nullptr;
 };
 hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                               int count, int swiglu, int area, const MvExtra *extra = nullptr);
@@ -278,13 +283,15 @@ hipError_t launch_gdn(dwim_dev *dev, const float *qkv, const float *conv_state, 
                       const float *conv_w, const dwim_weight *w_ab, const float *xw, const Rms &rms,
                       const float *decay, float *state, float *z, const float *norm_w, float eps, size_t nk,
                       size_t nv, size_t head_dim, int area);
-// The same step over 4 workgroups a head, the RMS norm of o left to the
-// product that reads the planes (area): each quarter's Σo² to head_ss
-// ([nv][4] floats), its columns' silu(z)·o·norm_w unnormalized as planes.
+// The same step over 4 workgroups a head, from gate logits ab = W_ab ·
+// x·attn_norm computed beforehand (not yet RMS-scaled), the RMS norm of o
+// left to the product that reads the planes (area): each quarter's Σo² to
+// head_ss ([nv][4] floats), its columns' silu(z)·o·norm_w unnormalized as
+// planes.
 hipError_t launch_gdn_split(dwim_dev *dev, const float *qkv, const float *conv_state, float *conv_state_out,
-                            const float *conv_w, const dwim_weight *w_ab, const float *xw, const Rms &rms,
-                            const float *decay, float *state, const float *z, const float *norm_w, float eps,
-                            size_t nk, size_t nv, size_t head_dim, float *head_ss, int area);
+                            const float *conv_w, const float *ab, const Rms &rms, const float *decay, float *state,
+                            const float *z, const float *norm_w, float eps, size_t nk, size_t nv, size_t head_dim,
+                            float *head_ss, int area);
 
 // ---- batches of tokens (k_gemm_q4k.hip) ----
 // out (+)= w · x for n tokens on the f16 matrix cores (x's hi/lo parts are
