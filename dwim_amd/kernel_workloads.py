@@ -1,6 +1,7 @@
 """Workloads for counter runs of single kernels (rocprofv3 --pmc / --kernel-trace).
 
     python -m dwim_amd.kernel_workloads attention [--reps N]
+    python -m dwim_amd.kernel_workloads tokens [--reps N]
 
 `attention`: first a device copy of 256 MiB (four times), the calibration
 of the FETCH_SIZE / WRITE_SIZE counters; then one-token GQA decode (24 query heads, 4 key/value heads of 256,
@@ -8,6 +9,10 @@ the 27B shape's attention layer) over Q8 caches filled with N(0, 1) keys and
 values at context depths 4096, 32768 and 131072, `reps` calls at each depth
 (k_attn_partial + k_attn_combine), each depth's caches distinct; then the
 same over f16 caches.  Every call goes through the C ABI (dwim_attention).
+
+`tokens`: the 4-token Q4_K product (a speculative-decoding verify batch,
+k_planes then k_mv_stream<4>) on the 27B shape's 17408x5120 and 5120x17408
+matrices (synthetic weights), `reps` calls each, through dwim_matmul.
 """
 from __future__ import annotations
 
@@ -43,12 +48,27 @@ def attention(reps: int) -> None:
     dev.close()
 
 
+def tokens(reps: int) -> None:
+    dev = D.Hip(0)
+    n = 4
+    for rows, cols in ((17408, 5120), (5120, 17408)):
+        w = dev.upload_synthetic(D.Q4_K, rows, cols, seed=5, sigma=0.02)
+        x = dev.buffer(D.synthetic_values(9, 0, n * cols, 1.0))
+        out = dev.alloc(n * rows)
+        for _ in range(reps):
+            dev.matmul(out, w, x)
+        dev.sync()
+        print(f"tokens {rows}x{cols} n={n}: {reps} calls", flush=True)
+        del w, x, out
+    dev.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=["attention"])
+    ap.add_argument("workload", choices=["attention", "tokens"])
     ap.add_argument("--reps", type=int, default=20)
     a = ap.parse_args()
-    attention(a.reps)
+    {"attention": attention, "tokens": tokens}[a.workload](a.reps)
 
 
 if __name__ == "__main__":
