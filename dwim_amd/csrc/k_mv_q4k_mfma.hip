@@ -700,11 +700,16 @@ struct Plan {
     unsigned S, P;
 };
 
-Plan plan(unsigned nb, unsigned tiles) {
+Plan plan(unsigned nb, unsigned tiles, bool swiglu) {
     Plan p{tiles >= 512 ? 5 : 3, 0, 1};
     if ((unsigned)p.K > nb) p.K = (int)nb;
     const unsigned ranges = (nb + p.K - 1) / p.K;
     while ((ranges + p.P - 1) / p.P > 8 && p.P < (unsigned)kMaxParts) p.P++;
+    // a large SwiGLU pair: its 8-wave workgroups (2 a CU resident) would
+    // run in 2.1 rounds; halves of tiles in 4-wave workgroups (5 a CU) make
+    // 1.7 and lose less to the last round than the meeting costs
+    // (17408x5120: 27.8 -> 26.4 us alone, 53 us a token in the 27B decode)
+    if (swiglu && tiles >= 512 && ranges >= 4 && p.P == 1) p.P = 2;
     p.S = (ranges + p.P - 1) / p.P;
     return p;
 }
@@ -719,7 +724,7 @@ hipError_t go(dwim_dev *dev, const Args &a, unsigned grid, unsigned waves) {
 hipError_t run(dwim_dev *dev, Args a, unsigned njobs, const size_t *rows) {
     unsigned tiles = 0;
     for (unsigned j = 0; j < njobs; j++) tiles += (unsigned)q4kt::tiles(rows[j]);
-    const Plan pl = plan(a.nb, tiles);
+    const Plan pl = plan(a.nb, tiles, a.swiglu != 0);
     a.S = pl.S;
     a.P = pl.P;
     if (a.P > 1 && tiles > dev->mv_tiles_cap) a.P = 1, a.S = (a.nb + pl.K - 1) / pl.K;
