@@ -174,20 +174,28 @@ DEV void bf16_row(const Args &a, unsigned row, int lane) {
 }
 
 // Per wave LDS, in 16-byte chunks: the planes of its K blocks (chunk
-// 48i + 16p + c holds activations 16c..16c+15 of digit p of block i), the
-// group statistics (chunks 8i + 2k and 8i + 2k + 1: scales and sums of groups
-// 4k..4k+3 of block i), two zero chunks and the decoded scales ([group][row]
-// floats).
+// 51i + 17p + c holds activations 16c..16c+15 of digit p of block i: each
+// digit's 16 chunks padded by one, so that the 12 lanes reading B operands,
+// chunks 17p + 4k + const, fall in distinct banks), the group statistics
+// (chunks 8i + 2k and 8i + 2k + 1: scales and sums of groups 4k..4k+3 of
+// block i), two zero chunks and the decoded scales ([group][row] floats,
+// rows of 20 floats: the float4 reads of 16 (group, row-quad) pairs and the
+// writes of 4 groups of 16 rows then spread over the banks).
 // The plane loads come in whole waves of 64 chunks; the spare ones past
 // K·48 are stored into the statistics area, which is written after them.
 template <int K>
 struct Lds {
+    static constexpr int kPStride = 17;
+    static constexpr int kBlk = 3 * kPStride;
     static constexpr int kPlaneLoads = (K * 48 + 63) / 64;
-    static constexpr int kStat = K * 48;
+    static constexpr int kStat = K * kBlk;
     static constexpr int kZero = kStat + 64;
     static constexpr int kHdr = kZero + 2;
-    static constexpr int kChunks = kHdr + 16 * 16 / 4;
-    static_assert(kPlaneLoads * 64 <= kZero, "spare plane chunks must land in the statistics area");
+    static constexpr int kHdrStride = 20;
+    static constexpr int kChunks = kHdr + 16 * kHdrStride / 4;
+    // chunk ci of the loads (48 a block, 16 a digit) lands at ci + ci / 16
+    static constexpr int kLastSpare = kPlaneLoads * 64 - 1 + (kPlaneLoads * 64 - 1) / 16;
+    static_assert(kLastSpare < kZero, "spare plane chunks must land in the statistics area");
 };
 
 template <int K>
@@ -269,7 +277,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     // let the compiler sink its load behind the weights); the statistics
     // then overwrite the spares
 #pragma unroll
-    for (int u = 0; u < kPlaneLoads; u++) my[lane + 64 * u] = xc[u];
+    for (int u = 0; u < kPlaneLoads; u++) my[lane + 64 * u + ((lane + 64 * u) >> 4)] = xc[u];
     if (a.head_ss) {
         const float f = 1.0f / sqrtf(((hss.x + hss.y) + (hss.z + hss.w)) / (float)a.head_dim + a.head_eps);
         st.x *= f;
@@ -285,7 +293,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     // B: lane (k-group kq, column c) carries digit c % 3 of sub-block 2·kq + h
     // when c / 3 == kq, else the zero chunks
     const bool active = c < 12 && c / 3 == kq;
-    const int bsel = active ? 16 * (c % 3) + 4 * kq : 0;
+    const int bsel = active ? L::kPStride * (c % 3) + 4 * kq : 0;
     const int gcol = 4 * (c < 12 ? c / 3 : 0);  // the column's first group of 16
     const int k4 = lane & 3, R4 = lane >> 2;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -308,10 +316,10 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
             // scale is d·sc/16 and 8·d·sc joins the min term
             macc += (dmin * mn0) * (xm.x + xm.y) + (dmin * mn1 - 8.0f * D1) * (xm.z + xm.w);
             const float D1h = D1 * 0.0625f;
-            hdr[(4 * k4) * 16 + R4] = D0 * xs.x;
-            hdr[(4 * k4 + 1) * 16 + R4] = D0 * xs.y;
-            hdr[(4 * k4 + 2) * 16 + R4] = D1h * xs.z;
-            hdr[(4 * k4 + 3) * 16 + R4] = D1h * xs.w;
+            hdr[(4 * k4) * L::kHdrStride + R4] = D0 * xs.x;
+            hdr[(4 * k4 + 1) * L::kHdrStride + R4] = D0 * xs.y;
+            hdr[(4 * k4 + 2) * L::kHdrStride + R4] = D1h * xs.z;
+            hdr[(4 * k4 + 3) * L::kHdrStride + R4] = D1h * xs.w;
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -319,7 +327,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
         for (int h = 0; h < 2; h++) {
             // the two MFMAs of a half cover its two groups of 16, each summed
             // apart to take its own activation scale
-            const uint4 *xv = my + (active ? 48 * i + 2 * h + bsel : L::kZero);
+            const uint4 *xv = my + (active ? L::kBlk * i + 2 * h + bsel : L::kZero);
             const uint32_t mask = h ? 0xf0f0f0f0u : 0x0f0f0f0fu;
 #pragma unroll
             for (int m = 0; m < 2; m++) {
@@ -327,7 +335,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
                 const v4i av = {(int)(q.x & mask), (int)(q.y & mask), (int)(q.z & mask), (int)(q.w & mask)};
                 const v4i bv = {(int)xq.x, (int)xq.y, (int)xq.z, (int)xq.w};
                 const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, v4i{0, 0, 0, 0}, 0, 0, 0);
-                const float4 D = *(const float4 *)&hdr[(gcol + 2 * h + m) * 16 + 4 * kq];
+                const float4 D = *(const float4 *)&hdr[(gcol + 2 * h + m) * L::kHdrStride + 4 * kq];
                 acc[0] += D.x * (float)C[0];
                 acc[1] += D.y * (float)C[1];
                 acc[2] += D.z * (float)C[2];
@@ -717,6 +725,13 @@ Plan plan(unsigned nb, unsigned tiles, bool swiglu) {
 template <int K>
 hipError_t go(dwim_dev *dev, const Args &a, unsigned grid, unsigned waves) {
     const size_t lds = (size_t)waves * Lds<K>::kChunks * 16;
+    static bool raised = false;  // past 64 KB (up to 16 waves) the launch needs the attribute
+    if (!raised) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_mv_q4k_mfma<K>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)(16 * Lds<K>::kChunks * 16));
+        if (e != hipSuccess) return e;
+        raised = true;
+    }
     k_mv_q4k_mfma<K><<<grid, waves * 64, lds, dev->stream>>>(a);
     return hipGetLastError();
 }
