@@ -40,6 +40,7 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -233,7 +234,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     // every load of the wave is issued before any compute: the planes and
     // statistics of its blocks first, then the weights
     constexpr int kPlaneLoads = L::kPlaneLoads;
-    uint4 xc[kPlaneLoads];
+    v4u xc[kPlaneLoads];  // (a vector type: uint4 copies went through private memory)
     const unsigned cols = nb * 256;
 #pragma unroll
     for (int u = 0; u < kPlaneLoads; u++) {
@@ -241,7 +242,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
         const int ci0 = lane + 64 * u;
         const int ci = ci0 < nblk * 48 ? ci0 : 0;
         const unsigned i = (unsigned)ci / 48u, p = ((unsigned)ci % 48u) / 16u, part16 = (unsigned)ci % 16u;
-        xc[u] = *(const uint4 *)(a.xq + p * cols + (b0 + i) * 256u + 16u * part16);
+        xc[u] = *(const v4u *)(a.xq + p * cols + (b0 + i) * 256u + 16u * part16);
     }
     const unsigned sti = b0 * 8u + (lane < nblk * 8 ? (unsigned)lane : 0u);
     float4 st = a.xstat[sti];
@@ -264,6 +265,11 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     const unsigned orow_c = orow < orows ? orow : 0u;
     const float old_out = (a.add_mask >> j) & 1u ? obase[orow_c] : 0.0f;
     const float next_w = a.emit_norm ? a.emit_norm[orow_c] : 0.0f;
+    // (no memory access or instruction crosses this point: the compiler
+    // would otherwise move plane loads behind the weights, so that the first
+    // block's wait for the planes waits for most of the weights too, or the
+    // planes' LDS stores, and their wait, ahead of the other loads)
+    asm volatile("");
     uint4 wq[K][2];
     uint32_t hw[K];
 #pragma unroll
@@ -277,7 +283,7 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     // let the compiler sink its load behind the weights); the statistics
     // then overwrite the spares
 #pragma unroll
-    for (int u = 0; u < kPlaneLoads; u++) my[lane + 64 * u + ((lane + 64 * u) >> 4)] = xc[u];
+    for (int u = 0; u < kPlaneLoads; u++) ((v4u *)my)[lane + 64 * u + ((lane + 64 * u) >> 4)] = xc[u];
     if (a.head_ss) {
         const float f = 1.0f / sqrtf(((hss.x + hss.y) + (hss.z + hss.w)) / (float)a.head_dim + a.head_eps);
         st.x *= f;
