@@ -55,7 +55,16 @@ constexpr int k_of(int nt) { return nt >= 4 ? 2 : 3; }
 constexpr int kJobs = 4;
 constexpr int kTok = 4;
 constexpr int kParts = 4;
-constexpr int kHdrChunks = 32;   // per wave: d·sc of the 8 sub-blocks × 16 rows (floats)
+// per wave: d·sc of the 8 sub-blocks × 16 rows (floats), rows of kHdrStride
+// floats so that the float4 reads of 16 (sub-block, row-quad) pairs and the
+// writes of 4 sub-blocks of 16 rows spread over the banks
+constexpr int kHdrStride = 24;
+constexpr int kHdrChunks = 8 * kHdrStride / 4;
+// the planes of a (block, token): 3 digits of 16 chunks, each padded by one,
+// so that the 12 lanes reading B operands (chunks 17p + 4k + const) fall in
+// distinct banks; staged chunk s of the unpadded layout lands at s + s / 16
+constexpr int kPStride = 17;
+constexpr int kBT = 3 * kPStride;
 // LDS for one part's planes and statistics: at most this many bytes
 constexpr size_t kPlaneBudget = 96 * 1024;
 
@@ -148,11 +157,11 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
     const unsigned i1 = (unsigned)((unsigned long long)(gp + 1) * Ip / G);
     const unsigned cols = nb * 256;
 
-    // LDS: planes [block][token][48 chunks], statistics [block][token][8],
+    // LDS: planes [block][token][51 chunks], statistics [block][token][8],
     // the zero region, per wave the decoded scales, the items' sums
-    const unsigned kStat = a.plane_cap * NT * 48;
+    const unsigned kStat = a.plane_cap * NT * kBT;
     const unsigned kZero = kStat + a.plane_cap * NT * 8;
-    const unsigned kHdr = kZero + kK * NT * 48;
+    const unsigned kHdr = kZero + kK * NT * kBT;
     const unsigned kSlots = kHdr + kW * kHdrChunks;
     v4i *lv = (v4i *)lds;
     const float4 *stl = (const float4 *)(lds + kStat);
@@ -215,22 +224,23 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
                     const float4 xm = stl[(bl * NT + t) * 8 + 2 * k4 + 1];
                     macc[t] += mA * (xm.x + xm.y) + mB * (xm.z + xm.w);
                 }
-                hdr[(2 * k4) * 16 + R4] = D0;
-                hdr[(2 * k4 + 1) * 16 + R4] = D1 * 0.0625f;
+                hdr[(2 * k4) * kHdrStride + R4] = D0;
+                hdr[(2 * k4 + 1) * kHdrStride + R4] = D1 * 0.0625f;
             }
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            const v4i *bbase = lv + (active ? (int)(bl * NT * 48) + 16 * (c % 3) + 4 * kq : (int)kZero + u * NT * 48);
+            const v4i *bbase =
+                lv + (active ? (int)(bl * NT * kBT) + kPStride * (c % 3) + 4 * kq : (int)kZero + u * NT * kBT);
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const uint32_t mask = h ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-                const float4 Dsb = *(const float4 *)&hdr[(2 * gcol + h) * 16 + 4 * kq];
+                const float4 Dsb = *(const float4 *)&hdr[(2 * gcol + h) * kHdrStride + 4 * kq];
                 const v4u q0 = R.q[u][0], q1 = R.q[u][1];
                 const v4i a0 = {(int)(q0.x & mask), (int)(q0.y & mask), (int)(q0.z & mask), (int)(q0.w & mask)};
                 const v4i a1 = {(int)(q1.x & mask), (int)(q1.y & mask), (int)(q1.z & mask), (int)(q1.w & mask)};
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
-                    const v4i *bp = bbase + t * 48 + 2 * h;
+                    const v4i *bp = bbase + t * kBT + 2 * h;
                     v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
                     C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bp[1], C, 0, 0, 0);
                     // token t's scale of sub-block 2·gcol + h
@@ -301,9 +311,9 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
 #pragma unroll
         for (int u = 0; u < kPL; u++) {
             const unsigned gi = threadIdx.x + 1024u * u;
-            if (gi < nplane + nstat) lv[gi < nplane ? gi : kStat + (gi - nplane)] = v[u];
+            if (gi < nplane + nstat) lv[gi < nplane ? gi + (gi >> 4) : kStat + (gi - nplane)] = v[u];
         }
-        if (threadIdx.x < (unsigned)(kK * NT * 48)) lv[kZero + threadIdx.x] = v4i{0, 0, 0, 0};
+        if (threadIdx.x < (unsigned)(kK * NT * kBT)) lv[kZero + threadIdx.x] = v4i{0, 0, 0, 0};
     }
     __syncthreads();
 
@@ -429,7 +439,7 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
     }
     if (TT > dev->mv_tiles_cap) return hipErrorInvalidValue;
     // parts: as few as keep a part's planes within the LDS budget
-    const size_t per_block = (size_t)NT * (48 + 8) * 16;
+    const size_t per_block = (size_t)NT * (kBT + 8) * 16;
     const unsigned pb_max = (unsigned)(kPlaneBudget / per_block);
     a.P = (a.nb + pb_max - 1) / pb_max;
     if (a.P > (unsigned)kParts) return hipErrorInvalidValue;
@@ -479,7 +489,7 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
         a.xq[t] = xq[t];
         a.xstat[t] = xstat[t];
     }
-    const size_t lds = ((size_t)plane_cap * NT * 56 + (size_t)K * NT * 48 + (size_t)kW * kHdrChunks) * 16 +
+    const size_t lds = ((size_t)plane_cap * NT * (kBT + 8) + (size_t)K * NT * kBT + (size_t)kW * kHdrChunks) * 16 +
                        (size_t)items_cap * NT * 16 * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     static bool raised[kTok + 1] = {};
