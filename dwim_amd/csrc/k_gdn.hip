@@ -236,8 +236,11 @@ __global__ void __launch_bounds__(kST) k_gdn_split(const GdnSplitArgs a) {
     const float v0s = a.conv_state[vchan], v1s = a.conv_state[ch + vchan], v2s = a.conv_state[2 * ch + vchan];
     const float4 vcw = ((const float4 *)a.conv_w)[vchan];
     const float la = a.ab[h], lb = a.ab[a.nv + h];
-    float ssp = 0.0f;
-    for (unsigned g = (unsigned)tid; g < a.rms.groups; g += kST) ssp += a.rms.ss[g];
+    // (two loads a thread, unrolled: a load in a loop waits for itself, and
+    // the state loads behind it would wait for that too)
+    const unsigned g1 = (unsigned)tid + kST;
+    const float ss0 = (unsigned)tid < a.rms.groups ? a.rms.ss[tid] : 0.0f;
+    const float ss1 = g1 < a.rms.groups ? a.rms.ss[g1] : 0.0f;
     const int c = tid % kCols, p = tid / kCols;
     const float zc = a.z[h * kD + c0 + c], nwc = a.norm_w[c0 + c];
     const float dec_a = a.decay[h], dec_dt = a.decay[a.nv + h];
@@ -266,7 +269,7 @@ __global__ void __launch_bounds__(kST) k_gdn_split(const GdnSplitArgs a) {
 
     // ---- one block reduction: the RMS sum, |q|² (waves 0-1), |k|² (2-3)
     {
-        const float v[2] = {ssp, y * y};
+        const float v[2] = {ss0 + ss1, y * y};
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const float t = group_sum<64>(v[i]);
@@ -358,7 +361,8 @@ hipError_t launch_gdn_split(dwim_dev *dev, const float *qkv, const float *conv_s
                             const float *conv_w, const float *ab, const Rms &rms, const float *decay, float *state,
                             const float *z, const float *norm_w, float eps, size_t nk, size_t nv, size_t head_dim,
                             float *head_ss, int area) {
-    if (head_dim != kD || nk == 0 || nv % nk || !rms.ss || area < 0 || !head_ss || !ab) return hipErrorInvalidValue;
+    if (head_dim != kD || nk == 0 || nv % nk || !rms.ss || rms.groups > 2 * kST || area < 0 || !head_ss || !ab)
+        return hipErrorInvalidValue;
     if (nv * kD > planes::kMaxCols || (nv * kD) % 256) return hipErrorInvalidValue;
     GdnSplitArgs a{};
     a.qkv = qkv;
