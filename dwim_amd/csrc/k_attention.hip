@@ -19,7 +19,6 @@
 
 namespace {
 
-constexpr int kThreads = 1024;  // a combine block: 16 groups of chunks
 constexpr int kMaxG = 8;
 constexpr int kMaxD = 256;
 constexpr int kPos = 64;        // positions a partial block scores
@@ -231,22 +230,34 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
 
 // out[t][h] = Σ_c e^(m_c − M) o_c / Σ_c e^(m_c − M) l_c, times sigmoid(gate)
 // when a gate is given (gpu/cpu.rs:244-248); with one token, its planes too.
-// Thread group cg = thread / (D/4) takes every CG-th chunk, four elements a
-// thread, merging them as it goes (a running max, the sums rescaled when it
-// grows), four chunks' loads at a time; the groups meet in LDS.
-__global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ out, const float *__restrict__ partials,
-                                                           Shape sh, const float *__restrict__ gate, planes::View pv) {
-    __shared__ float gm[kThreads / 8], gl[kThreads / 8];  // per chunk group (head_dim >= 32)
-    __shared__ float4 part_s[kThreads];
-    const size_t h = blockIdx.x, t = blockIdx.y;
-    const int D = (int)sh.head_dim, TPR = D / 4, CG = kThreads / TPR;
-    const int dg = threadIdx.x % TPR, cg = threadIdx.x / TPR;
+// A head's elements split over DS = head_dim / 64 blocks (blockIdx.x = head ·
+// DS + slice; one block for a head_dim not a multiple of 64) of 16 threads a
+// chunk row, four elements a thread, and 16 groups of them (more for a
+// smaller row): group cg takes every 16th chunk, all its loads issued at
+// once (up to kU chunks, so that a 4k context needs one round trip), merging
+// them as it goes (the batch's max first, then one rescale); the groups meet
+// in LDS.
+constexpr int kCThreads = 256;
+constexpr int kU = 8;
+
+DEV int combine_slices(int D) { return D % 64 == 0 ? D / 64 : 1; }
+
+__global__ void __launch_bounds__(kCThreads) k_attn_combine(float *__restrict__ out, const float *__restrict__ partials,
+                                                            Shape sh, const float *__restrict__ gate,
+                                                            planes::View pv) {
+    __shared__ float gm[kCThreads / 8], gl[kCThreads / 8];  // (head_dim >= 32: 8 threads a row at least)
+    __shared__ float4 part_s[kCThreads];
+    const int D = (int)sh.head_dim, DS = combine_slices(D), TPR = D / (4 * DS);
+    const size_t h = blockIdx.x / DS, t = blockIdx.y;
+    const int slice = (int)(blockIdx.x % DS);
+    const int dg = (int)threadIdx.x % TPR, cg = (int)threadIdx.x / TPR, CG = kCThreads / TPR;
+    const int e0 = slice * (D / DS) + 4 * dg;  // the thread's first element
     const size_t stride = (size_t)(D + 2);
     const float *part = partials + (t * sh.n_heads + h) * sh.chunks * stride;
     float M = -INFINITY, L = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    constexpr int kU = 4;
-    for (size_t c0 = cg; c0 < sh.chunks; c0 += (size_t)kU * CG) {
+    // (threads past the last whole group take no chunks)
+    for (size_t c0 = cg; cg < CG && c0 < sh.chunks; c0 += (size_t)kU * CG) {
         float m[kU], l[kU];
         float2 oa[kU], ob[kU];
 #pragma unroll
@@ -256,10 +267,9 @@ __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ o
             const float *row = part + cc * stride;
             m[u] = c < sh.chunks ? row[D] : -INFINITY;
             l[u] = row[D + 1];
-            oa[u] = *(const float2 *)(row + 4 * dg);  // (D + 2)·4 bytes apart: 8-byte aligned only
-            ob[u] = *(const float2 *)(row + 4 * dg + 2);
+            oa[u] = *(const float2 *)(row + e0);  // (D + 2)·4 bytes apart: 8-byte aligned only
+            ob[u] = *(const float2 *)(row + e0 + 2);
         }
-        // the batch's max first, then one rescale and independent terms
         float Mb = M;
 #pragma unroll
         for (int u = 0; u < kU; u++) Mb = fmaxf(Mb, m[u]);
@@ -306,7 +316,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_combine(float *__restrict__ o
         sum.z += o.z * r;
         sum.w += o.w * r;
     }
-    const size_t i = (t * sh.n_heads + h) * D + 4 * dg;
+    const size_t i = (t * sh.n_heads + h) * D + e0;
     float4 o = make_float4(sum.x / Lt, sum.y / Lt, sum.z / Lt, sum.w / Lt);
     if (gate) {
         const float4 gv = *(const float4 *)(gate + i);
@@ -648,8 +658,9 @@ hipError_t attention_run(dwim_dev *dev, float *partials, float *out, const float
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    dim3 g2((unsigned)n_heads, (unsigned)n);
-    k_attn_combine<<<g2, kThreads, 0, dev->stream>>>(out, partials, sh, gate, pv);
+    const unsigned ds = head_dim % 64 == 0 ? (unsigned)(head_dim / 64) : 1u;
+    dim3 g2((unsigned)n_heads * ds, (unsigned)n);
+    k_attn_combine<<<g2, kCThreads, 0, dev->stream>>>(out, partials, sh, gate, pv);
     return hipGetLastError();
 }
 
