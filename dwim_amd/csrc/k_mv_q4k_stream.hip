@@ -197,8 +197,102 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
     const int gcol = c < 12 ? c / 3 : 0;
     const int k4 = lane & 3, R4 = lane >> 2;
     const float f = c < 12 ? (c % 3 == 0 ? 1.0f : c % 3 == 1 ? 256.0f : 65536.0f) : 0.0f;
+    // three or four tokens: B's column c is (group c / 4, token c % 4), one
+    // MFMA chain a digit, so that a lane's three digits meet in its own
+    // registers and every column but a missing token's carries data
+    constexpr bool kPack = NT >= 3;
+    const int pg = c / 4, pt = c % 4;
+    const bool pactive = pg == kq && pt < NT;
 
+    auto compute_packed = [=](const Regs<kK> &R, const Item &it, unsigned slot) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, macc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) macc[t] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kK; u++) {
+            if (u >= it.nblk) break;
+            const unsigned bl = it.bl + (unsigned)u;
+            {
+                const uint32_t w0 = quad_bcast<0>(R.h[u]), w1 = quad_bcast<1>(R.h[u]), w2 = quad_bcast<2>(R.h[u]),
+                               w3 = quad_bcast<3>(R.h[u]);
+                const float d = f16_bits(w0 & 0xffffu), dmin = f16_bits(w0 >> 16);
+                float sc0, sc1, mn0, mn1;
+                scales_pair(w1, w2, w3, k4, sc0, sc1, mn0, mn1);
+                const float D0 = d * sc0, D1 = d * sc1;
+                const float mA = dmin * mn0, mB = dmin * mn1 - 8.0f * D1;
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const float4 xm = stl[(bl * NT + t) * 8 + 2 * k4 + 1];
+                    macc[t] += mA * (xm.x + xm.y) + mB * (xm.z + xm.w);
+                }
+                hdr[(2 * k4) * kHdrStride + R4] = D0;
+                hdr[(2 * k4 + 1) * kHdrStride + R4] = D1 * 0.0625f;
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            // lane (kq, c): token pt's planes of sub-blocks 2kq + h, if pg == kq
+            const v4i *bbase = lv + (pactive ? (int)((bl * NT + (unsigned)pt) * kBT) + 4 * kq : (int)kZero);
+            const float4 *sxp = stl + (bl * NT + (unsigned)(pt < NT ? pt : 0)) * 8 + 2 * pg;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t mask = h ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+                const float4 Dsb = *(const float4 *)&hdr[(2 * pg + h) * kHdrStride + 4 * kq];
+                const float sx = ((const float *)sxp)[2 * h];
+                const v4u q0 = R.q[u][0], q1 = R.q[u][1];
+                const v4i a0 = {(int)(q0.x & mask), (int)(q0.y & mask), (int)(q0.z & mask), (int)(q0.w & mask)};
+                const v4i a1 = {(int)(q1.x & mask), (int)(q1.y & mask), (int)(q1.z & mask), (int)(q1.w & mask)};
+                v4i C[3];
+#pragma unroll
+                for (int r = 0; r < 3; r++) {
+                    const v4i *bp = bbase + r * kPStride + 2 * h;
+                    C[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    C[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bp[1], C[r], 0, 0, 0);
+                }
+                // the digits meet (weights 1, 256, 65536), then the scale
+                const float Ds[4] = {Dsb.x * sx, Dsb.y * sx, Dsb.z * sx, Dsb.w * sx};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float v = (float)C[0][e] + 256.0f * (float)C[1][e] + 65536.0f * (float)C[2][e];
+                    acc[e] += Ds[e] * v;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        // the groups meet: lanes c, c + 4, c + 8, c + 12 of a row of 16 hold
+        // token c % 4 (row rotations by 4 and 8); lanes 16kq..16kq+15 hold
+        // rows 4kq..4kq+3.  The min terms of row R sit in lanes 4R..4R+3:
+        // summed, parked per wave in the (now free) scale rows, read back by
+        // the lanes that write the slots
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float v = acc[e];
+            v += xlane::mov<0x124>(v);
+            v += xlane::mov<0x128>(v);
+            acc[e] = v;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float mt = group_sum<4>(macc[t]);
+            if (k4 == 0) hdr[t * 16 + R4] = mt;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (c < NT) {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                slots[(slot * NT + (unsigned)c) * 16 + 4 * kq + e] = acc[e] - hdr[c * 16 + 4 * kq + e];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    };
     auto compute = [=](const Regs<kK> &R, const Item &it, unsigned slot) {
+        if constexpr (kPack) {
+            compute_packed(R, it, slot);
+            return;
+        }
         float acc[NT][4], macc[NT];
 #pragma unroll
         for (int t = 0; t < NT; t++) {
