@@ -369,43 +369,50 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
     Regs<kK> A, B;
     Item ia{}, ib{};
     {
-        // chunk gi of the planes, then of the statistics (past both: a
-        // reload of chunk 0, stored nowhere)
-        const unsigned nplane = PB * NT * 48, nstat = PB * NT * 8;
-        constexpr int kPL = (int)((kPlaneBudget / 16 + 1023) / 1024);
-        const GMEM int8_t *xqs[NT];
-        const GMEM float *xss[NT];
+        // a run of global memory a wave: token t's digit p (PB·16 chunks at
+        // xq[t] + p·cols + pb·256) for run 4t + p, its statistics (PB·8 chunks
+        // at xstat[t] + pb·32 floats) for run 4t + 3; with two tokens each run
+        // is split over two waves.  Loads past a run's end reload its first
+        // chunk and are stored nowhere.
+        constexpr int kRuns = 4 * NT, kWpr = kW / kRuns > 0 ? kW / kRuns : 1;
+        constexpr int kSL = (int)((kPlaneBudget / 16 / NT / 3 + 64 * kWpr - 1) / (64 * kWpr));
+        const int run = wave % kRuns, sub = wave / kRuns;
+        const bool staging = wave < kRuns * kWpr;
+        const unsigned st_t = (unsigned)(run / 4), st_p = (unsigned)(run % 4);
+        const bool st_stat = st_p == 3;
+        const unsigned len = st_stat ? PB * 8u : PB * 16u;
+        const GMEM int8_t *qrun = (const GMEM int8_t *)sload(a.xq[0]);
+        const GMEM int8_t *srun = (const GMEM int8_t *)sload(a.xstat[0]);
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            xqs[t] = (const GMEM int8_t *)sload(a.xq[t]);
-            xss[t] = (const GMEM float *)sload(a.xstat[t]);
+        for (int q = 1; q < NT; q++) {
+            const GMEM int8_t *xq_q = (const GMEM int8_t *)sload(a.xq[q]);
+            const GMEM int8_t *xs_q = (const GMEM int8_t *)sload(a.xstat[q]);
+            qrun = st_t == (unsigned)q ? xq_q : qrun;
+            srun = st_t == (unsigned)q ? xs_q : srun;
         }
-        v4i v[kPL];
+        const GMEM v4i *src = (const GMEM v4i *)(st_stat ? srun + (size_t)pb * 32u * 4u
+                                                         : qrun + (size_t)(st_p < 3 ? st_p : 0u) * cols + pb * 256u);
+        v4i v[kSL];
 #pragma unroll
-        for (int u = 0; u < kPL; u++) {
-            const unsigned gi = threadIdx.x + 1024u * u;
-            const bool plane = gi < nplane;
-            const unsigned s = plane ? gi : gi - nplane < nstat ? gi - nplane : 0u;
-            const unsigned bt = plane ? s / 48u : s / 8u, bl = bt / NT, t = bt % NT;
-            const GMEM int8_t *qsrc = xqs[0];
-            const GMEM float *ssrc = xss[0];
-#pragma unroll
-            for (int q = 1; q < NT; q++) {
-                qsrc = t == (unsigned)q ? xqs[q] : qsrc;
-                ssrc = t == (unsigned)q ? xss[q] : ssrc;
-            }
-            const unsigned ch = s % 48u, k = s % 8u;
-            v[u] = plane ? *(const GMEM v4i *)(qsrc + (ch / 16u) * cols + (pb + bl) * 256u + 16u * (ch % 16u))
-                         : *(const GMEM v4i *)(ssrc + ((pb + bl) * 8u + k) * 4u);
+        for (int u = 0; u < kSL; u++) {
+            const unsigned j = (unsigned)lane + 64u * (unsigned)(sub + kWpr * u);
+            v[u] = src[j < len ? j : 0u];
         }
         // (unconditional, so that the waits count it: a wave without items
         // reloads the run's first, which every run has)
         ia = item_of(i0 + (n_w > 0 ? (unsigned)wave : 0u));
         load(A, ia);
+        if (staging) {
 #pragma unroll
-        for (int u = 0; u < kPL; u++) {
-            const unsigned gi = threadIdx.x + 1024u * u;
-            if (gi < nplane + nstat) lv[gi < nplane ? gi + (gi >> 4) : kStat + (gi - nplane)] = v[u];
+            for (int u = 0; u < kSL; u++) {
+                const unsigned j = (unsigned)lane + 64u * (unsigned)(sub + kWpr * u);
+                if (j >= len) continue;
+                // plane chunk j: block j / 16, chunk j % 16 of the digit;
+                // statistics chunk j: block j / 8, chunk j % 8
+                const unsigned dst = st_stat ? kStat + ((j / 8u) * NT + st_t) * 8u + j % 8u
+                                             : ((j / 16u) * NT + st_t) * kBT + st_p * kPStride + j % 16u;
+                lv[dst] = v[u];
+            }
         }
         if (threadIdx.x < (unsigned)(kK * NT * kBT)) lv[kZero + threadIdx.x] = v4i{0, 0, 0, 0};
     }
