@@ -287,6 +287,8 @@ def main():
         tok = model.forward_greedy([tok], pos)
         decoded.append(tok)
         pos += 1
+    model.mark()
+    start_tok, start_pos = tok, pos
     dev.sync()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -295,6 +297,14 @@ def main():
         pos += 1
     dev.sync()
     decode_s = time.perf_counter() - t0
+    # the same steps from the same state with the picks fed back on the device
+    # (dwim_model_decode_greedy): the host queues every step without waiting
+    model.rewind_to_mark()
+    dev.sync()
+    t0 = time.perf_counter()
+    fed = model.decode_greedy(start_tok, start_pos, args.steps)
+    dev.sync()
+    fed_s = time.perf_counter() - t0
     ms_per_step = decode_s / args.steps * 1e3
     decode_tps = args.steps / decode_s
     # bytes a decode token must read: the Q4_K body, Q6_K head, DeltaNet states
@@ -334,6 +344,8 @@ def main():
         "prefill_tok_s": args.prompt / prefill_s,
         "prefill_s": prefill_s,
         "prefill_roofline": prefill_roofline,
+        "decode_device_fed_tok_s": args.steps / fed_s,
+        "decode_device_fed_equals_host_loop": fed == decoded[-args.steps:],
         "decode_hbm_frac": token_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "decode_bytes_per_token": token_bytes,
         "model_build_s": build_s,

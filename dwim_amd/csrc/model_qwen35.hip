@@ -96,6 +96,12 @@ struct dwim_model {
     dwim_buf *up = nullptr, *gate_ffn = nullptr, *logits = nullptr, *rope = nullptr, *drafted = nullptr;
     // the one-token DeltaNet step's Σo² per head quarter ([v_heads][4])
     dwim_buf *head_ss = nullptr;
+    // device-fed greedy decoding: the picks, and where the step running
+    // reads its token and writes its pick (null outside decode_greedy)
+    uint32_t *picks = nullptr;
+    size_t picks_cap = 0;
+    const uint32_t *embed_from = nullptr;
+    uint32_t *argmax_to = nullptr;
     Sequence seq;
     std::map<size_t, Sequence> parked;  // the sequences not running
     // verifying: the linear layers' states run through the batch, and their
@@ -602,7 +608,11 @@ struct dwim_model {
     int forward_batch(const uint32_t *tokens, size_t n, size_t pos, bool verify, bool wanted, float *logits_out,
                       uint32_t *greedy) {
         TRY(batch(n));
-        TRY(dwim_embed(dev, x, embd, tokens, n));
+        if (embed_from) {
+            DWIM_HIP(launch_embed(dev->stream, x->data, embd, embed_from, n));
+        } else {
+            TRY(dwim_embed(dev, x, embd, tokens, n));
+        }
         handed = false;
         for (size_t i = 0; i < layers.size(); i++)
             TRY(layer(layers[i], n, pos, verify, i + 1 < layers.size() ? layers[i + 1].attn_norm : nullptr));
@@ -649,6 +659,11 @@ struct dwim_model {
     }
 
     int read_logits(float *logits_out, uint32_t *greedy, size_t rows = 1) {
+        if (argmax_to) {
+            // the pick stays on the device, where the next step's embedding reads it
+            DWIM_HIP(launch_argmax(dev->stream, logits->data, rows, c.vocab, argmax_to));
+            return 0;
+        }
         if (greedy) TRY(dwim_argmax(dev, logits, rows, greedy));
         if (logits_out) TRY(dwim_read(dev, logits, logits_out, rows * c.vocab));
         if (!greedy && !logits_out) return finish();
@@ -666,6 +681,47 @@ struct dwim_model {
             TRY(forward_batch(tokens + i * most, m, pos + i * most, false, last, last ? logits_out : nullptr,
                               last ? greedy : nullptr));
         }
+        return check_chains();
+    }
+
+    // Greedy decoding of `steps` tokens from `token` at `pos`, as the reply
+    // loop runs it token by token (inference/local.rs:162-240, each step
+    // LanguageModel::forward of the token picked, qwen35/mod.rs:1021-1038,
+    // then qwen35::argmax).  Each step's pick stays on the device: the argmax
+    // writes it into `picks` and the next step's embedding reads it there, so
+    // the host queues every step without waiting and reads the picks back
+    // once.  picks[0] is the first token; step i's argmax writes picks[i+1]
+    // and uses the words after it as its partials, which step i+1's pick then
+    // overwrites, in stream order.  A drafting model runs the steps one by
+    // one (its drafter takes the token ids on the host).
+    int decode_greedy(uint32_t token, size_t pos, size_t steps, uint32_t *out) {
+        if (steps == 0) return 0;
+        if (token >= embd->rows) return dwim_fail("decode: token " + std::to_string(token) + " is past the table");
+        if (pos + steps > seq.max_len) return dwim_fail("tokens past the end of the cache");
+        if (has_draft) {
+            for (size_t i = 0; i < steps; i++) {
+                TRY(forward(&token, 1, pos + i, nullptr, &token));
+                out[i] = token;
+            }
+            return 0;
+        }
+        if (c.vocab > embd->rows) return dwim_fail("decode: the head picks tokens past the embedding table");
+        const size_t words = steps + 1 + argmax_scratch_words(1);
+        DWIM_HIP(dev_grow(dev, (void **)&picks, &picks_cap, words, 4));
+        DWIM_HIP(hipMemcpyAsync(picks, &token, 4, hipMemcpyHostToDevice, dev->stream));
+        // the pageable source is read before the call returns; waiting here
+        // keeps that so whatever the runtime does with small copies
+        DWIM_HIP(hipStreamSynchronize(dev->stream));
+        int err = 0;
+        for (size_t i = 0; i < steps && !err; i++) {
+            embed_from = picks + i;
+            argmax_to = picks + i + 1;
+            err = forward_batch(nullptr, 1, pos + i, false, true, nullptr, nullptr);
+        }
+        embed_from = argmax_to = nullptr;
+        TRY(err);
+        DWIM_HIP(hipMemcpyAsync(out, picks + 1, steps * 4, hipMemcpyDeviceToHost, dev->stream));
+        DWIM_HIP(hipStreamSynchronize(dev->stream));
         return check_chains();
     }
 
@@ -960,6 +1016,10 @@ struct dwim_model {
     }
 
     ~dwim_model() {
+        if (picks) {
+            hipStreamSynchronize(dev->stream);
+            hipFree(picks);
+        }
         for (auto *b : bufs) dwim_free_buffer(b);
         for (auto *w : weights) dwim_free_weight(w);
         for (auto *cc : cache_list) dwim_free_cache(cc);
@@ -1068,6 +1128,10 @@ extern "C" int dwim_model_forward(dwim_model *m, const uint32_t *tokens, size_t 
 
 extern "C" int dwim_model_forward_greedy(dwim_model *m, const uint32_t *tokens, size_t n, size_t pos, uint32_t *next) {
     return m->forward(tokens, n, pos, nullptr, next);
+}
+
+extern "C" int dwim_model_decode_greedy(dwim_model *m, uint32_t token, size_t pos, size_t steps, uint32_t *out) {
+    return m->decode_greedy(token, pos, steps, out);
 }
 
 extern "C" int dwim_model_reset(dwim_model *m) { return m->reset(); }

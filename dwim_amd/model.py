@@ -64,6 +64,8 @@ def _declare(L):
     L.dwim_model_forward.argtypes = [vp, u32p, sz, sz, f32p]
     L.dwim_model_forward_greedy.restype = ctypes.c_int
     L.dwim_model_forward_greedy.argtypes = [vp, u32p, sz, sz, u32p]
+    L.dwim_model_decode_greedy.restype = ctypes.c_int
+    L.dwim_model_decode_greedy.argtypes = [vp, ctypes.c_uint32, sz, sz, u32p]
     L.dwim_model_reset.restype = ctypes.c_int
     L.dwim_model_reset.argtypes = [vp]
     L.dwim_model_draft.restype = ctypes.c_int
@@ -87,7 +89,7 @@ def _declare(L):
 
 
 MODEL_SIGNATURES = ["dwim_model_synthetic", "dwim_model_free", "dwim_model_batch", "dwim_model_forward",
-                    "dwim_model_forward_greedy", "dwim_model_reset", "dwim_model_draft", "dwim_model_verify",
+                    "dwim_model_forward_greedy", "dwim_model_decode_greedy", "dwim_model_reset", "dwim_model_draft", "dwim_model_verify",
                     "dwim_model_rewind", "dwim_model_mark", "dwim_model_rewind_to_mark", "dwim_model_add_sequence",
                     "dwim_model_select_sequence", "dwim_model_save", "dwim_model_restore"]
 
@@ -121,6 +123,13 @@ class Model:
         D._check(self.L.dwim_model_forward_greedy(self.h, t.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), t.size,
                                                   pos, ctypes.byref(nxt)))
         return nxt.value
+
+    def decode_greedy(self, token: int, pos: int, steps: int) -> list[int]:
+        """`steps` greedy steps from `token` at `pos`, the picks fed back on the device."""
+        out = np.zeros(max(steps, 1), np.uint32)
+        D._check(self.L.dwim_model_decode_greedy(self.h, token, pos, steps,
+                                                 out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))))
+        return [int(t) for t in out[:steps]]
 
     def reset(self):
         D._check(self.L.dwim_model_reset(self.h))

@@ -238,6 +238,12 @@ int dwim_model_forward(dwim_model *m, const uint32_t *tokens, size_t n, size_t p
  * the device: only 4 bytes come back. */
 int dwim_model_forward_greedy(dwim_model *m, const uint32_t *tokens, size_t n, size_t pos,
                               uint32_t *next);
+/* Greedy decoding of `steps` tokens, the reply loop's step (feed the token
+ * picked, inference/local.rs:162-240) without the host between steps: from
+ * `token` at position `pos`, out[i] = the greedy pick after step i, which is
+ * step i+1's token.  The picks stay on the device until all steps are queued;
+ * the same tokens as `steps` calls of dwim_model_forward_greedy. */
+int dwim_model_decode_greedy(dwim_model *m, uint32_t token, size_t pos, size_t steps, uint32_t *out);
 /* LanguageModel::reset (qwen35/mod.rs:1230-1246). */
 int dwim_model_reset(dwim_model *m);
 /* LanguageModel::draft (qwen35/mod.rs:1045-1071): up to k (at most 8, and as

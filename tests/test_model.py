@@ -387,3 +387,34 @@ def test_chained_one_token_path_agrees_with_cpu(monkeypatch):
         _close(g.forward([t], 5 + i), o.forward([t], 5 + i), 2e-3, f"tiny, token {i}")
     assert g.draft(8, 8, 3) == [int(t) for t in o.draft(8, 8, 3)]
     g.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", ["tiny", "tiny+drafter", "27b-widths"])
+def test_device_fed_decode_is_greedy_decode(shape):
+    """dwim_model_decode_greedy (each step's pick handed to the next step's
+    embedding on the device) gives the tokens of the host loop of
+    forward_greedy calls, leaves the same state behind (the step after it
+    agrees), and on the 27B widths runs the fused one-token path with the
+    Q6_K head's planes."""
+    if shape == "27b-widths":
+        cfg = M.config_27b(False)
+        cfg.layers, cfg.vocab = 4, 512
+    else:
+        cfg = _tiny(shape == "tiny+drafter")
+    gpu = D.Hip(0)
+    prompt = [5, 9, 33, 1, 60, 12, 7, 2]
+    host, dev = M.Model(gpu, cfg, SEED + 3, max_len=64), M.Model(gpu, cfg, SEED + 3, max_len=64)
+    want = _greedy(host, prompt, 21)
+    first = dev.forward_greedy(prompt, 0)
+    assert first == want[0]
+    got = [first] + dev.decode_greedy(first, len(prompt), 13)
+    got += dev.decode_greedy(got[-1], len(prompt) + 13, 7)
+    assert got[:21] == want
+    assert dev.decode_greedy(got[-1], len(prompt) + 20, 0) == []
+    with pytest.raises(RuntimeError):
+        dev.decode_greedy(got[-1], 60, 5)  # past the cache
+    with pytest.raises(RuntimeError):
+        dev.decode_greedy(cfg.vocab + 10**6, 30, 1)  # past the table
+    host.close()
+    dev.close()
