@@ -44,8 +44,9 @@ DEV float sum16(float v) {
 __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out, const float *__restrict__ q,
                                                         const float *__restrict__ k, const float *__restrict__ v,
                                                         const float *__restrict__ gates,
-                                                        const float *__restrict__ decay, float *__restrict__ state,
-                                                        size_t n, int n_k_heads, int n_v_heads, Rms rms) {
+                                                        const float *__restrict__ decay, float *state,
+                                                        const float *state_in, size_t n, int n_k_heads, int n_v_heads,
+                                                        Rms rms) {
     // a run's keys and queries [token][key] (also the state slice's staging
     // at the start and the end), values [token][column] and gates
     __shared__ v4f kq[2][kRun][kD / 4];
@@ -65,9 +66,10 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
     const int kh = h / (n_v_heads / n_k_heads);
     const int c = threadIdx.x / kParts, p = threadIdx.x % kParts;
     float *S = state + (size_t)h * kD * kD;
+    const float *Sin = state_in + (size_t)h * kD * kD;
 
-    // state slice in: rows of 16 columns, coalesced
-    for (int e = threadIdx.x; e < kD * kCols; e += kThreads) tile[e / kCols][e % kCols] = S[(e / kCols) * kD + c0 + e % kCols];
+    // state slice in (from state_in, out to state): rows of 16 columns, coalesced
+    for (int e = threadIdx.x; e < kD * kCols; e += kThreads) tile[e / kCols][e % kCols] = Sin[(e / kCols) * kD + c0 + e % kCols];
     __syncthreads();
     float s[kKeys];
 #pragma unroll
@@ -530,8 +532,9 @@ hipError_t delta_net_reserve(dwim_dev *dev, size_t n, size_t n_v_heads) {
 
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k, const float *v,
                             const float *gates, const float *decay, float *state, size_t n, size_t n_k_heads,
-                            size_t n_v_heads, size_t head_dim, const Rms *rms, bool unit_keys) {
+                            size_t n_v_heads, size_t head_dim, const Rms *rms, bool unit_keys, const float *state_in) {
     if (unit_keys && n >= (size_t)kC && !(rms && rms->ss)) {
+        if (state_in && state_in != state) return hipErrorInvalidValue;  // (the token loop reads one state, writes another)
         const size_t nch = (n + kC - 1) / kC;
         hipError_t e = delta_net_reserve(dev, n, n_v_heads);
         if (e != hipSuccess) return e;
@@ -551,7 +554,8 @@ hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const flo
         return hipGetLastError();
     }
     dim3 grid(kD / kCols, (unsigned)n_v_heads);
-    k_delta_net<<<grid, kThreads, 0, dev->stream>>>(out, q, k, v, gates, decay, state, n, (int)n_k_heads,
+    k_delta_net<<<grid, kThreads, 0, dev->stream>>>(out, q, k, v, gates, decay, state, state_in ? state_in : state, n,
+                                                    (int)n_k_heads,
                                                     (int)n_v_heads, rms ? *rms : Rms{});
     return hipGetLastError();
 }

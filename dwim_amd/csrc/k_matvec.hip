@@ -328,6 +328,52 @@ __global__ void __launch_bounds__(256) k_skinny_bf16(const uint16_t *__restrict_
     }
 }
 
+// A few tokens (a verify batch) through a bf16 matrix of few rows: a block of
+// 256 threads per row and run of up to 4 tokens, thread i summing columns
+// 8i.. in steps of 2048 for each token (16-byte weight loads, read once for
+// the run), then the block's sums meet per token.  Enough blocks to spread the
+// rows' bytes over the chip: 96 × 5120 is 96 blocks of 40 KB.
+constexpr int kRowTok = 4;
+
+__global__ void __launch_bounds__(256) k_rows_bf16(const uint16_t *__restrict__ w, const float *__restrict__ x,
+                                                   float *__restrict__ out, size_t rows, size_t cols, size_t n,
+                                                   int add) {
+    __shared__ float part[kRowTok][4];
+    const size_t row = blockIdx.x, t0 = (size_t)blockIdx.y * kRowTok;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nt = (int)(n - t0 < (size_t)kRowTok ? n - t0 : (size_t)kRowTok);
+    float acc[kRowTok] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint16_t *wr = w + row * cols;
+    for (size_t c = 8 * (size_t)tid; c < cols; c += 8 * 256) {
+        const uint4 q = *(const uint4 *)(wr + c);
+        const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+        float wf[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            wf[2 * i] = dq::bf16_to_f32((uint16_t)(v[i] & 0xffffu));
+            wf[2 * i + 1] = dq::bf16_to_f32((uint16_t)(v[i] >> 16));
+        }
+#pragma unroll
+        for (int t = 0; t < kRowTok; t++) {
+            if (t >= nt) break;
+            const float4 a = *(const float4 *)(x + (t0 + t) * cols + c), b = *(const float4 *)(x + (t0 + t) * cols + c + 4);
+            acc[t] += ((wf[0] * a.x + wf[1] * a.y) + (wf[2] * a.z + wf[3] * a.w)) +
+                      ((wf[4] * b.x + wf[5] * b.y) + (wf[6] * b.z + wf[7] * b.w));
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kRowTok; t++) {
+        const float v = group_sum<64>(acc[t]);
+        if (lane == 0) part[t][wave] = v;
+    }
+    __syncthreads();
+    if (tid < nt) {
+        const float v = (part[tid][0] + part[tid][1]) + (part[tid][2] + part[tid][3]);
+        float *o = out + (t0 + tid) * rows + row;
+        *o = add ? *o + v : v;
+    }
+}
+
 hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const float *x, size_t n, int add) {
     hipStream_t s = dev->stream;
     Weights w{wt->q, wt->s, wt->s2, wt->s3, wt->rows, wt->cols};
@@ -343,6 +389,11 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
     case DWIM_Q4_0: return launch_fmt<DWIM_Q4_0>(s, w, x, out, n, add);
     case DWIM_Q8_0: return launch_fmt<DWIM_Q8_0>(s, w, x, out, n, add);
     default:
+        if (n < 16 && wt->rows <= kSkRows && wt->cols % 8 == 0) {
+            k_rows_bf16<<<dim3((unsigned)wt->rows, (unsigned)((n + kRowTok - 1) / kRowTok)), 256, 0, s>>>(
+                (const uint16_t *)wt->q, x, out, wt->rows, wt->cols, n, add);
+            return hipGetLastError();
+        }
         if (n >= 16 && wt->rows <= kSkRows && wt->cols % kSkK == 0) {
             k_skinny_bf16<<<(unsigned)((n + kSkTok - 1) / kSkTok), 256, 0, s>>>((const uint16_t *)wt->q, x, out,
                                                                                wt->rows, wt->cols, n, add);

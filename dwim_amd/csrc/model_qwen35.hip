@@ -526,13 +526,27 @@ struct dwim_model {
             dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
             dwim_buf *ssm = verify ? ssm_scratch[l.slot] : seq.ssm_state[l.slot];
             if (fused) {
+                // a verified batch's projections go straight to where rewind
+                // reads them, and its state runs from the real one into the
+                // scratch (no copies)
+                dwim_buf *qkv_in = verify ? qkv_saved[l.slot] : qkv, *ab_in = verify ? ab_saved[l.slot] : ab;
+                if (verify) {
+                    TRY(dwim_resize(dev, qkv_in, n * (2 * k_dim() + v_dim())));
+                    TRY(dwim_resize(dev, ab_in, n * 2 * c.v_heads));
+                }
                 const dwim_weight *ws[2] = {l.qkv, l.z};
-                dwim_buf *outs[2] = {qkv, z};
+                dwim_buf *outs[2] = {qkv_in, z};
                 TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
-                TRY(dwim_matmul(dev, ab, l.ab, xh));
-                if (verify) TRY(save_inputs(l.slot, n));
-                TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv, state, l.conv, c.state_dim, eps));
-                TRY(dwim_delta_net_unit_keys(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads, c.state_dim));
+                TRY(dwim_matmul(dev, ab_in, l.ab, xh));
+                TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv_in, state, l.conv, c.state_dim, eps));
+                if (verify) {
+                    DWIM_HIP(launch_delta_net(dev, att->data, q->data, k->data, v->data, ab_in->data, l.decay->data,
+                                              ssm->data, n, c.k_heads, c.v_heads, c.state_dim, nullptr, true,
+                                              seq.ssm_state[l.slot]->data));
+                } else {
+                    TRY(dwim_delta_net_unit_keys(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads,
+                                                 c.state_dim));
+                }
                 DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps, -1));
                 TRY(dwim_matmul_add(dev, x, l.out, z, xb));
             } else {
@@ -561,6 +575,8 @@ struct dwim_model {
 
     // the verified batch's inputs of linear layer `slot`, and its state
     int save_inputs(size_t slot, size_t n) {
+        TRY(dwim_resize(dev, qkv_saved[slot], n * (2 * k_dim() + v_dim())));
+        TRY(dwim_resize(dev, ab_saved[slot], n * 2 * c.v_heads));
         TRY(dwim_copy(dev, qkv_saved[slot], 0, qkv, 0, n * (2 * k_dim() + v_dim())));
         TRY(dwim_copy(dev, ab_saved[slot], 0, ab, 0, n * 2 * c.v_heads));
         return dwim_copy(dev, ssm_scratch[slot], 0, seq.ssm_state[slot], 0, ssm_width());
@@ -786,11 +802,22 @@ struct dwim_model {
             TRY(dwim_resize(dev, att, keep * v_dim()));
             for (const Layer &l : layers) {
                 if (l.attention) continue;
-                TRY(dwim_copy(dev, qkv, 0, qkv_saved[l.slot], 0, keep * (2 * k_dim() + v_dim())));
-                TRY(dwim_copy(dev, ab, 0, ab_saved[l.slot], 0, keep * 2 * c.v_heads));
                 auto &pair = seq.conv_state[l.slot];
                 dwim_buf *state = seq.parity ? pair[0] : pair[1];
                 dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
+                if (fusable(l)) {
+                    // as the batch ran: conv and key norms in one launch, the
+                    // saved inputs read where they lie
+                    TRY(dwim_resize(dev, qkv_saved[l.slot], keep * (2 * k_dim() + v_dim())));
+                    TRY(dwim_resize(dev, ab_saved[l.slot], keep * 2 * c.v_heads));
+                    TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv_saved[l.slot], state, l.conv, c.state_dim,
+                                         c.eps));
+                    TRY(dwim_delta_net_unit_keys(dev, att, q, k, v, ab_saved[l.slot], l.decay,
+                                                 seq.ssm_state[l.slot], c.k_heads, c.v_heads, c.state_dim));
+                    continue;
+                }
+                TRY(dwim_copy(dev, qkv, 0, qkv_saved[l.slot], 0, keep * (2 * k_dim() + v_dim())));
+                TRY(dwim_copy(dev, ab, 0, ab_saved[l.slot], 0, keep * 2 * c.v_heads));
                 TRY(dwim_conv(dev, q, k, v, state_out, qkv, state, l.conv));
                 TRY(dwim_l2norm(dev, q, c.state_dim, c.eps));
                 TRY(dwim_l2norm(dev, k, c.state_dim, c.eps));

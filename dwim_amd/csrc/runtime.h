@@ -205,11 +205,13 @@ struct Rms {
     float eps = 0.0f;
 };
 // with rms, the gate logits (alpha, beta) are scaled by it first; with
-// unit_keys (keys of unit length), 64 tokens and more take the chunked form
+// unit_keys (keys of unit length), 64 tokens and more take the chunked form;
+// with state_in (fewer tokens only), the state is read from there and the
+// updated one written to `state`
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k,
                             const float *v, const float *gates, const float *decay, float *state,
                             size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim, const Rms *rms = nullptr,
-                            bool unit_keys = false);
+                            bool unit_keys = false, const float *state_in = nullptr);
 hipError_t launch_embed(hipStream_t s, float *out, const dwim_weight *w, const uint32_t *tokens,
                         size_t n);
 // first index of each row's maximum, into the first `rows` words of scratch

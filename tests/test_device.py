@@ -97,7 +97,8 @@ def test_matmul_matches_cpu(gpu):
 def test_bf16_batches_through_few_rows_match_cpu(gpu):
     # DeltaNet's gate projection shape (96 x 5120) and ragged batches
     rng = O.Rng(5)
-    for rows, cols, n in [(96, 5120, 40), (128, 1024, 17), (3, 64, 300)]:
+    for rows, cols, n in [(96, 5120, 40), (128, 1024, 17), (3, 64, 300), (96, 5120, 4), (96, 5120, 1), (96, 5120, 7),
+                          (5, 72, 3), (96, 2056, 15)]:
         w = rng.bf16(rows, cols)
         x = rng.floats(n * cols)
         want = O.matmul(w, x)
