@@ -385,6 +385,9 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
             hipError_t e = launch_planes(dev, x, wt->cols, nullptr, 0.0f, nullptr, 0);
             return e != hipSuccess ? e : launch_mv_q6k_mfma(dev, wt, out, 0);
         }
+        // a few tokens (a verify batch): the weights read once a run of four
+        if (n > 1 && n < 16 && !add && wt->cols % 256 == 0 && wt->cols <= 10240)
+            return launch_mv_q6k_tokens(dev, wt, out, x, n);
         return launch_fmt<DWIM_Q6_K>(s, w, x, out, n, add);
     case DWIM_Q4_0: return launch_fmt<DWIM_Q4_0>(s, w, x, out, n, add);
     case DWIM_Q8_0: return launch_fmt<DWIM_Q8_0>(s, w, x, out, n, add);

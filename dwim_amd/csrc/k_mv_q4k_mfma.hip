@@ -837,6 +837,16 @@ hipError_t launch_planes(dwim_dev *dev, const float *x, size_t cols, const float
     return hipGetLastError();
 }
 
+hipError_t launch_planes_batch(dwim_dev *dev, const float *x, size_t cols, size_t nt, int pair, planes::View *views) {
+    if (cols > planes::kMaxCols || cols % 256 || nt < 1 || nt > (size_t)kMaxTok) return hipErrorInvalidValue;
+    dev->prepared = 0;
+    const unsigned blocks = (unsigned)((cols / 4 + kPlanesThreads - 1) / kPlanesThreads);
+    k_planes<<<dim3(blocks, (unsigned)nt), kPlanesThreads, 0, dev->stream>>>(x, nullptr, 0.0f, 0, nullptr,
+                                                                             planes_area(dev, kBatchArea, cols), pair);
+    for (size_t t = 0; t < nt; t++) views[t] = planes_area(dev, kBatchArea + (int)t, cols);
+    return hipGetLastError();
+}
+
 hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                               int count, int swiglu, int area, const MvExtra *extra) {
     if (count < 1 || count > kMaxJobs || (swiglu && count != 2)) return hipErrorInvalidValue;

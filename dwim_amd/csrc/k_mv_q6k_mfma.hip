@@ -172,7 +172,277 @@ __global__ void __launch_bounds__(512) k_mv_q6k_mfma(const Q6Args a) {
     if (r < a.rows) a.out[r] = v;
 }
 
+// ---------------------------------------------------------------- tokens
+// Two to four tokens at once (a verify batch through the head), the weights
+// read once for all of them.  B's columns are (k-group g, token t), column
+// 4g + t, nonzero only in k-group g, so every column is used, and each digit
+// of the planes takes one MFMA: B lane (kq, c) carries digit p of token c % 4's
+// activations of group G(kq, u) = 8(kq / 2) + kq % 2 + 2u when c / 4 == kq.
+// A column's three int32 sums combine in f32 (C0 + 256·C1 + 65536·C2), are
+// scaled by the token's activation scale of the column's group and by the
+// row's d·sc, and the four k-groups of a token meet by row rotations.  The
+// loads are the one-token kernel's: every one issued before any compute, the
+// planes and statistics of the wave's blocks for every token first.
+constexpr int kMaxTok6 = 4;
+
+struct Q6TArgs {
+    const uint8_t *ql, *qh;
+    const int8_t *sc;
+    const uint16_t *d;
+    float *out;              // [NT][rows]
+    unsigned rows, nb, S;
+    const int8_t *xq[kMaxTok6];     // each token's planes [3][cols] (groups of 16)
+    const float4 *xstat[kMaxTok6];  // [cols/64][2]
+};
+
+// Per wave LDS, in 16-byte chunks: the planes [block][digit][group][token]
+// (so that the 16 B lanes of an MFMA read 16 distinct chunks), the statistics
+// [block][token][8] (chunks 2k, 2k + 1: scales and sums of groups 4k..4k+3),
+// a zero chunk and the decoded d·sc ([group][row] floats, rows of 20), whose
+// area also takes the spare loads' stores before it is written.
+template <int NT>
+struct Lds6T {
+    static constexpr int kPlaneChunks = kK * 48 * NT;
+    static constexpr int kPlaneLoads = (kPlaneChunks + 63) / 64;
+    static constexpr int kStatChunks = kK * 8 * NT;
+    static constexpr int kStatLoads = (kStatChunks + 63) / 64;
+    static constexpr int kStat = kPlaneChunks;
+    static constexpr int kZero = kStat + kStatChunks;
+    static constexpr int kHdr = kZero + 1;
+    static constexpr int kHdrStride = 20;
+    static constexpr int kChunks = kHdr + 16 * kHdrStride / 4;
+    static_assert(16 * kHdrStride / 4 >= 64, "the spare loads land in the header area");
+    static_assert(16 * kHdrStride >= 2 * NT * 16, "the sums of a wave fit its header area");
+};
+
+// the group of 16 a k-group x of an MFMA takes in run u (the lanes' layout above)
+DEV int q6_group(int x, int u) { return 8 * (x >> 1) + (x & 1) + 2 * u; }
+
+template <int NT>
+__global__ void __launch_bounds__(512) k_mv_q6k_tokens(const Q6TArgs a) {
+    using L = Lds6T<NT>;
+    typedef unsigned v4u6 __attribute__((ext_vector_type(4)));
+    extern __shared__ uint4 lds_all[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kq = lane >> 4, c = lane & 15;
+    const unsigned S = a.S, nb = a.nb, tile = blockIdx.x;
+    const unsigned b0 = wave * nb / S, b1 = (wave + 1) * nb / S;
+    const int nblk = (int)(b1 - b0);
+    uint4 *my = lds_all + wave * L::kChunks;
+    float *hdr = (float *)(my + L::kHdr);
+    const unsigned cols = nb * 256;
+
+    // planes and statistics of the wave's blocks, every token; loads past
+    // them reload chunk 0 (no branch around a load)
+    v4u6 xc[L::kPlaneLoads], xs[L::kStatLoads];
+#pragma unroll
+    for (int u = 0; u < L::kPlaneLoads; u++) {
+        const int ci0 = lane + 64 * u, ci = ci0 < nblk * 48 * NT ? ci0 : 0;
+        const int g = ci % 16, p = (ci / 16) % 3, t = (ci / 48) % NT, i = ci / (48 * NT);
+        const int8_t *src = t == 0 ? a.xq[0] : t == 1 ? a.xq[1] : t == 2 ? a.xq[2] : a.xq[3];
+        xc[u] = *(const v4u6 *)(src + p * cols + (b0 + i) * 256u + 16u * g);
+    }
+#pragma unroll
+    for (int u = 0; u < L::kStatLoads; u++) {
+        const int ci0 = lane + 64 * u, ci = ci0 < nblk * 8 * NT ? ci0 : 0;
+        const int j = ci % 8, t = (ci / 8) % NT, i = ci / (8 * NT);
+        const float4 *src = t == 0 ? a.xstat[0] : t == 1 ? a.xstat[1] : t == 2 ? a.xstat[2] : a.xstat[3];
+        xs[u] = *(const v4u6 *)&src[(b0 + i) * 8u + j];
+    }
+    const unsigned row = tile * 16 + (unsigned)c, row_c = row < a.rows ? row : a.rows - 1;
+    const unsigned n = (unsigned)kq >> 1, lb = 16u * ((unsigned)kq & 1u);
+    const int k4 = lane & 3, R4 = lane >> 2;
+    const unsigned hrow = tile * 16 + (unsigned)R4, hrow_c = hrow < a.rows ? hrow : a.rows - 1;
+    asm volatile("");
+    uint4 ql[kK][2], qh[kK];
+    uint32_t scw[kK];
+    uint16_t dw[kK];
+#pragma unroll
+    for (int i = 0; i < kK; i++) {
+        const unsigned b = b0 + (unsigned)(i < nblk ? i : 0);
+        const size_t blk = (size_t)row_c * nb + b;
+        ql[i][0] = *(const uint4 *)(a.ql + blk * 128 + 64 * n + lb);
+        ql[i][1] = *(const uint4 *)(a.ql + blk * 128 + 64 * n + 32 + lb);
+        qh[i] = *(const uint4 *)(a.qh + blk * 64 + 32 * n + lb);
+        const size_t hblk = (size_t)hrow_c * nb + b;
+        scw[i] = *(const uint32_t *)(a.sc + hblk * 16 + 4 * k4);
+        dw[i] = a.d[hblk];
+    }
+    // every load's chunk is stored, the spare ones into the header area
+#pragma unroll
+    for (int u = 0; u < L::kPlaneLoads; u++) {
+        const int ci0 = lane + 64 * u;
+        const int g = ci0 % 16, p = (ci0 / 16) % 3, t = (ci0 / 48) % NT, i = ci0 / (48 * NT);
+        const int dst = ci0 < nblk * 48 * NT ? ((i * 3 + p) * 16 + g) * NT + t : L::kHdr + lane;
+        ((v4u6 *)my)[dst] = xc[u];
+    }
+#pragma unroll
+    for (int u = 0; u < L::kStatLoads; u++) {
+        const int ci0 = lane + 64 * u;
+        ((v4u6 *)my)[ci0 < nblk * 8 * NT ? L::kStat + ci0 : L::kHdr + lane] = xs[u];
+    }
+    if (lane == 0) my[L::kZero] = make_uint4(0, 0, 0, 0);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+
+    // B lane (kq, c): token c % 4 of k-group kq when c / 4 == kq; output
+    // lane (kq, c): rows 4kq.., column group gq = c / 4, token tc = c % 4
+    const int tb = c & 3, gq = c >> 2;
+    const bool active = gq == kq && tb < NT;
+    const float *stf = (const float *)(my + L::kStat);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, macc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) macc[t] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kK; i++) {
+        if (i >= nblk) break;
+        {
+            // lane (k4, R4): d·sc of row R4's groups 4k4..4k4+3, and each
+            // token's −32 term −32·Σ d·sc·Σx
+            const float d = dq::from_f16(dw[i]);
+            const float s0 = d * (float)(int8_t)(scw[i] & 0xffu), s1 = d * (float)(int8_t)((scw[i] >> 8) & 0xffu);
+            const float s2 = d * (float)(int8_t)((scw[i] >> 16) & 0xffu), s3 = d * (float)(int8_t)(scw[i] >> 24);
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const float4 xm = *(const float4 *)&stf[((i * NT + t) * 8 + 2 * k4 + 1) * 4];
+                macc[t] -= 32.0f * ((s0 * xm.x + s1 * xm.y) + (s2 * xm.z + s3 * xm.w));
+            }
+            hdr[(4 * k4) * L::kHdrStride + R4] = s0;
+            hdr[(4 * k4 + 1) * L::kHdrStride + R4] = s1;
+            hdr[(4 * k4 + 2) * L::kHdrStride + R4] = s2;
+            hdr[(4 * k4 + 3) * L::kHdrStride + R4] = s3;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint4 lo = ql[i][u & 1], hi = qh[i];
+            const unsigned nsh = 4u * (unsigned)(u >> 1), hsh = 2u * (unsigned)u;
+            const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w}, hw[4] = {hi.x, hi.y, hi.z, hi.w};
+            v4i6 av;
+#pragma unroll
+            for (int w = 0; w < 4; w++)
+                av[w] = (int)(((lw[w] >> nsh) & 0x0f0f0f0fu) | (((hw[w] >> hsh) & 0x03030303u) << 4));
+            const int gb = q6_group(kq, u), go = q6_group(gq, u);
+            v4i6 C[3];
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                const uint4 xq = my[active ? ((i * 3 + p) * 16 + gb) * NT + tb : L::kZero];
+                const v4i6 bv = {(int)xq.x, (int)xq.y, (int)xq.z, (int)xq.w};
+                C[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, v4i6{0, 0, 0, 0}, 0, 0, 0);
+            }
+            // the column's activation scale (zero for the columns past NT)
+            const float sx = tb < NT ? stf[((i * NT + tb) * 8 + 2 * (go >> 2)) * 4 + (go & 3)] : 0.0f;
+            const float4 D = *(const float4 *)&hdr[go * L::kHdrStride + 4 * kq];
+            const float Dv[4] = {D.x, D.y, D.z, D.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                acc[e] += Dv[e] * (sx * (((float)C[0][e] + 256.0f * (float)C[1][e]) + 65536.0f * (float)C[2][e]));
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    // a token's four column groups meet (lanes c, c ± 4, c ± 8 of a row);
+    // then lane (kq, t < NT) holds token t's rows 4kq..4kq+3
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        acc[e] += xlane::mov<0x124>(acc[e]);
+        acc[e] += xlane::mov<0x128>(acc[e]);
+    }
+    // each wave's sums go to its header area ([token][row], then the −32
+    // terms [token][row]), done with
+    float *red = hdr;
+    if (c < NT)
+#pragma unroll
+        for (int e = 0; e < 4; e++) red[c * 16 + 4 * kq + e] = acc[e];
+#pragma unroll
+    for (int t = 0; t < NT; t++) macc[t] = group_sum<4>(macc[t]);
+    if (k4 == 0)
+#pragma unroll
+        for (int t = 0; t < NT; t++) red[(NT + t) * 16 + R4] = macc[t];
+    __syncthreads();
+    if (wave != 0 || lane >= 16 * NT) return;
+    const int t = lane >> 4, rl = lane & 15;
+    float v = 0.0f;
+    for (unsigned w = 0; w < S; w++) {
+        const float *rw = (const float *)(lds_all + w * L::kChunks + L::kHdr);
+        v += rw[t * 16 + rl] + rw[(NT + t) * 16 + rl];
+    }
+    const unsigned r = tile * 16 + (unsigned)rl;
+    if (r < a.rows) a.out[(size_t)t * a.rows + r] = v;
+}
+
+template <int NT>
+hipError_t go_tokens(dwim_dev *dev, const Q6TArgs &a, unsigned tiles) {
+    const size_t lds = (size_t)a.S * Lds6T<NT>::kChunks * 16;
+    static bool raised = false;  // the attribute holds for the process
+    if (!raised) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_mv_q6k_tokens<NT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)(8 * Lds6T<NT>::kChunks * 16));
+        if (e != hipSuccess) return e;
+        raised = true;
+    }
+    k_mv_q6k_tokens<NT><<<tiles, a.S * 64, lds, dev->stream>>>(a);
+    return hipGetLastError();
+}
+
+Q6Args one_token_args(const dwim_weight *w, float *out, const planes::View &in) {
+    Q6Args a{};
+    a.ql = (const uint8_t *)w->q;
+    a.qh = (const uint8_t *)w->s;
+    a.sc = (const int8_t *)w->s2;
+    a.d = (const uint16_t *)w->s3;
+    a.out = out;
+    a.rows = (unsigned)w->rows;
+    a.nb = (unsigned)(w->cols / 256);
+    a.S = (a.nb + kK - 1) / kK;
+    a.xq = in.q;
+    a.xstat = (const float4 *)in.stat;
+    return a;
+}
+
+bool q6_shape_ok(const dwim_weight *w) {
+    return w->fmt == DWIM_Q6_K && w->cols % 256 == 0 && w->cols <= planes::kMaxCols && w->rows < (1u << 31) &&
+           (w->cols / 256 + kK - 1) / kK <= 8;
+}
+
 }  // namespace
+
+hipError_t launch_mv_q6k_tokens(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n) {
+    if (!q6_shape_ok(w) || n < 1) return hipErrorInvalidValue;
+    const size_t cols = w->cols, rows = w->rows;
+    const unsigned tiles = (unsigned)((rows + 15) / 16);
+    // runs of up to four tokens, as even as they come (7 = 4 + 3)
+    const size_t runs = (n + kMaxTok6 - 1) / kMaxTok6;
+    for (size_t r = 0, t0 = 0; r < runs; r++) {
+        const size_t nt = (n - t0) / (runs - r);
+        planes::View v[kMaxTok6];
+        hipError_t e = launch_planes_batch(dev, x + t0 * cols, cols, nt, 0, v);
+        if (e != hipSuccess) return e;
+        if (nt == 1) {
+            const Q6Args a = one_token_args(w, out + t0 * rows, v[0]);
+            k_mv_q6k_mfma<<<tiles, a.S * 64, (size_t)a.S * Lds6::kChunks * 16, dev->stream>>>(a);
+            e = hipGetLastError();
+        } else {
+            Q6TArgs a{};
+            a.ql = (const uint8_t *)w->q;
+            a.qh = (const uint8_t *)w->s;
+            a.sc = (const int8_t *)w->s2;
+            a.d = (const uint16_t *)w->s3;
+            a.out = out + t0 * rows;
+            a.rows = (unsigned)rows;
+            a.nb = (unsigned)(cols / 256);
+            a.S = (a.nb + kK - 1) / kK;
+            for (size_t t = 0; t < (size_t)kMaxTok6; t++) {
+                const planes::View &vt = v[t < nt ? t : 0];
+                a.xq[t] = vt.q;
+                a.xstat[t] = (const float4 *)vt.stat;
+            }
+            e = nt == 2 ? go_tokens<2>(dev, a, tiles) : nt == 3 ? go_tokens<3>(dev, a, tiles) : go_tokens<4>(dev, a, tiles);
+        }
+        if (e != hipSuccess) return e;
+        t0 += nt;
+    }
+    return hipSuccess;
+}
 
 hipError_t launch_mv_q6k_mfma(dwim_dev *dev, const dwim_weight *w, float *out, int area) {
     if (w->fmt != DWIM_Q6_K || w->cols % 256 || w->cols > planes::kMaxCols || w->rows >= (1u << 31))

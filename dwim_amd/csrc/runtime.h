@@ -185,9 +185,15 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                                      int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
                                      float *xn_out);
+// The planes of nt <= 4 rows of x ([nt][cols]) in the batch areas, one launch;
+// views[t] is token t's (pair: per-32 scales)
+hipError_t launch_planes_batch(dwim_dev *dev, const float *x, size_t cols, size_t nt, int pair, planes::View *views);
 // A Q6_K weight times one token's planes in plane area `area` (the output
 // head; k_mv_q6k_mfma.hip).
 hipError_t launch_mv_q6k_mfma(dwim_dev *dev, const dwim_weight *w, float *out, int area);
+// A Q6_K weight times n tokens (rows of x), out [n][rows], in launches of up
+// to four tokens that read the weights once (a verify batch through the head)
+hipError_t launch_mv_q6k_tokens(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,

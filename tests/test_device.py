@@ -157,6 +157,13 @@ def test_q6_k_matmul_matches_cpu(gpu):
     block_matmul_matches_cpu(gpu, _k_quantized(O.Q6_K, 46), K_SHAPES)
 
 
+def test_q6_k_few_tokens_match_cpu(gpu):
+    # a verify batch through the head: runs of up to four tokens sharing the
+    # weight loads (2, 3, 4, then 5 = 3 + 2 and 7 = 4 + 3), 8 waves a tile at 10240
+    shapes = [(4000, 5120, 4), (1000, 10240, 3), (33, 256, 2), (517, 2048, 5), (64, 4608, 7)]
+    block_matmul_matches_cpu(gpu, _k_quantized(O.Q6_K, 47), shapes)
+
+
 @pytest.mark.parametrize("rows,cols", [(17408, 5120), (5120, 17408)])
 def test_q4_k_matvec_at_the_model_shapes(gpu, rows, cols):
     # W from seeded N(0, 0.02) weights, x N(0, 1), batch 1
