@@ -90,3 +90,14 @@ DEV float block_sum(float v, float *red) {
 
 DEV float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 DEV float softplusf_(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+
+// One wave's copy of 64 × 16 bytes from global memory (lane l's address) into
+// LDS at dst + 16·l (dst the same for every lane): global_load_lds_dwordx4
+// with the LDS base in M0.  Issued as inline assembly so that the compiler
+// does not wait for every earlier vector memory operation before it (it
+// cannot tell which LDS bytes the copy writes); a kernel waits for its copies
+// itself (s_waitcnt vmcnt) before a barrier, then reads them.
+DEV void lds_copy16(const uint8_t *src, uint8_t *dst) {
+    const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) uint8_t *)dst);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(base), "v"(src) : "memory", "m0");
+}

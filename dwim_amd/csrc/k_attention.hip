@@ -12,6 +12,10 @@
 // arithmetic.  It writes, per query head, the chunk's max, sum of
 // exponentials and weighted values.  Pass 2, one block per (query head,
 // token), merges the chunks.  Each cache byte is read once per token.
+//
+// A batch of 16 tokens or more (head_dim 256) runs flash attention on the
+// f16 matrix cores over a copy of the cache expanded to f16 hi + lo parts in
+// the layout the kernel holds in LDS (k_kv_expand, k_attn_flash below).
 #include "device_util.h"
 #include "planes.h"
 #include "quant_math.h"
@@ -330,34 +334,11 @@ __global__ void __launch_bounds__(kCThreads) k_attn_combine(float *__restrict__ 
 }
 
 // ---------------------------------------------------------------- prefill
-//
-// Causal GQA for a batch of tokens on the f16 matrix cores (flash attention
-// with an online softmax), head_dim 256.  A block of 8 waves takes one query
-// head and 128 tokens, a wave 16 of them (the keys' and values' conversion
-// serves 128 queries); the queries stay in registers as f16 hi + lo parts
-// (times 1/16 = 1/sqrt(256), exact).  The block walks the positions in
-// blocks of 32, the next block's loads in flight meanwhile:
-//   * the keys, int8 (exact in f16), give per 32-dimension group g the sums
-//     Σ q·k8 (two MFMAs, hi and lo), which the group's f16 cache scale then
-//     weights: S = Σ_g s_k[p][g] · Σ_{d∈g} q_d k8_d;
-//   * the online softmax (gpu/cpu.rs:388-423 takes the max first, then
-//     exp(s − max) / Σ): each row's running max and sum, the output rescaled
-//     when the max grows;
-//   * the values, dequantized exactly (v8·s as f32) into f16 hi + lo,
-//     transposed in LDS so that the MFMA operands read 8 positions as one
-//     16-byte chunk, and P as hi + lo: O += P_hi·V_hi + P_hi·V_lo + P_lo·V_hi.
+
 typedef _Float16 ahalf8 __attribute__((ext_vector_type(8)));
 typedef float afloat4 __attribute__((ext_vector_type(4)));
 
 constexpr int kFD = 256, kFQ = 128, kFP = 32, kFThreads = 512;
-
-struct PrefillArgs {
-    float *out;
-    const float *q, *gate;
-    const int8_t *kq, *vq;
-    const uint16_t *ks, *vs;
-    unsigned n, pos, heads, kv_heads;
-};
 
 DEV ahalf8 hi8(const float *v) {
     ahalf8 h;
@@ -372,22 +353,130 @@ DEV ahalf8 lo8(const float *v, const ahalf8 &h) {
     return l;
 }
 
-template <bool F16>
-__global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a) {
-    __shared__ uint4 kf[kFP * kFD / 8];          // keys as f16, [pos][256], 16-byte chunks swizzled by pos
-    __shared__ float ksc[kFP][kFD / 32];         // key scales
-    __shared__ uint32_t v8[kFP][F16 ? kFD / 2 : kFD / 4];  // values as stored (int8 or f16), [pos][256]
-    __shared__ float vsc[kFP][kFD / 32];         // value scales
-    __shared__ uint4 vt[2][kFD][kFP / 8];        // values hi / lo, [dim][pos]
-    __shared__ uint4 pw[kFThreads / 64][2][16][kFP / 8];  // per wave: P hi / lo, [row][pos]
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, kg = lane >> 4;
-    const unsigned h = blockIdx.y, kvh = h / (a.heads / a.kv_heads);
-    const unsigned t0 = blockIdx.x * kFQ;
-    const unsigned kv_dim = a.kv_heads * kFD;
-    const unsigned last = min(t0 + kFQ, a.n) - 1;   // the block's last token
-    const unsigned len = a.pos + last + 1;         // positions it attends to
+// ---------------------------------------------------------------- prefill, expanded cache
+//
+// The batch path in two launches.  k_kv_expand writes, per key/value head
+// and step of 32 positions, 64 KB exactly as k_attn_flash holds a step in
+// LDS, so that the attention kernel copies each step straight from global
+// memory into LDS (global_load_lds, no registers, no conversion):
+//   * keys [position r][64 chunks]: logical chunk c < 32 holds the f16 hi
+//     parts of dimensions 8c..8c+7, chunk 32 + c their lo parts; chunk c of
+//     row r is stored at c ^ (r % 16), so that the 16 lanes reading one
+//     chunk column of 16 rows hit 16 different bank groups;
+//   * values transposed, [part][dimension d][4 chunks of 8 positions], chunk
+//     j of row d stored at j ^ ((d / 4) % 4), likewise.
+// A Q8 value k8·s (an int8 times an f16 scale, 19 significant bits) is hi +
+// lo exactly; an f16 cache's value is its hi part, lo 0.  Positions past
+// the last are zeros.
+constexpr unsigned kXStep = 32;                  // positions a step
+constexpr size_t kXStepBytes = 65536;            // a step of one key/value head
+constexpr int kXThreads = 256;
 
-    // the wave's 16 queries as A fragments: row r16, dims 32g + 8kg..+7
+template <bool F16>
+__global__ void __launch_bounds__(kXThreads) k_kv_expand(uint4 *__restrict__ xs, const int8_t *__restrict__ kq,
+                                                          const uint16_t *__restrict__ ks,
+                                                          const int8_t *__restrict__ vq,
+                                                          const uint16_t *__restrict__ vs, unsigned len,
+                                                          unsigned steps, unsigned kv_heads) {
+    __shared__ float vt[kXStep][kFD + 1];
+    const unsigned s = blockIdx.x, kvh = blockIdx.y, t = threadIdx.x;
+    const unsigned r = t >> 3, c8 = t & 7;  // position r of the step, 32 dimensions 32·c8..
+    const unsigned p = s * kXStep + r;
+    const bool live = p < len;
+    const size_t off = (size_t)(live ? p : 0) * kv_heads * kFD + (size_t)kvh * kFD + 32 * c8;
+    uint4 *step = xs + ((size_t)kvh * steps + s) * (kXStepBytes / 16);
+    float kv[32], vv[32];
+    if constexpr (F16) {
+        const uint4 *k16 = (const uint4 *)((const uint16_t *)kq + off), *v16 = (const uint4 *)((const uint16_t *)vq + off);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 a = k16[i], b = v16[i];
+            const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                kv[8 * i + e] = half_of(aw[e / 2], e % 2);
+                vv[8 * i + e] = half_of(bw[e / 2], e % 2);
+            }
+        }
+    } else {
+        const float ksc = dq::from_f16(ks[off / 32]), vsc = dq::from_f16(vs[off / 32]);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint4 a = ((const uint4 *)(kq + off))[i], b = ((const uint4 *)(vq + off))[i];
+            const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                kv[16 * i + e] = (float)(int8_t)((aw[e / 4] >> (8 * (e % 4))) & 0xffu) * ksc;
+                vv[16 * i + e] = (float)(int8_t)((bw[e / 4] >> (8 * (e % 4))) & 0xffu) * vsc;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        kv[i] = live ? kv[i] : 0.0f;
+        vt[r][32 * c8 + i] = live ? vv[i] : 0.0f;
+    }
+    // keys: chunks 4·c8 + j (hi) and 32 + 4·c8 + j (lo) of row r
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const ahalf8 h = hi8(kv + 8 * j), l = lo8(kv + 8 * j, h);
+        const unsigned c = 4 * c8 + j;
+        step[r * 64 + (c ^ (r & 15))] = __builtin_bit_cast(uint4, h);
+        step[r * 64 + ((32 + c) ^ (r & 15))] = __builtin_bit_cast(uint4, l);
+    }
+    __syncthreads();
+    // values: thread t takes dimension t, 8 positions a chunk
+    uint4 *vdst = step + 2048;
+    const unsigned d = t, sw = (d >> 2) & 3;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) x[i] = vt[8 * j + i][d];
+        const ahalf8 h = hi8(x), l = lo8(x, h);
+        vdst[d * 4 + (j ^ sw)] = __builtin_bit_cast(uint4, h);
+        vdst[(kFD + d) * 4 + (j ^ sw)] = __builtin_bit_cast(uint4, l);
+    }
+}
+
+// Causal GQA for a batch of tokens over the expanded cache, on the f16
+// matrix cores.  A block of 8 waves takes one query head and 128 tokens, a
+// wave 16 of them; the longest tiles are dispatched first.  Per step of 32
+// positions, one barrier: every wave waits for its own copies of the step
+// (issued a step earlier into the other LDS buffer), the barrier makes the
+// whole step visible and frees the buffer of the step before, into which the
+// next step's copies are then issued.  Scores S = q·k take three MFMA chains
+// (q hi·k hi, q lo·k hi, q hi·k lo; the queries times 1/16 = 1/sqrt(256),
+// exact), the online softmax is the one above, and O += P·V three more
+// (P hi·V hi, P hi·V lo, P lo·V hi).
+constexpr int kFlashLds = 2 * (int)kXStepBytes + 8 * 2 * 16 * 4 * 16;
+
+struct FlashArgs {
+    float *out;
+    const float *q, *gate;
+    const uint8_t *xs;  // the expanded cache, [kv head][step][64 KB]
+    unsigned n, pos, heads, kv_heads, steps, tiles;
+};
+
+__global__ void __launch_bounds__(kFThreads) k_attn_flash(const FlashArgs a) {
+    extern __shared__ uint4 smem[];
+    uint4 *pwa = smem + 2 * (kXStepBytes / 16);  // per wave: P hi / lo, [row][4 chunks]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, kg = lane >> 4;
+    const unsigned tile = a.tiles - 1 - blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+    const unsigned kvh = h / (a.heads / a.kv_heads);
+    const unsigned t0 = tile * kFQ;
+    const unsigned last = min(t0 + kFQ, a.n) - 1;
+    const unsigned len = a.pos + last + 1;
+    const unsigned steps = (len + kXStep - 1) / kXStep;
+    const uint8_t *src = a.xs + (size_t)kvh * a.steps * kXStepBytes + 8192 * w + 16 * lane;
+    auto copy = [&](unsigned s) {
+        const uint8_t *g = src + (size_t)s * kXStepBytes;
+        uint8_t *d = (uint8_t *)(smem + (s & 1) * (kXStepBytes / 16)) + 8192 * w;
+#pragma unroll
+        for (int k = 0; k < 8; k++) lds_copy16(g + 1024 * k, d + 1024 * k);
+    };
+    copy(0);
+
     ahalf8 qh[8], ql[8];
     {
         const unsigned t = t0 + 16 * w + r16;
@@ -404,7 +493,6 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
             ql[g] = lo8(v, qh[g]);
         }
     }
-    // this lane's rows (C layout): 4kg + e of the wave's 16; their tokens
     unsigned tr[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) tr[e] = t0 + 16 * w + 4 * kg + e;
@@ -417,128 +505,27 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
     }
 #pragma unroll
     for (int i = 0; i < 16; i++) o[i] = afloat4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int vsw = (r16 >> 2) & 3;  // the value chunks' swizzle of this lane's dimensions
 
-    // staging: threads 0-255 take the keys, 256-511 the values, of position
-    // pp = (tid % 256) / 8, 32-byte piece c; the next step's are loaded while
-    // this step is computed
-    const int sp = (tid & 255) >> 3, sc8 = tid & 7;
-    const bool skeys = tid < 256;
-    const int8_t *const ssrc = skeys ? a.kq : a.vq;
-    const uint16_t *const sscl = skeys ? a.ks : a.vs;
-    uint4 nx[F16 ? 4 : 2];
-    uint16_t nxs;
-    auto fetch = [&](unsigned p0) {
-        const unsigned p = p0 + sp;
-        const bool live = p < len;
-        const size_t row = (size_t)(live ? p : 0) * kv_dim + (size_t)kvh * kFD;
-        const uint4 z = make_uint4(0, 0, 0, 0);
-        if constexpr (F16) {
-            const uint4 *src = (const uint4 *)((const uint16_t *)ssrc + row + 32 * sc8);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint4 v = src[i];
-                nx[i] = live ? v : z;
-            }
-            nxs = 0;
-        } else {
-            const uint4 v0 = *(const uint4 *)(ssrc + row + 32 * sc8), v1 = *(const uint4 *)(ssrc + row + 32 * sc8 + 16);
-            const uint16_t sv = sscl[row / 32 + sc8];
-            nx[0] = live ? v0 : z;
-            nx[F16 ? 1 : 1] = live ? v1 : z;
-            nxs = live ? sv : 0;
-        }
-    };
-    fetch(0);
-    for (unsigned p0 = 0; p0 < len; p0 += kFP) {
-        // ---- stage the 32 positions: keys to f16, values raw, scales
+    for (unsigned s = 0; s < steps; s++) {
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // this wave's copies of step s
         __syncthreads();
-        {
-            uint4 x[F16 ? 4 : 2];
-#pragma unroll
-            for (int i = 0; i < (F16 ? 4 : 2); i++) x[i] = nx[i];
-            const uint16_t xs = nxs;
-            if (p0 + kFP < len) fetch(p0 + kFP);
-            if constexpr (F16) {
-                // keys: as stored; values: raw words of two dims
-                if (skeys) {
-                    ksc[sp][sc8] = 1.0f;
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const int chunk = 4 * sc8 + q;
-                        kf[sp * 32 + (chunk ^ (sp & 15))] = x[q];
-                    }
-                } else {
-                    vsc[sp][sc8] = 1.0f;
-#pragma unroll
-                    for (int q = 0; q < 16; q++) v8[sp][16 * sc8 + q] = word_of(x[q / 4], q % 4);
-                }
-            } else if (skeys) {
-                ksc[sp][sc8] = dq::from_f16(xs);
-                const uint32_t kw[8] = {x[0].x, x[0].y, x[0].z, x[0].w, x[1].x, x[1].y, x[1].z, x[1].w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {  // 8 keys a 16-byte chunk of f16
-                    uint32_t hw[4];
-#pragma unroll
-                    for (int e = 0; e < 2; e++) {
-                        const uint32_t word = kw[2 * q + e];
-                        const _Float16 b0 = (_Float16)(float)(int8_t)(word & 0xffu), b1 = (_Float16)(float)(int8_t)((word >> 8) & 0xffu);
-                        const _Float16 b2 = (_Float16)(float)(int8_t)((word >> 16) & 0xffu), b3 = (_Float16)(float)(int8_t)(word >> 24);
-                        hw[2 * e] = (uint32_t)__builtin_bit_cast(uint16_t, b0) | (uint32_t)__builtin_bit_cast(uint16_t, b1) << 16;
-                        hw[2 * e + 1] = (uint32_t)__builtin_bit_cast(uint16_t, b2) | (uint32_t)__builtin_bit_cast(uint16_t, b3) << 16;
-                    }
-                    const int chunk = 4 * sc8 + q;  // of 32 per row
-                    kf[sp * 32 + (chunk ^ (sp & 15))] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-                }
-            } else {
-                vsc[sp][sc8] = dq::from_f16(xs);
-                const uint32_t vw[8] = {x[0].x, x[0].y, x[0].z, x[0].w, x[1].x, x[1].y, x[1].z, x[1].w};
-#pragma unroll
-                for (int q = 0; q < 8; q++) v8[sp][8 * sc8 + q] = vw[q];
-            }
-        }
-        __syncthreads();
-        // ---- the values transposed: thread (dims 4dq + 2hf, + 1; positions 8j..8j+7)
-        {
-            const int dq4 = tid & 63, j = (tid >> 6) & 3, hf = tid >> 8;
-            float vv[2][8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int p = 8 * j + i;
-                if constexpr (F16) {
-                    const uint32_t word = v8[p][2 * dq4 + hf];  // dims 4dq4 + 2hf, + 1
-#pragma unroll
-                    for (int d = 0; d < 2; d++) vv[d][i] = half_of(word, d);
-                } else {
-                    const uint32_t word = v8[p][dq4];
-                    const float sc = vsc[p][dq4 / 8];
-#pragma unroll
-                    for (int d = 0; d < 2; d++) vv[d][i] = (float)(int8_t)((word >> (8 * (2 * hf + d))) & 0xffu) * sc;
-                }
-            }
-#pragma unroll
-            for (int d = 0; d < 2; d++) {
-                const ahalf8 hh = hi8(vv[d]), ll = lo8(vv[d], hh);
-                vt[0][4 * dq4 + 2 * hf + d][j] = __builtin_bit_cast(uint4, hh);
-                vt[1][4 * dq4 + 2 * hf + d][j] = __builtin_bit_cast(uint4, ll);
-            }
-        }
-        __syncthreads();
+        if (s + 1 < steps) copy(s + 1);
+        const uint4 *K = smem + (s & 1) * (kXStepBytes / 16), *V = K + 2048;
+        const unsigned p0 = s * kXStep;
         // ---- scores of the wave's 16 rows against the 32 positions (2 tiles)
-        afloat4 sacc[2];
+        afloat4 sacc[2] = {afloat4{0.0f, 0.0f, 0.0f, 0.0f}, afloat4{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-        for (int tcol = 0; tcol < 2; tcol++) {
-            sacc[tcol] = afloat4{0.0f, 0.0f, 0.0f, 0.0f};
-            const int pp = 16 * tcol + r16;  // B column: position
+        for (int g = 0; g < 8; g++)
 #pragma unroll
-            for (int g = 0; g < 8; g++) {
-                const ahalf8 kb = __builtin_bit_cast(ahalf8, kf[pp * 32 + ((4 * g + kg) ^ (pp & 15))]);
-                afloat4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[g], kb, afloat4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[g], kb, c, 0, 0, 0);
-                const float sc = ksc[pp][g];  // C column r16 is this position
-#pragma unroll
-                for (int e = 0; e < 4; e++) sacc[tcol][e] += sc * c[e];
+            for (int tcol = 0; tcol < 2; tcol++) {
+                const int row = 16 * tcol + r16;
+                const ahalf8 kh = __builtin_bit_cast(ahalf8, K[row * 64 + ((4 * g + kg) ^ r16)]);
+                const ahalf8 kl = __builtin_bit_cast(ahalf8, K[row * 64 + ((32 + 4 * g + kg) ^ r16)]);
+                sacc[tcol] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[g], kh, sacc[tcol], 0, 0, 0);
+                sacc[tcol] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[g], kh, sacc[tcol], 0, 0, 0);
+                sacc[tcol] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[g], kl, sacc[tcol], 0, 0, 0);
             }
-        }
         // ---- mask, online softmax (rows 4kg + e; the 16 lanes of a row group hold its columns)
         float pv[2][4];
 #pragma unroll
@@ -569,7 +556,7 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
         }
         // ---- P to the A layout through the wave's LDS tile (hi, lo)
         {
-            _Float16 *ph = (_Float16 *)&pw[w][0][0][0], *pl = (_Float16 *)&pw[w][1][0][0];
+            _Float16 *ph = (_Float16 *)(pwa + w * 128), *pl = (_Float16 *)(pwa + w * 128 + 64);
 #pragma unroll
             for (int tcol = 0; tcol < 2; tcol++)
 #pragma unroll
@@ -582,14 +569,14 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const ahalf8 pa_h = __builtin_bit_cast(ahalf8, pw[w][0][r16][kg]);
-        const ahalf8 pa_l = __builtin_bit_cast(ahalf8, pw[w][1][r16][kg]);
+        const ahalf8 pa_h = __builtin_bit_cast(ahalf8, pwa[w * 128 + r16 * 4 + kg]);
+        const ahalf8 pa_l = __builtin_bit_cast(ahalf8, pwa[w * 128 + 64 + r16 * 4 + kg]);
         // ---- O += P·V over the 16 dimension tiles
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int d = 16 * i + r16;  // B column: dimension
-            const ahalf8 vh = __builtin_bit_cast(ahalf8, vt[0][d][kg]);
-            const ahalf8 vl = __builtin_bit_cast(ahalf8, vt[1][d][kg]);
+            const int d = 16 * i + r16;
+            const ahalf8 vh = __builtin_bit_cast(ahalf8, V[d * 4 + (kg ^ vsw)]);
+            const ahalf8 vl = __builtin_bit_cast(ahalf8, V[(kFD + d) * 4 + (kg ^ vsw)]);
             o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa_h, vh, o[i], 0, 0, 0);
             o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa_h, vl, o[i], 0, 0, 0);
             o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa_l, vh, o[i], 0, 0, 0);
@@ -611,7 +598,6 @@ __global__ void __launch_bounds__(kFThreads) k_attn_prefill(const PrefillArgs a)
         }
     }
 }
-
 }  // namespace
 
 // The decode path's partial results: [token][head][chunk][head_dim + 2] floats.
@@ -633,14 +619,29 @@ namespace {
 // `partials` (at least attention_partials_floats).
 hipError_t attention_run(dwim_dev *dev, float *partials, float *out, const float *q, const dwim_cache *k,
                          const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
-                         size_t n_kv_heads, const float *gate, planes::View pv) {
+                         size_t n_kv_heads, const float *gate, planes::View pv, uint8_t *kvx) {
     if (n >= 16 && !pv.q && head_dim == (size_t)kFD && n_heads % n_kv_heads == 0) {
-        // a batch of tokens: flash attention on the matrix cores
-        PrefillArgs pa{out, q, gate, k->q, v->q, k->s, v->s, (unsigned)n, (unsigned)pos, (unsigned)n_heads,
-                       (unsigned)n_kv_heads};
-        dim3 grid((unsigned)((n + kFQ - 1) / kFQ), (unsigned)n_heads);
-        if (k->f16) k_attn_prefill<true><<<grid, kFThreads, 0, dev->stream>>>(pa);
-        else k_attn_prefill<false><<<grid, kFThreads, 0, dev->stream>>>(pa);
+        // a batch of tokens over the expanded cache (kvx: attention_kvx_bytes)
+        const size_t len = pos + n, steps = (len + kXStep - 1) / kXStep;
+        dim3 gx((unsigned)steps, (unsigned)n_kv_heads);
+        if (k->f16)
+            k_kv_expand<true><<<gx, kXThreads, 0, dev->stream>>>((uint4 *)kvx, k->q, k->s, v->q, v->s, (unsigned)len,
+                                                               (unsigned)steps, (unsigned)n_kv_heads);
+        else
+            k_kv_expand<false><<<gx, kXThreads, 0, dev->stream>>>((uint4 *)kvx, k->q, k->s, v->q, v->s, (unsigned)len,
+                                                                (unsigned)steps, (unsigned)n_kv_heads);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        static bool raised = false;
+        if (!raised) {
+            e = hipFuncSetAttribute((const void *)k_attn_flash, hipFuncAttributeMaxDynamicSharedMemorySize, kFlashLds);
+            if (e != hipSuccess) return e;
+            raised = true;
+        }
+        const unsigned tiles = (unsigned)((n + kFQ - 1) / kFQ);
+        FlashArgs fa{out, q, gate, kvx, (unsigned)n, (unsigned)pos, (unsigned)n_heads, (unsigned)n_kv_heads,
+                     (unsigned)steps, tiles};
+        k_attn_flash<<<tiles * (unsigned)n_heads, kFThreads, kFlashLds, dev->stream>>>(fa);
         return hipGetLastError();
     }
     const size_t len = pos + n, ch = kPos, chunks = (len + ch - 1) / ch;
@@ -691,8 +692,22 @@ hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, con
     if (!batch) {
         hipError_t e = attention_reserve(dev, attention_partials_floats(n, pos, n_heads, head_dim));
         if (e != hipSuccess) return e;
+        return attention_run(dev, dev->partials, out, q, k, v, n, pos, n_heads, head_dim, n_kv_heads, gate, pv,
+                             nullptr);
     }
-    return attention_run(dev, dev->partials, out, q, k, v, n, pos, n_heads, head_dim, n_kv_heads, gate, pv);
+    hipError_t e = attention_kvx_reserve(dev, attention_kvx_bytes(pos + n, n_kv_heads));
+    if (e != hipSuccess) return e;
+    return attention_run(dev, dev->partials, out, q, k, v, n, pos, n_heads, head_dim, n_kv_heads, gate, pv,
+                         (uint8_t *)dev->kvx);
+}
+
+// The expanded cache of a batch over `len` positions (head_dim 256).
+size_t attention_kvx_bytes(size_t len, size_t n_kv_heads) {
+    return (len + kXStep - 1) / kXStep * kXStepBytes * n_kv_heads;
+}
+
+hipError_t attention_kvx_reserve(dwim_dev *dev, size_t bytes) {
+    return dev_grow(dev, &dev->kvx, &dev->kvx_cap, bytes, 1);
 }
 
 // ---------------------------------------------------------------- without allocating
@@ -733,14 +748,14 @@ extern "C" int dwim_attention_noalloc(dwim_dev *dev, dwim_buf *out, const dwim_b
     DWIM_CHECK(dev->attn_scratch != nullptr, "attention_noalloc: the device's scratch array has no address");
     if (n == 0) return 0;
     const bool batch = n >= 16 && head_dim == (size_t)kFD;
-    if (!batch) {
-        const size_t need = attention_partials_floats(n, pos, n_heads, head_dim);
-        DWIM_CHECK(need <= kScratchFloats,
-                   "attention_noalloc: " + std::to_string(n) + " tokens at position " + std::to_string(pos) +
-                       " need " + std::to_string(need * 4) + " bytes of partial results, more than the " +
-                       std::to_string(kScratchFloats * 4) + " bytes of its scratch array");
-    }
+    // the decode path's partial results, or a batch's expanded cache
+    const size_t need = batch ? attention_kvx_bytes(pos + n, n_kv_heads)
+                              : attention_partials_floats(n, pos, n_heads, head_dim) * sizeof(float);
+    DWIM_CHECK(need <= kScratchFloats * sizeof(float),
+               "attention_noalloc: " + std::to_string(n) + " tokens at position " + std::to_string(pos) + " need " +
+                   std::to_string(need) + " bytes of " + (batch ? "expanded cache" : "partial results") +
+                   ", more than the " + std::to_string(kScratchFloats * 4) + " bytes of its scratch array");
     DWIM_HIP(attention_run(dev, dev->attn_scratch, out->data, q->data, k_cache, v_cache, n, pos, n_heads, head_dim,
-                           n_kv_heads, nullptr, planes::View{}));
+                           n_kv_heads, nullptr, planes::View{}, (uint8_t *)dev->attn_scratch));
     return 0;
 }

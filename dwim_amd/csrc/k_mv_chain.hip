@@ -154,16 +154,6 @@ DEV Where locate(const Product *prods, unsigned np, unsigned item) {
     return w;
 }
 
-// One wave's copy of 64 × 16 bytes from global memory (lane l's address) into
-// LDS at dst + 16·l: global_load_lds_dwordx4 with the LDS base in M0.  Issued
-// as inline assembly so that the compiler does not wait for every earlier
-// vector memory operation before it (it cannot tell that the copies of an
-// item go to LDS no earlier copy writes); the kernel waits for them itself
-// (wait_vm) before a barrier, then reads them.
-DEV void lds_copy16(const uint8_t *src, uint8_t *dst) {
-    const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) uint8_t *)dst);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(base), "v"(src) : "memory", "m0");
-}
 
 // Copies an item's weight units into an LDS slot: 1 KB pieces, piece k by
 // wave k % kCopyWaves.  Returns how many copies this wave issued.

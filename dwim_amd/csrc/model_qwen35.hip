@@ -1008,6 +1008,7 @@ struct dwim_model {
         DWIM_HIP(attention_reserve(
             dev, attention_partials_floats(small, max_len > small ? max_len - small : 0, c.heads, c.head_dim)));
         DWIM_HIP(delta_net_reserve(dev, most, c.v_heads));
+        if (c.head_dim == 256 && most >= 16) DWIM_HIP(attention_kvx_reserve(dev, attention_kvx_bytes(max_len, c.kv_heads)));
         if (fmt == DWIM_Q4_K) {
             const size_t H = c.hidden, I = c.intermediate;
             const size_t shapes[][2] = {{q_dim(), H}, {kv_dim(), H}, {H, q_dim()}, {2 * k_dim() + v_dim(), H},

@@ -36,6 +36,8 @@ struct dwim_dev {
     size_t work_cap = 0;     // floats
     float *gemm_parts = nullptr;  // a k-split batch product's partial results (k_gemm_q4k)
     size_t gemm_parts_cap = 0;    // floats
+    void *kvx = nullptr;          // a batch attention's expanded key/value cache (k_attention.hip)
+    size_t kvx_cap = 0;           // bytes
     float *dn_work = nullptr;     // a batch delta rule's per-chunk matrices (k_delta_net.hip)
     size_t dn_work_cap = 0;       // floats
     // Split one-token Q4_K products (k_mv_q4k_mfma.hip): the partial sums of
@@ -278,6 +280,8 @@ hipError_t launch_mv_chain(dwim_dev *dev, const ChainStep *steps, int n);
 int chain_error(dwim_dev *dev);
 size_t attention_partials_floats(size_t n, size_t pos, size_t n_heads, size_t head_dim);
 hipError_t attention_reserve(dwim_dev *dev, size_t floats);
+size_t attention_kvx_bytes(size_t len, size_t n_kv_heads);
+hipError_t attention_kvx_reserve(dwim_dev *dev, size_t bytes);
 hipError_t attention_scratch_init(dwim_dev *dev);
 hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                                   const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,

@@ -132,6 +132,7 @@ void dwim_dev_release_resources(dwim_dev *dev) {
     if (dev->work) hipFree(dev->work);
     if (dev->gemm_parts) hipFree(dev->gemm_parts);
     if (dev->dn_work) hipFree(dev->dn_work);
+    if (dev->kvx) hipFree(dev->kvx);
     hipStreamDestroy(dev->stream);
     delete dev;
 }

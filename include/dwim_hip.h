@@ -142,12 +142,15 @@ int dwim_attention(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_c
 /* No counterpart in the reference: dwim_attention for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  The same kernels and results as
- * dwim_attention, but the decode path's partial results live in a file-scope
- * device array of 64 MiB per GPU (held until the process ends) instead of a
- * buffer the library grows: no hipMalloc or hipFree is called.  Fails with a
- * clear error when n·n_heads·ceil((pos + n)/64)·(head_dim + 2) floats exceed
- * it (one token of 24 heads of 256 reaches past 170 000 positions).  Calls
- * that overlap on one GPU share the array and race. */
+ * dwim_attention, but the decode path's partial results (fewer than 16
+ * tokens) or a batch's expanded key/value cache (16 tokens or more, head_dim
+ * 256) live in a file-scope device array of 64 MiB per GPU (held until the
+ * process ends) instead of a buffer the library grows: no hipMalloc or
+ * hipFree is called.  Fails with a clear error when they exceed it: the
+ * partials are n·n_heads·ceil((pos + n)/64)·(head_dim + 2) floats (one token
+ * of 24 heads of 256 reaches past 170 000 positions), the expanded cache
+ * 64 KiB per 32 positions and key/value head (8192 positions at 4 key/value
+ * heads).  Calls that overlap on one GPU share the array and race. */
 int dwim_attention_noalloc(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_cache *k_cache,
                            const dwim_cache *v_cache, size_t pos, size_t n_heads, size_t head_dim,
                            size_t n_kv_heads);

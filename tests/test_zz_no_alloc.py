@@ -44,4 +44,10 @@ def test_noalloc_attention_refuses_more_than_its_scratch():
     q, out = gpu.alloc(n * heads * hd), gpu.alloc(n * heads * hd)
     with pytest.raises(D.DwimError, match="scratch array"):
         gpu.attention_noalloc(out, q, kc, vc, pos, heads, hd, kvh)
+    # a batch's expanded cache: 64 KiB per 32 positions and key/value head,
+    # 8192 positions at 4 heads; 16 tokens at 8180 pass that
+    n, pos = 16, 8180
+    q, out = gpu.alloc(n * heads * hd), gpu.alloc(n * heads * hd)
+    with pytest.raises(D.DwimError, match="expanded cache"):
+        gpu.attention_noalloc(out, q, kc, vc, pos, heads, hd, kvh)
     gpu.close()
