@@ -101,3 +101,16 @@ DEV void lds_copy16(const uint8_t *src, uint8_t *dst) {
     const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) uint8_t *)dst);
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(base), "v"(src) : "memory", "m0");
 }
+
+// The same copy with the source as a 64-bit base held in SGPRs (the same for
+// every lane) plus a 32-bit byte offset per lane: one VGPR an address.
+DEV void lds_copy16_off(const void *base, uint32_t off, uint8_t *dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) uint8_t *)dst);
+    const uint64_t b = (uint64_t)base;
+    // (readfirstlane returns an int: through unsigned, so that the low word
+    // is not sign-extended into the high one)
+    const uint64_t sb = (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)b) |
+                        (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)(b >> 32)) << 32;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" : : "s"(m0), "v"(off), "s"(sb)
+                 : "memory", "m0");
+}

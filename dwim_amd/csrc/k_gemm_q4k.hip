@@ -19,8 +19,10 @@
 // Its waves have two roles, one of each on every SIMD, so that the matrix
 // cores and the vector ALUs work at once: four matrix waves (a 128 × 64 part
 // each, 8 × 4 MFMA tiles) multiply step s out of one buffer while four loader
-// waves dequantize step s + 1 (loaded from global memory during step s − 1)
-// into the other and issue the loads of step s + 2.  LDS rows are 128 bytes whose 16-byte chunks are XOR-swizzled by row,
+// waves dequantize step s + 1's weights (loaded from global memory during step
+// s − 1) into the other and issue the loads of step s + 2.  The activations
+// of step s + 1 are copied into the other buffer by the matrix waves
+// themselves, straight from global memory into LDS.  LDS rows are 128 bytes whose 16-byte chunks are XOR-swizzled by row,
 // so that the 16 lanes reading one k-slice of 16 rows hit different banks.  Workgroups are numbered XCD-major: those on
 // one XCD share its L2 and mostly one token tile.
 #include "device_util.h"
@@ -110,11 +112,10 @@ DEV uint32_t pack2(_Float16 a, _Float16 b) {
 }
 
 // A loader thread's global loads of one step: its row's 32 quant bytes of
-// the group and 16-byte header, its token's 64 hi or lo activations, and 16
-// bytes of its token's sub-block sums (the header and sums are reloaded every
-// step; they only change per block).
+// the group and 16-byte header, and 16 bytes of its token's sub-block sums
+// (the header and sums are reloaded every step; they only change per block).
 struct StepLoad {
-    uint4 q[2], hdr, x[8], m;
+    uint4 q[2], hdr, m;
 };
 
 __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
@@ -144,25 +145,12 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         const unsigned wtile = (row0 + ar) / 16;
         const bool wlive = wtile < wtiles;
         typedef const __attribute__((address_space(1))) u4v *gq;
-        // activations: 16-byte chunk xc of the group's 64 halves of tokens
-        // xt + 32k (k = 0..3), hi and lo parts: eight lanes read a token's
-        // 128 bytes, so that a wave's load touches eight cache lines
-        const int xc = lt & 7, xt = lt >> 3;
-        bool xlv[4];
-        gq xsrc[4];
         // sub-block sums: token bt, 16 bytes bq
         const int bt = lt >> 1, bq = lt & 1;
         const bool xlive = tok0 + bt < a.n;
         const uint8_t *wsrc = a.w + ((size_t)(wlive ? wtile : 0) * nbt + b0) * q4kt::kUnit;
         const gq qsrc = (gq)(wsrc + q4kt::qs_off(0, (row0 + ar) % 16));
         const gq hsrc = (gq)(wsrc + q4kt::meta_off((row0 + ar) % 16));
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const unsigned t = tok0 + xt + 32 * k;
-            xlv[k] = t < a.n;
-            xsrc[k] = (gq)(a.xh + (size_t)(xlv[k] ? t : tok0) * a.cols + 256 * b0 + 8 * xc);
-        }
-        const size_t lo_off = (size_t)(a.xl - a.xh) / 8;  // the lo parts, in 16-byte chunks
         const gq ms0 = (gq)(a.xm + ((size_t)(tok0 + (xlive ? bt : 0)) * nbt + b0) * 16 + 8 * bq);
         const uint4 z4 = make_uint4(0, 0, 0, 0);
         // step s: block s / 4 (unit b·2304), group s % 4 (512 bytes); x at
@@ -176,11 +164,6 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
             }
             const uint4 h = __builtin_bit_cast(uint4, hsrc[b * q4kt::kUnit / 16]);
             L.hdr = wlive ? h : z4;  // zero: d = dmin = 0
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint4 v = __builtin_bit_cast(uint4, xsrc[k & 3][s * (kStep / 8) + (k >= 4 ? lo_off : 0)]);
-                L.x[k] = xlv[k & 3] ? v : z4;
-            }
             const uint4 m = __builtin_bit_cast(uint4, ms0[b * 2]);
             L.m = xlive ? m : z4;
         };
@@ -232,11 +215,6 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
                 row[swz(ar, 2 * hq + 1)] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
                 row[swz(ar, 4 + 2 * hq)] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
                 row[swz(ar, 5 + 2 * hq)] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int t = xt + 32 * (k & 3);
-                (k >= 4 ? Bl : Bh)[(buf * kToks + t) * 8 + swz(t, xc)] = L.x[k];
             }
             if (g == 0) {
                 // the block's min operands −dmin·m_sb/unit (hi, lo), the unit
@@ -303,6 +281,37 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = float16v{};
+    // The activations of step s (hi and lo parts, 32 KB) go into buffer
+    // s % 2 straight from global memory (global_load_lds, no registers), 32
+    // copies of 8 token rows, wave `wave` taking 8 of them: lane l lands in
+    // row 8·(k % 16) + l / 8 at physical chunk l % 8, so it reads the logical
+    // chunk that the row's swizzle puts there.  A step's copies are issued
+    // when the barrier before it has freed the buffer, and waited for before
+    // the barrier that publishes it.
+    // Wave w copies part w / 2 (hi, lo) of token rows 64·(w % 2) + 8j + l / 8
+    // (j = 0..7); the logical chunk of physical chunk l % 8 in row r is
+    // (l % 8) ^ ((r / 2) % 8), which for these rows depends on j's parity.
+    const _Float16 *xpart = wave >= 2 ? a.xl : a.xh;
+    const unsigned trow0 = 64u * (wave & 1) + (unsigned)(lane >> 3);
+    const unsigned cj0 = (unsigned)(lane & 7) ^ ((trow0 >> 1) & 7);
+    const unsigned rowoff0 = (tok0 + trow0) * a.cols + 256u * b0;  // halves
+    auto dma = [&](unsigned s) {
+        const unsigned buf = s % 2;
+        // (opaque copies, so that the offsets are formed here each step
+        // rather than kept in registers across the step)
+        unsigned r0 = rowoff0, t0r = tok0 + trow0, c0 = cj0;
+        asm volatile("" : "+v"(r0), "+v"(t0r), "+v"(c0));
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const bool live = t0r + 8u * j < a.n;
+            const unsigned ro = live ? r0 + 8u * j * a.cols : tok0 * a.cols + 256u * b0;
+            const unsigned off = 2u * (ro + s * kStep + 8u * ((j & 1) ? c0 ^ 4u : c0));
+            uint4 *dst = (wave >= 2 ? Bl : Bh) + (buf * kToks + 64 * (wave & 1) + 8 * j) * 8;
+            lds_copy16_off(xpart, off, (uint8_t *)dst);
+        }
+    };
+    dma(0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
     struct Frags {
         half8 a[4], bh[2], bl[2];
@@ -355,6 +364,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     Frags f0, f1;
     auto step = [&](unsigned s, int g) {
         const unsigned buf = s % 2, bb = (s / 4) % 2;
+        if (s + 1 < steps) dma(s + 1);
         read(buf, 0, f0);
         if (g == 0 && s > 0) scale_rows(Dr + bb * kRows);
         read(buf, 1, f1);
@@ -403,6 +413,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
                 }
             }
         }
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // this wave's copies of step s + 1
         __syncthreads();
     };
     for (unsigned b = 0; b < nb; b++) {
