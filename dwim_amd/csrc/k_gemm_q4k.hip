@@ -336,14 +336,17 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) f.a[i] = __builtin_bit_cast(half8, pa[ks][(buf * kRows + i * 32) * 8]);
     };
+    // (the hi products of the 8 tiles, then the lo ones: an accumulator's two
+    // MFMAs are 8 apart, not back to back)
     auto mma = [&](const Frags &f) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.bh[j], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.bl[j], acc[i][j], 0, 0, 0);
-            }
+            for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.bl[j], acc[i][j], 0, 0, 0);
     };
     // per-row factors of this lane's rows: tile i, rows 8g + 4kh + e
     auto scale_rows = [&](const float *v) {
