@@ -39,7 +39,7 @@ typedef unsigned u4v __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int kRows = 256, kToks = 128, kStep = 64;
-constexpr int kThreads = 512;
+constexpr int kThreads = 768;  // 8 matrix waves, 4 loader waves
 
 // x [n][cols] f32 -> xh, xl [n][cols] f16 (hi and lo parts), and per
 // (token, block) xm [n][nb][16] f16: the 8 sub-block sums' hi parts, then
@@ -137,9 +137,9 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     const unsigned nbt = a.cols / 256, b0 = part * nbt / a.parts, nb = (part + 1) * nbt / a.parts - b0;
     const unsigned steps = 4 * nb, wtiles = (a.rows + 15) / 16;
 
-    if (wave >= 4) {
+    if (wave >= 8) {
         // ---------------- loader waves: 256 threads
-        const int lt = tid - 256;
+        const int lt = tid - 512;
         // weights: row ar, the group's 32 quant bytes
         const int ar = lt;
         const unsigned wtile = (row0 + ar) / 16;
@@ -264,8 +264,8 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         return;
     }
 
-    // ---------------- matrix waves: wave (wr, wc) computes rows 128·wr..,
-    // tokens 64·wc.., as 4 × 2 tiles of 32 × 32 (v_mfma_f32_32x32x16_f16:
+    // ---------------- matrix waves: wave (wr, wc) computes rows 64·wr..,
+    // tokens 64·wc.., as 2 × 2 tiles of 32 × 32 (v_mfma_f32_32x32x16_f16:
     // lane l holds A's row l % 32, B's column l % 32, at k 8(l / 32)..+7 of
     // a 16-wide k slice; C's column l % 32, rows 8g + 4(l / 32) + e).  A
     // step's four k slices are software-pipelined: slice k + 1's fragments are
@@ -276,23 +276,23 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     // unit_b / unit_{b+1}, once, at the end by the last unit.
     const int wr = wave >> 1, wc = wave & 1;
     const int r32 = lane & 31, kh = lane >> 5;
-    float16v acc[4][2];
+    float16v acc[2][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = float16v{};
     // The activations of step s (hi and lo parts, 32 KB) go into buffer
     // s % 2 straight from global memory (global_load_lds, no registers), 32
-    // copies of 8 token rows, wave `wave` taking 8 of them: lane l lands in
+    // copies of 8 token rows, wave `wave` taking 4 of them: lane l lands in
     // row 8·(k % 16) + l / 8 at physical chunk l % 8, so it reads the logical
     // chunk that the row's swizzle puts there.  A step's copies are issued
     // when the barrier before it has freed the buffer, and waited for before
     // the barrier that publishes it.
-    // Wave w copies part w / 2 (hi, lo) of token rows 64·(w % 2) + 8j + l / 8
-    // (j = 0..7); the logical chunk of physical chunk l % 8 in row r is
+    // Wave w copies part w / 4 (hi, lo) of token rows 32·(w % 4) + 8j + l / 8
+    // (j = 0..3); the logical chunk of physical chunk l % 8 in row r is
     // (l % 8) ^ ((r / 2) % 8), which for these rows depends on j's parity.
-    const _Float16 *xpart = wave >= 2 ? a.xl : a.xh;
-    const unsigned trow0 = 64u * (wave & 1) + (unsigned)(lane >> 3);
+    const _Float16 *xpart = wave >= 4 ? a.xl : a.xh;
+    const unsigned trow0 = 32u * (wave & 3) + (unsigned)(lane >> 3);
     const unsigned cj0 = (unsigned)(lane & 7) ^ ((trow0 >> 1) & 7);
     const unsigned rowoff0 = (tok0 + trow0) * a.cols + 256u * b0;  // halves
     auto dma = [&](unsigned s) {
@@ -302,11 +302,11 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         unsigned r0 = rowoff0, t0r = tok0 + trow0, c0 = cj0;
         asm volatile("" : "+v"(r0), "+v"(t0r), "+v"(c0));
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < 4; j++) {
             const bool live = t0r + 8u * j < a.n;
             const unsigned ro = live ? r0 + 8u * j * a.cols : tok0 * a.cols + 256u * b0;
             const unsigned off = 2u * (ro + s * kStep + 8u * ((j & 1) ? c0 ^ 4u : c0));
-            uint4 *dst = (wave >= 2 ? Bl : Bh) + (buf * kToks + 64 * (wave & 1) + 8 * j) * 8;
+            uint4 *dst = (wave >= 4 ? Bl : Bh) + (buf * kToks + 32 * (wave & 3) + 8 * j) * 8;
             lds_copy16_off(xpart, off, (uint8_t *)dst);
         }
     };
@@ -314,7 +314,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
     struct Frags {
-        half8 a[4], bh[2], bl[2];
+        half8 a[2], bh[2], bl[2];
     };
     // a lane's LDS rows (A: rows 128wr + 32i + l % 32; B: tokens 64wc + 32j
     // + l % 32) share the swizzle (l % 32 / 2) % 8, so per k slice one
@@ -324,7 +324,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         const int c = (2 * ks + kh) ^ sw;
-        pa[ks] = A + (wr * 128 + r32) * 8 + c;
+        pa[ks] = A + (wr * 64 + r32) * 8 + c;
         pb[ks] = Bh + (wc * 64 + r32) * 8 + c;
     }
     auto read = [&](unsigned buf, int ks, Frags &f) {
@@ -334,27 +334,27 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
             f.bl[j] = __builtin_bit_cast(half8, pb[ks][(buf * kToks + j * 32) * 8 + 2 * kToks * 8]);
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) f.a[i] = __builtin_bit_cast(half8, pa[ks][(buf * kRows + i * 32) * 8]);
+        for (int i = 0; i < 2; i++) f.a[i] = __builtin_bit_cast(half8, pa[ks][(buf * kRows + i * 32) * 8]);
     };
     // (the hi products of the 8 tiles, then the lo ones: an accumulator's two
     // MFMAs are 8 apart, not back to back)
     auto mma = [&](const Frags &f) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.bh[j], acc[i][j], 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.bl[j], acc[i][j], 0, 0, 0);
     };
     // per-row factors of this lane's rows: tile i, rows 8g + 4kh + e
     auto scale_rows = [&](const float *v) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const float4 d = *(const float4 *)&v[wr * 128 + i * 32 + 8 * g + 4 * kh];
+                const float4 d = *(const float4 *)&v[wr * 64 + i * 32 + 8 * g + 4 * kh];
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     acc[i][j][4 * g] *= d.x;
@@ -377,20 +377,22 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         read(buf, 3, f1);
         mma(f0);
         mma(f1);
-        // the order the scheduler keeps: slice 0's 8 fragment reads, then the
-        // 16 MFMAs of slices 0-2 each with the next slice's reads between
-        // them (a read after every two MFMAs), then slice 3's MFMAs; left to
-        // itself it reuses one set of fragment registers and waits for each
-        // read
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        // the order the scheduler keeps: slice 0's 6 fragment reads, then the
+        // 8 MFMAs of slices 0-2 each with the next slice's reads between
+        // them (a read after each of the first six), then slice 3's MFMAs;
+        // left to itself it reuses one set of fragment registers and waits
+        // for each read
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
-        for (int k = 0; k < 3; k++)
+        for (int k = 0; k < 3; k++) {
 #pragma unroll
-            for (int r = 0; r < 8; r++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            for (int r = 0; r < 6; r++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
         if (g == 3) {
             // the block's min term, in its unit: [−hi, −hi]·[X_hi, X_lo] and
             // [−lo, 0]·[X_hi, 0] over the 8 sub-blocks of each k half
@@ -405,8 +407,8 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
                 x2[j] = kh == 0 ? xh : zero;
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = wr * 128 + i * 32 + r32;
+            for (int i = 0; i < 2; i++) {
+                const int r = wr * 64 + i * 32 + r32;
                 const half8 mh = __builtin_bit_cast(half8, Am[(bb * kRows + r) * 2]);
                 const half8 ml = kh == 0 ? __builtin_bit_cast(half8, Am[(bb * kRows + r) * 2 + 1]) : zero;
 #pragma unroll
@@ -435,10 +437,10 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         const unsigned t = tok0 + wc * 64 + j * 32 + r32;
         if (t >= a.n) continue;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const unsigned r = row0 + wr * 128 + i * 32 + 8 * g + 4 * kh;
+                const unsigned r = row0 + wr * 64 + i * 32 + 8 * g + 4 * kh;
                 float *o = dst + (size_t)t * a.rows + r;
                 if (a.rows % 4 == 0 && r + 3 < a.rows) {
                     // four rows of the token: one 16-byte access
