@@ -462,3 +462,33 @@ hipError_t launch_synthetic_bf16(hipStream_t s, uint16_t *q, size_t rows, size_t
     k_synthetic_bf16<<<blocks_for(n, 256), 256, 0, s>>>(q, n, seed, c);
     return hipGetLastError();
 }
+
+// ---------------------------------------------------------------- measurement
+// The streaming floor the decode products are measured against: a read of
+// `bytes` (a multiple of 16) and nothing else, 16 bytes a lane, eight loads
+// in flight a lane, grid-strided over a fixed grid.  The words are folded
+// into one value that is stored only if it equals `never`, so that no load
+// is dropped.  No counterpart in the reference; measurement only.
+__global__ void __launch_bounds__(256) k_stream_read(const uint4 *__restrict__ p, size_t n, unsigned never,
+                                                     unsigned *sink) {
+    unsigned x = 0;
+    const size_t step = (size_t)gridDim.x * 256 * 8;
+    for (size_t i0 = (size_t)blockIdx.x * 256 * 8 + threadIdx.x; i0 < n; i0 += step) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const size_t i = i0 + (size_t)u * 256;
+            v[u] = p[i < n ? i : i0];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) x ^= (v[u].x ^ v[u].y) ^ (v[u].z ^ v[u].w);
+    }
+    if (x == never) sink[0] = x;
+}
+
+extern "C" int dwim_measure_stream(dwim_dev *dev, const void *p, size_t bytes, unsigned *sink, unsigned blocks) {
+    if (!dev || !p || !sink || bytes % 16 || blocks == 0) return dwim_fail("measure_stream: bad arguments");
+    k_stream_read<<<blocks, 256, 0, dev->stream>>>((const uint4 *)p, bytes / 16, 0x9e3779b9u, sink);
+    DWIM_HIP(hipGetLastError());
+    return 0;
+}

@@ -2,6 +2,7 @@
 
     python -m dwim_amd.kernel_workloads attention [--reps N]
     python -m dwim_amd.kernel_workloads tokens [--reps N]
+    python -m dwim_amd.kernel_workloads stream [--reps N]
 
 `attention`: first a device copy of 256 MiB (four times), the calibration
 of the FETCH_SIZE / WRITE_SIZE counters; then one-token GQA decode (24 query heads, 4 key/value heads of 256,
@@ -13,6 +14,13 @@ same over f16 caches.  Every call goes through the C ABI (dwim_attention).
 `tokens`: the 4-token Q4_K product (a speculative-decoding verify batch,
 k_planes then k_mv_stream<4>) on the 27B shape's 17408x5120 and 5120x17408
 matrices (synthetic weights), `reps` calls each, through dwim_matmul.
+
+`stream`: the HBM streaming floor the decode products are measured against.
+A read and nothing else (dwim_measure_stream, 16 bytes a lane, eight loads
+in flight a lane) over 8 distinct buffers of the 17408x5120 product's
+50,135,040 weight bytes in turn (400 MB, past the 256 MB Infinity Cache),
+launched back to back on the device's stream, `reps` rounds timed with
+events, at 256 to 2048 workgroups; prints the read rate.
 """
 from __future__ import annotations
 
@@ -63,12 +71,43 @@ def tokens(reps: int) -> None:
     dev.close()
 
 
+def stream(reps: int) -> None:
+    import ctypes
+
+    import torch
+
+    from . import lib
+    from .timing import Event
+    nbytes = 17408 * 5120 // 256 * 144
+    bufs = [torch.ones(nbytes // 4, device="cuda:0") for _ in range(8)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
+    torch.cuda.synchronize()
+    L = lib()
+    L.dwim_measure_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                      ctypes.c_uint]
+    dev = D.Hip(0)
+    st = dev.stream()
+    for blocks in (256, 512, 1024, 2048):
+        for i in range(16):
+            D._check(L.dwim_measure_stream(dev.h, bufs[i % 8].data_ptr(), nbytes, sink.data_ptr(), blocks))
+        dev.sync()
+        a, b = Event(), Event()
+        a.record(st)
+        for i in range(8 * reps):
+            D._check(L.dwim_measure_stream(dev.h, bufs[i % 8].data_ptr(), nbytes, sink.data_ptr(), blocks))
+        b.record(st)
+        us = a.elapsed_ms(b) * 1e3 / (8 * reps)
+        print(f"stream: {blocks} blocks, {nbytes} bytes a read in {us:.2f} us = {nbytes / us / 1e6:.2f} TB/s "
+              f"({nbytes / us / 1e6 / 8.0:.3f} of 8 TB/s)", flush=True)
+    dev.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=["attention", "tokens"])
+    ap.add_argument("workload", choices=["attention", "tokens", "stream"])
     ap.add_argument("--reps", type=int, default=20)
     a = ap.parse_args()
-    {"attention": attention, "tokens": tokens}[a.workload](a.reps)
+    {"attention": attention, "tokens": tokens, "stream": stream}[a.workload](a.reps)
 
 
 if __name__ == "__main__":
