@@ -154,6 +154,12 @@ int dwim_attention(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_c
 int dwim_attention_noalloc(dwim_dev *dev, dwim_buf *out, const dwim_buf *q, const dwim_cache *k_cache,
                            const dwim_cache *v_cache, size_t pos, size_t n_heads, size_t head_dim,
                            size_t n_kv_heads);
+/* No counterpart in the reference; measurement only: reads `bytes` (a
+ * multiple of 16) at p on the device's stream and nothing else, over `blocks`
+ * workgroups of 256 (16 bytes a lane, eight loads in flight a lane; `sink`, 4
+ * bytes of device memory, is written only if the folded words equal a fixed
+ * value).  The HBM streaming floor the decode products are read against. */
+int dwim_measure_stream(dwim_dev *dev, const void *p, size_t bytes, unsigned *sink, unsigned blocks);
 /* Device::silu_mul (gpu/mod.rs:351): gate = silu(gate) * up */
 int dwim_silu_mul(dwim_dev *dev, dwim_buf *gate, const dwim_buf *up);
 /* Device::sigmoid_mul (gpu/mod.rs:354): x *= sigmoid(gate) */
