@@ -75,6 +75,7 @@ SIGNATURES = {
     "dwim_rope": (_int, [_vp, _vp, _vp, _sz, _sz, _sz, _sz]),
     "dwim_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz]),
     "dwim_attention_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz]),
+    "dwim_measure_stream": (_int, [_vp, _vp, _sz, _vp, ctypes.c_uint]),
     "dwim_silu_mul": (_int, [_vp, _vp, _vp]),
     "dwim_sigmoid_mul": (_int, [_vp, _vp, _vp]),
     "dwim_conv": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

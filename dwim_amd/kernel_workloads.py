@@ -72,8 +72,6 @@ def tokens(reps: int) -> None:
 
 
 def stream(reps: int) -> None:
-    import ctypes
-
     import torch
 
     from . import lib
@@ -83,8 +81,6 @@ def stream(reps: int) -> None:
     sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
     torch.cuda.synchronize()
     L = lib()
-    L.dwim_measure_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
-                                      ctypes.c_uint]
     dev = D.Hip(0)
     st = dev.stream()
     for blocks in (256, 512, 1024, 2048):
