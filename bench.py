@@ -83,6 +83,34 @@ def kernel_roofline(dev, D, iters=200, copies=8):
             "bytes": algo}
 
 
+def stream_floor(dev, reps=50, copies=8, blocks=2048):
+    """The box's HBM streaming floor for the roofline kernel's bytes: a read of
+    the 17408x5120 product's 50,135,040 weight bytes and nothing else
+    (dwim_measure_stream), over `copies` distinct buffers in turn (past the
+    Infinity Cache), timed with HIP events on the device's stream; GB/s."""
+    import torch
+    from dwim_amd import lib
+    from dwim_amd.device import _check
+    from dwim_amd.timing import Event
+    nbytes = 17408 * 5120 // 256 * 144
+    bufs = [torch.ones(nbytes // 4, device="cuda:0") for _ in range(copies)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
+    torch.cuda.synchronize()
+    L, st = lib(), dev.stream()
+    for i in range(2 * copies):
+        _check(L.dwim_measure_stream(dev.h, bufs[i % copies].data_ptr(), nbytes, sink.data_ptr(), blocks))
+    dev.sync()
+    a, b = Event(), Event()
+    a.record(st)
+    for i in range(copies * reps):
+        _check(L.dwim_measure_stream(dev.h, bufs[i % copies].data_ptr(), nbytes, sink.data_ptr(), blocks))
+    b.record(st)
+    us = a.elapsed_ms(b) * 1e3 / (copies * reps)
+    del bufs
+    torch.cuda.empty_cache()
+    return nbytes / us / 1e3
+
+
 def copy_calibration(dev, mib=256, reps=8):
     """A plain device copy of known size (torch's copy kernel, `mib` MiB read
     and written per launch) for scaling the FETCH_SIZE / WRITE_SIZE counters
@@ -258,8 +286,10 @@ def main():
 
     dev = D.Hip(0)
     roof = kernel_roofline(dev, D)
+    floor_gbs = stream_floor(dev)
     if args.kernel_only:
-        print(json.dumps({"roofline_kernel": roof, "calibration": copy_calibration(dev)}), flush=True)
+        print(json.dumps({"roofline_kernel": roof, "stream_floor_gbs": floor_gbs, "calibration": copy_calibration(dev)}),
+              flush=True)
         return
 
     cfg = M.config_27b(drafter=False)
@@ -351,7 +381,9 @@ def main():
         "model_build_s": build_s,
         "roofline": {"bound": "hbm", "achieved": roof["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": roof["achieved"] / HBM_PEAK_GBS, "traffic": measured_traffic(), "kernel": roof["kernel"],
-                     "kernel_us": roof["us"], "algorithmic_bytes": roof["bytes"]},
+                     "kernel_us": roof["us"], "algorithmic_bytes": roof["bytes"],
+                     # the same bytes read and nothing else (dwim_measure_stream), measured in this run
+                     "stream_floor_gbs": floor_gbs, "frac_of_stream_floor": roof["achieved"] / floor_gbs},
     }
     model.close()
     if args.mtp:
