@@ -69,6 +69,34 @@ __global__ void k_split(const float *__restrict__ x, _Float16 *__restrict__ xh, 
     }
 }
 
+// k_split of silu(g)·u (gpu/cpu.rs:238-242, the SwiGLU's product computed
+// here instead of in the up product's epilogue), the same bits as k_split of
+// the product written out.
+__global__ void k_split_swiglu(const float *__restrict__ g, const float *__restrict__ u, _Float16 *__restrict__ xh,
+                               _Float16 *__restrict__ xl, _Float16 *__restrict__ xm, size_t n, size_t cols) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * (cols / 4)) return;
+    const float4 a = ((const float4 *)g)[i], b = ((const float4 *)u)[i];
+    const float4 v = make_float4(a.x * sigmoidf_(a.x) * b.x, a.y * sigmoidf_(a.y) * b.y, a.z * sigmoidf_(a.z) * b.z,
+                                 a.w * sigmoidf_(a.w) * b.w);
+    const _Float16 h0 = (_Float16)v.x, h1 = (_Float16)v.y, h2 = (_Float16)v.z, h3 = (_Float16)v.w;
+    const _Float16 l0 = (_Float16)(v.x - (float)h0), l1 = (_Float16)(v.y - (float)h1);
+    const _Float16 l2 = (_Float16)(v.z - (float)h2), l3 = (_Float16)(v.w - (float)h3);
+    auto pk = [](_Float16 p, _Float16 q) {
+        return (uint32_t)__builtin_bit_cast(uint16_t, p) | (uint32_t)__builtin_bit_cast(uint16_t, q) << 16;
+    };
+    ((uint2 *)xh)[i] = make_uint2(pk(h0, h1), pk(h2, h3));
+    ((uint2 *)xl)[i] = make_uint2(pk(l0, l1), pk(l2, l3));
+    const float sum = group_sum<8>((v.x + v.y) + (v.z + v.w));
+    if ((i & 7) == 0) {
+        const size_t sbi = i / 8, t = sbi / (cols / 32), sb = sbi % (cols / 32), bk = sb / 8, j = sb % 8;
+        _Float16 *m = xm + (t * (cols / 256) + bk) * 16;
+        const _Float16 sh = (_Float16)sum;
+        m[j] = sh;
+        m[8 + j] = (_Float16)(sum - (float)sh);
+    }
+}
+
 // what a product does with its result r and the output's old value o
 // (gpu/mod.rs:259 the add, gpu/cpu.rs:238-242 the SwiGLU's silu(gate)·up)
 DEV float gemm_out(int mode, float o, float r) {
@@ -84,6 +112,11 @@ struct GemmArgs {
     float *out;
     float *part_out;                // [parts][n][rows]
     int mode;                       // GemmMode
+    // jobs = 2: a second matrix of the same shape over the same activations
+    // (w2 into out2), its tiles after the first's in one launch
+    const uint8_t *w2;
+    float *out2;
+    unsigned jobs;
 };
 
 // the physical 16-byte chunk of logical chunk c (0..7) in LDS row r
@@ -128,9 +161,12 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // XCD-major numbering: workgroup bx runs on XCD bx % 8
     const unsigned per = a.grid / 8, lin = (blockIdx.x % 8) * per + blockIdx.x / 8;
-    const unsigned tiles = a.rtiles * a.ttiles;
-    if (lin >= tiles * a.parts) return;
-    const unsigned part = lin / tiles, tile = lin % tiles;
+    const unsigned tiles = a.rtiles * a.ttiles, jt = tiles * a.parts;
+    if (lin >= jt * a.jobs) return;
+    const unsigned job = lin / jt, lr = lin - job * jt;
+    const unsigned part = lr / tiles, tile = lr % tiles;
+    const uint8_t *const wmat = job ? a.w2 : a.w;
+    float *const omat = job ? a.out2 : a.out;
     const unsigned tt = tile / a.rtiles, rt = tile % a.rtiles;
     const unsigned row0 = rt * kRows, tok0 = tt * kToks;
     // this part's blocks [b0, b0 + nb) of the row's nbt
@@ -148,7 +184,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
         // sub-block sums: token bt, 16 bytes bq
         const int bt = lt >> 1, bq = lt & 1;
         const bool xlive = tok0 + bt < a.n;
-        const uint8_t *wsrc = a.w + ((size_t)(wlive ? wtile : 0) * nbt + b0) * q4kt::kUnit;
+        const uint8_t *wsrc = wmat + ((size_t)(wlive ? wtile : 0) * nbt + b0) * q4kt::kUnit;
         const gq qsrc = (gq)(wsrc + q4kt::qs_off(0, (row0 + ar) % 16));
         const gq hsrc = (gq)(wsrc + q4kt::meta_off((row0 + ar) % 16));
         const gq ms0 = (gq)(a.xm + ((size_t)(tok0 + (xlive ? bt : 0)) * nbt + b0) * 16 + 8 * bq);
@@ -430,7 +466,7 @@ __global__ void __launch_bounds__(kThreads) k_gemm_q4k(const GemmArgs a) {
     scale_rows(Dd + ((nb - 1) % 2) * kRows);  // out of the last block's unit
     // C tile (i, j): lane holds rows 32i + 8g + 4kh + e of token 32j + l % 32
     // (a part of a k-split product: its own slice of part_out, plainly)
-    float *const dst = a.parts > 1 ? a.part_out + (size_t)part * a.n * a.rows : a.out;
+    float *const dst = a.parts > 1 ? a.part_out + (size_t)part * a.n * a.rows : omat;
     const int mode = a.parts > 1 ? kGemmStore : a.mode;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
@@ -540,6 +576,7 @@ hipError_t gemm_run(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, i
         if (e != hipSuccess) return e;
         a.part_out = dev->gemm_parts;
     }
+    a.jobs = 1;
     a.grid = (a.rtiles * a.ttiles * a.parts + 7) / 8 * 8;
     a.xh = xh;
     a.xl = xl;
@@ -551,6 +588,62 @@ hipError_t gemm_run(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, i
     if (e != hipSuccess || a.parts == 1) return e;
     const size_t count = n * w->rows;
     k_gemm_reduce<<<(unsigned)((count + 255) / 256), 256, 0, dev->stream>>>(out, a.part_out, count, a.parts, mode);
+    return hipGetLastError();
+}
+
+// gate and up over the prepared split in one launch (their tiles make
+// whole rounds of workgroups together where each alone ends in a part-empty
+// one), plain results into g and u; then the split of silu(g)·u for the down
+// product.  Falls back to two launches when a k split would be needed.
+hipError_t gemm_run_swiglu_pair(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *g, float *u,
+                                size_t n) {
+    if (gate->fmt != DWIM_Q4_K || up->fmt != DWIM_Q4_K || gate->rows != up->rows || gate->cols != up->cols ||
+        gate->rows >= (1u << 30) || dev->split_n != n || dev->split_cols != gate->cols)
+        return hipErrorInvalidValue;
+    const unsigned rtiles = (unsigned)((gate->rows + kRows - 1) / kRows), ttiles = (unsigned)((n + kToks - 1) / kToks);
+    hipError_t e;
+    if (gemm_parts(rtiles * ttiles, (unsigned)(gate->cols / 256)) > 1) {
+        e = gemm_run(dev, gate, g, n, kGemmStore);
+        if (e == hipSuccess) e = gemm_run(dev, up, u, n, kGemmStore);
+        if (e != hipSuccess) return e;
+    } else {
+        static bool raised = false;
+        if (!raised) {
+            e = hipFuncSetAttribute((const void *)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
+            if (e != hipSuccess) return e;
+            raised = true;
+        }
+        _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * gate->cols, *xm = xl + n * gate->cols;
+        GemmArgs a{};
+        a.w = (const uint8_t *)gate->q;
+        a.w2 = (const uint8_t *)up->q;
+        a.rows = (unsigned)gate->rows;
+        a.cols = (unsigned)gate->cols;
+        a.n = (unsigned)n;
+        a.rtiles = rtiles;
+        a.ttiles = ttiles;
+        a.parts = 1;
+        a.jobs = 2;
+        a.grid = (2 * rtiles * ttiles + 7) / 8 * 8;
+        a.xh = xh;
+        a.xl = xl;
+        a.xm = xm;
+        a.out = g;
+        a.out2 = u;
+        a.mode = kGemmStore;
+        k_gemm_q4k<<<a.grid, kThreads, kLds, dev->stream>>>(a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    // the down product's split, of silu(g)·u
+    const size_t cols = gate->rows;
+    e = dev_grow(dev, &dev->split, &dev->split_cap, gemm_split_bytes(n, cols), 1);
+    if (e != hipSuccess) return e;
+    _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * cols, *xm = xl + n * cols;
+    const size_t subs = n * (cols / 32);
+    k_split_swiglu<<<(unsigned)((subs * 8 + 255) / 256), 256, 0, dev->stream>>>(g, u, xh, xl, xm, n, cols);
+    dev->split_n = n;
+    dev->split_cols = cols;
     return hipGetLastError();
 }
 

@@ -59,3 +59,17 @@ hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_
         return e;
     }
 }
+
+hipError_t launch_ffn_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, const dwim_weight *down,
+                          float *x, size_t n, const float *norm, float eps, float *g, float *u) {
+    if (n < kGemmTokens || gate->fmt != DWIM_Q4_K || down->fmt != DWIM_Q4_K || down->cols != gate->rows)
+        return hipErrorInvalidValue;
+    const size_t cols = gate->cols;
+    float *xn = dev_work(dev, n * cols);
+    if (!xn) return hipErrorOutOfMemory;
+    hipError_t e = launch_rmsnorm(dev->stream, xn, x, norm, n, cols, eps);
+    if (e == hipSuccess) e = gemm_prepare(dev, xn, n, cols);
+    if (e == hipSuccess) e = gemm_run_swiglu_pair(dev, gate, up, g, u, n);
+    if (e == hipSuccess) e = gemm_run(dev, down, x, n, kGemmAdd);
+    return e;
+}

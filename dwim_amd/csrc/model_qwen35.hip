@@ -563,6 +563,14 @@ struct dwim_model {
                 TRY(dwim_matmul_add(dev, x, l.out, z, xb));
             }
         }
+        if (fused && n >= 16 && l.down->fmt == DWIM_Q4_K) {
+            // gate and up in one launch, the SwiGLU in the down product's split
+            TRY(dwim_resize(dev, up, n * c.intermediate));
+            TRY(dwim_resize(dev, gate_ffn, n * c.intermediate));
+            DWIM_HIP(launch_ffn_q4k(dev, l.gate, l.up, l.down, x->data, n, l.mlp_norm->data, eps, gate_ffn->data,
+                                    up->data));
+            return 0;
+        }
         if (fused) {
             DWIM_HIP(launch_swiglu_q4k(dev, l.gate, l.up, up->data, x->data, n, l.mlp_norm->data, eps));
         } else {

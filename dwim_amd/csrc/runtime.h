@@ -315,5 +315,13 @@ hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, cons
 enum GemmMode { kGemmStore = 0, kGemmAdd = 1, kGemmSiluGate = 2 /* out = silu(out)·(w·x) */ };
 hipError_t gemm_prepare(dwim_dev *dev, const float *x, size_t n, size_t cols);
 hipError_t gemm_run(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, int mode);
+// gate and up over the prepared split in one launch, g and u written plain;
+// then the split of silu(g)·u prepared for the down product
+hipError_t gemm_run_swiglu_pair(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *g, float *u,
+                                size_t n);
+// the FFN of a batch (n >= 16 tokens, Q4_K): x += down · (silu(gate·xn) · (up·xn)),
+// xn = rmsnorm(x)·norm; g and u hold n·rows floats each
+hipError_t launch_ffn_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, const dwim_weight *down,
+                          float *x, size_t n, const float *norm, float eps, float *g, float *u);
 // the device's work scratch, grown to at least `floats`
 float *dev_work(dwim_dev *dev, size_t floats);
