@@ -221,11 +221,6 @@ int pick_lpr(size_t cpr) {
     return best;
 }
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
-
 template <int FMT>
 hipError_t launch_fmt(hipStream_t s, const Weights &w, const float *x, float *out, size_t n, int add) {
     int lpr = pick_lpr(Fmt<FMT>::chunks(w.cols));

@@ -436,279 +436,6 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
 // more, else 3 (more, lighter waves for the smaller matrices); a tile's waves
 // split over P workgroups only as far as keeps a workgroup to 8 waves per
 // matrix, since the meeting of the parts costs about a microsecond.
-// ---------------------------------------------------------------- tokens
-// Two to four tokens (a speculative-decoding verify batch) at once: the
-// weights are read once for all of them.  The MFMA layout is the one-token
-// kernel's, with the planes scaled per 32 activations (k_planes' pair
-// mode), so that the two MFMAs of a sub-block (m = 0, 1) sum in int32: per
-// token and half, one chain of two MFMAs, its result scaled by d·sc (decoded
-// once for every token) times the token's sub-block scale.  The lanes outside
-// B's nonzero blocks read a zero region at the same constant offsets.
-//
-// The planes of NT tokens take NT times the LDS, so a workgroup here is 16
-// waves that share them: T tiles times S ranges of blocks (times 2 for a
-// SwiGLU pair), the planes of the workgroup's S ranges (its part of the row)
-// staged once, by all 1024 lanes, before the barrier.  A wave takes up to
-// kTokK blocks of its tile and, as in the one-token kernel, issues every load
-// first: its share of the planes and statistics, then its weights.
-constexpr int kTokK = 5;  // blocks a wave (at most)
-constexpr int kTokWaves = 16;
-
-// Workgroup LDS, in 16-byte chunks (under 90 KB): planes [block][token][48] and statistics
-// [block][token][8] of up to kBlocks blocks, a trash area for the loads past
-// the part's blocks (every lane stores every load it made: a store under a
-// branch would let the compiler sink its load behind the weights), the zero
-// region and per wave the decoded scales ([sub-block][row] floats).
-template <int NT>
-struct TokLds {
-    static constexpr int kHdrChunks = 32;
-    // as many blocks as four plane loads a lane bring (more would cost
-    // registers the weights need: 1024 lanes have 128 each)
-    static constexpr int kBlocks = 4 * 64 * kTokWaves / (NT * 48) < 80 ? 4 * 64 * kTokWaves / (NT * 48) : 80;
-    static constexpr int kPlaneLoads = (kBlocks * NT * 48 + 64 * kTokWaves - 1) / (64 * kTokWaves);
-    static constexpr int kStatLoads = (kBlocks * NT * 8 + 64 * kTokWaves - 1) / (64 * kTokWaves);
-    static constexpr int kStat = kBlocks * NT * 48;
-    static constexpr int kTrash = kStat + kBlocks * NT * 8;
-    static constexpr int kZero = kTrash + 64;
-    static constexpr int kZeroChunks = kTokK * NT * 48;
-    static constexpr int kHdr = kZero + kZeroChunks;
-    static_assert(kZeroChunks <= 64 * kTokWaves, "the zero region is cleared by one store a lane");
-    static constexpr int kChunks = kHdr + kTokWaves * kHdrChunks;
-};
-
-struct TokArgs {
-    const uint8_t *w[kMaxJobs];
-    float *out[kMaxJobs];              // [NT][rows]
-    unsigned rows[kMaxJobs];
-    unsigned tiles[kMaxJobs];
-    unsigned first[kMaxJobs];          // first workgroup of each matrix; all ones past the last
-    unsigned tile0[kMaxJobs];
-    unsigned add_mask;
-    unsigned nb, S, T, P;
-    int swiglu;                        // waves T·S.. take W_1 of the same tiles
-    const int8_t *xq[kMaxTok];         // each token's planes [3][cols]
-    const float *xstat[kMaxTok];       // [cols/64][8]
-    float *partials;
-    unsigned *counters;
-};
-
-template <int NT>
-__global__ void __launch_bounds__(1024) k_mv_q4k_tokens(const TokArgs a) {
-    using L = TokLds<NT>;
-    constexpr int K = kTokK;
-    extern __shared__ uint4 lds_all[];
-    __shared__ float red[kTokWaves][NT][16];
-    const int lane = threadIdx.x & 63, wave_all = threadIdx.x >> 6, kq = lane >> 4, c = lane & 15;
-    const unsigned S = a.S, T = a.T, P = a.P, nb = a.nb, bx = blockIdx.x;
-    const unsigned f1 = a.first[1], f2 = a.first[2], f3 = a.first[3];
-    const int j = (int)(bx >= f1) + (int)(bx >= f2) + (int)(bx >= f3);
-    const unsigned wg = bx - (j == 0 ? 0u : j == 1 ? f1 : j == 2 ? f2 : f3);
-    const unsigned group = wg / P, part = wg - group * P;
-    const unsigned w = (unsigned)wave_all % S, tt = ((unsigned)wave_all / S) % T;
-    const int pairj = (unsigned)wave_all >= S * T;  // a SwiGLU workgroup's W_1 waves
-    const int jw = j + pairj;
-    const uint8_t *wbase = jw == 0 ? a.w[0] : jw == 1 ? a.w[1] : jw == 2 ? a.w[2] : a.w[3];
-    const unsigned ntiles = j == 0 ? a.tiles[0] : j == 1 ? a.tiles[1] : j == 2 ? a.tiles[2] : a.tiles[3];
-    const unsigned tile = group * T + tt;
-    const bool tile_ok = tile < ntiles;
-    const unsigned tile_c = tile_ok ? tile : ntiles - 1;
-    // this wave's blocks [b0, b1): range part·S + w of P·S; the part's [pb0, pb1)
-    const unsigned R = P * S, r = part * S + w;
-    const unsigned b0 = r * nb / R, b1 = (r + 1) * nb / R;
-    const unsigned pb0 = part * S * nb / R, pb1 = (part + 1) * S * nb / R;
-    const int nblk = (int)(b1 - b0);
-    const uint8_t *wt = wbase + ((size_t)tile_c * nb + b0) * q4kt::kUnit;
-    const unsigned cols = nb * 256;
-    const int8_t *xqs[NT];
-    const float *xss[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        xqs[t] = a.xq[t];
-        xss[t] = a.xstat[t];
-    }
-
-    // the part's planes and statistics, spread over the workgroup's lanes
-    const unsigned gl = threadIdx.x;
-    const unsigned nplane = (pb1 - pb0) * NT * 48, nstat = (pb1 - pb0) * NT * 8;
-    v4i xc[L::kPlaneLoads];
-#pragma unroll
-    for (int u = 0; u < L::kPlaneLoads; u++) {
-        const unsigned g = gl + 1024u * u;
-        const unsigned gg = g < nplane ? g : 0u;
-        const unsigned bt = gg / 48u, ch = gg % 48u;
-        const unsigned bl = bt / NT, t = bt % NT;
-        const int8_t *src = xqs[0];
-#pragma unroll
-        for (int q = 1; q < NT; q++) src = t == (unsigned)q ? xqs[q] : src;
-        xc[u] = *(const v4i *)(src + (ch / 16u) * cols + (pb0 + bl) * 256u + 16u * (ch % 16u));
-    }
-    v4f st[L::kStatLoads];
-#pragma unroll
-    for (int u = 0; u < L::kStatLoads; u++) {
-        const unsigned g = gl + 1024u * u;
-        const unsigned gg = g < nstat ? g : 0u;
-        const unsigned bt = gg / 8u, k = gg % 8u;
-        const unsigned bl = bt / NT, t = bt % NT;
-        const float *src = xss[0];
-#pragma unroll
-        for (int q = 1; q < NT; q++) src = t == (unsigned)q ? xss[q] : src;
-        st[u] = *(const v4f *)(src + ((pb0 + bl) * 8u + k) * 4u);
-    }
-    // the old outputs (x of x += W·in), loaded whatever adds says
-    const unsigned orows = j == 0 ? a.rows[0] : j == 1 ? a.rows[1] : j == 2 ? a.rows[2] : a.rows[3];
-    float *const obase = j == 0 ? a.out[0] : j == 1 ? a.out[1] : j == 2 ? a.out[2] : a.out[3];
-    const unsigned orow = tile_c * 16 + (unsigned)(lane & 15);
-    const unsigned orow_c = orow < orows ? orow : 0u;
-    const bool adds = (a.add_mask >> j) & 1u;
-    float old_out[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const float o = obase[(size_t)t * orows + orow_c];
-        old_out[t] = adds ? o : 0.0f;
-    }
-    uint4 wq[K][2];
-    uint32_t hw[K];
-#pragma unroll
-    for (int i = 0; i < K; i++) {
-        const unsigned off = (unsigned)(i < nblk ? i : 0) * (unsigned)q4kt::kUnit;
-        wq[i][0] = *(const uint4 *)(wt + off + q4kt::qs_off(kq, c));
-        wq[i][1] = *(const uint4 *)(wt + off + q4kt::qs_off(kq, c) + 16);
-        hw[i] = *(const uint32_t *)(wt + off + 4 * lane);
-    }
-    v4i *lv = (v4i *)lds_all;
-#pragma unroll
-    for (int u = 0; u < L::kPlaneLoads; u++) {
-        const unsigned g = gl + 1024u * u;
-        lv[g < nplane ? g : L::kTrash + (unsigned)lane] = xc[u];
-    }
-#pragma unroll
-    for (int u = 0; u < L::kStatLoads; u++) {
-        const unsigned g = gl + 1024u * u;
-        ((v4f *)lds_all)[g < nstat ? L::kStat + g : L::kTrash + (unsigned)lane] = st[u];
-    }
-    lv[threadIdx.x < (unsigned)L::kZeroChunks ? L::kZero + threadIdx.x : L::kTrash + (unsigned)lane] = v4i{0, 0, 0, 0};
-    __syncthreads();
-
-    // B: lane (k-group kq, column c) reads digit c % 3 of its block's
-    // sub-block 2kq + h when c / 3 == kq, else zeros
-    const bool active = c < 12 && c / 3 == kq;
-    const v4i *bbase = lv + (active ? (int)((b0 - pb0) * NT * 48) + 16 * (c % 3) + 4 * kq : L::kZero);
-    const int gp = c < 12 ? c / 3 : 0;
-    const int k4 = lane & 3, R4 = lane >> 2;
-    const float4 *stl = (const float4 *)(lds_all + L::kStat);
-    float *hdr = (float *)(lds_all + L::kHdr + wave_all * L::kHdrChunks);
-    float acc[NT][4], macc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        acc[t][0] = acc[t][1] = acc[t][2] = acc[t][3] = 0.0f;
-        macc[t] = 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < K; i++) {
-        if (i >= nblk) break;
-        const unsigned bl = b0 + (unsigned)i - pb0;
-        {
-            const uint32_t w0 = quad_bcast<0>(hw[i]), w1 = quad_bcast<1>(hw[i]), w2 = quad_bcast<2>(hw[i]),
-                           w3 = quad_bcast<3>(hw[i]);
-            const float d = f16_bits(w0 & 0xffffu), dmin = f16_bits(w0 >> 16);
-            float sc0, sc1, mn0, mn1;
-            scales_pair(w1, w2, w3, k4, sc0, sc1, mn0, mn1);
-            const float D0 = d * sc0, D1 = d * sc1;
-            const float mA = dmin * mn0, mB = dmin * mn1 - 8.0f * D1;
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const float4 xm = stl[(bl * NT + t) * 8 + 2 * k4 + 1];
-                macc[t] += mA * (xm.x + xm.y) + mB * (xm.z + xm.w);
-            }
-            hdr[(2 * k4) * 16 + R4] = D0;
-            hdr[(2 * k4 + 1) * 16 + R4] = D1 * 0.0625f;
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint32_t mask = h ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-            const float4 Dsb = *(const float4 *)&hdr[(2 * gp + h) * 16 + 4 * kq];
-            const uint4 q0 = wq[i][0], q1 = wq[i][1];
-            const v4i a0 = {(int)(q0.x & mask), (int)(q0.y & mask), (int)(q0.z & mask), (int)(q0.w & mask)};
-            const v4i a1 = {(int)(q1.x & mask), (int)(q1.y & mask), (int)(q1.z & mask), (int)(q1.w & mask)};
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const v4i *bp = bbase + (i * NT + t) * 48 + 2 * h;
-                v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
-                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bp[1], C, 0, 0, 0);
-                // token t's scale of sub-block 2gp + h (its groups 4gp + 2h, + 1)
-                const float sx = ((const float *)&stl[(bl * NT + t) * 8 + 2 * gp])[2 * h];
-                acc[t][0] += (Dsb.x * sx) * (float)C[0];
-                acc[t][1] += (Dsb.y * sx) * (float)C[1];
-                acc[t][2] += (Dsb.z * sx) * (float)C[2];
-                acc[t][3] += (Dsb.w * sx) * (float)C[3];
-                // a token at a time: scheduled freely, the MFMAs of a whole
-                // block hold their results at once and spill the weights
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-    }
-    const float f = c < 12 ? (c % 3 == 0 ? 1.0f : c % 3 == 1 ? 256.0f : 65536.0f) : 0.0f;
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc[t][e] = group_sum<16>(acc[t][e] * f);
-        const float mt = group_sum<4>(macc[t]);
-        const float mrow = __shfl(mt, 16 * kq + 4 * (c & 3), 64);
-        if (c < 4)
-            red[wave_all][t][4 * kq + c] =
-                (c == 0 ? acc[t][0] : c == 1 ? acc[t][1] : c == 2 ? acc[t][2] : acc[t][3]) - mrow;
-    }
-    __syncthreads();
-    // wave 0 of each tile's matrix-0 waves finishes the tile
-    if (w != 0 || pairj || !tile_ok) return;
-    const int rl = lane & 15;
-    float v[NT], uu[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        v[t] = 0.0f;
-        uu[t] = 0.0f;
-        for (unsigned q = 0; q < S; q++) v[t] += red[tt * S + q][t][rl];
-        if (a.swiglu)
-            for (unsigned q = 0; q < S; q++) uu[t] += red[(T + tt) * S + q][t][rl];
-    }
-    const unsigned gtile = (j == 0 ? a.tile0[0] : j == 1 ? a.tile0[1] : j == 2 ? a.tile0[2] : a.tile0[3]) + tile;
-    if (P > 1) {
-        // the parts meet as in the one-token kernel
-        float *pp = a.partials + ((size_t)gtile * kMaxParts + part) * NT * 32;
-        if (lane < 16)
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                __hip_atomic_store(pp + 32 * t + lane, v[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(pp + 32 * t + 16 + lane, uu[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);
-        unsigned old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(&a.counters[gtile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __shfl(old, 0, 64);
-        if (old != P - 1) return;
-        const float *tp = a.partials + (size_t)gtile * kMaxParts * NT * 32;
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            v[t] = 0.0f;
-            uu[t] = 0.0f;
-            for (unsigned q = 0; q < P; q++) {
-                v[t] += __hip_atomic_load(tp + (q * NT + t) * 32 + rl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                uu[t] += __hip_atomic_load(tp + (q * NT + t) * 32 + 16 + rl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        if (lane == 0) __hip_atomic_store(&a.counters[gtile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (lane >= 16 || orow >= orows) return;
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        if (a.swiglu) v[t] = v[t] * sigmoidf_(v[t]) * uu[t];  // silu(gate) · up (gpu/cpu.rs:238-242)
-        obase[(size_t)t * orows + orow] = v[t] + old_out[t];
-    }
-}
-
 struct Plan {
     int K;
     unsigned S, P;
@@ -774,50 +501,6 @@ hipError_t run(dwim_dev *dev, Args a, unsigned njobs, const size_t *rows) {
         case 5: return go<5>(dev, a, total, waves);
         default: return go<6>(dev, a, total, waves);
     }
-}
-
-// Several tokens: parts P (each at most TokLds::kBlocks blocks of the
-// row), ranges S a part (a power of two, each at most kTokK blocks) and
-// tiles T = 16 / (S · pair) a workgroup.
-template <int NT>
-hipError_t run_tokens(dwim_dev *dev, TokArgs a, unsigned njobs, const size_t *rows) {
-    using L = TokLds<NT>;
-    const unsigned J = a.swiglu ? 2 : 1, nb = a.nb;
-    unsigned P = (nb + L::kBlocks - 1) / L::kBlocks, S = 1;
-    for (;; P++) {
-        if (P > (unsigned)kMaxParts) return hipErrorInvalidValue;
-        const unsigned bp = (nb + P - 1) / P, need = (bp + kTokK - 1) / kTokK;
-        S = 1;
-        while (S < need) S *= 2;
-        if (S * J <= (unsigned)kTokWaves) break;
-    }
-    const unsigned T = kTokWaves / (S * J);
-    a.S = S, a.T = T, a.P = P;
-    unsigned tiles = 0, total = 0;
-    for (unsigned j = 0; j < kMaxJobs; j++) {
-        a.first[j] = j < njobs ? total : 0xffffffffu;
-        a.tile0[j] = tiles;
-        if (j < njobs) {
-            const unsigned t = (unsigned)q4kt::tiles(rows[j]);
-            a.tiles[j] = t;
-            total += (t + T - 1) / T * P;
-            tiles += t;
-        }
-    }
-    a.first[0] = 0;
-    if (P > 1 && tiles > dev->mv_tiles_cap) return hipErrorInvalidValue;
-    a.partials = dev->mv_partials;
-    a.counters = dev->mv_counters;
-    constexpr size_t lds = (size_t)L::kChunks * 16;
-    static bool raised = false;  // the attribute holds for the process
-    if (!raised) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_mv_q4k_tokens<NT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        raised = true;
-    }
-    k_mv_q4k_tokens<NT><<<total, kTokWaves * 64, lds, dev->stream>>>(a);
-    return hipGetLastError();
 }
 
 }  // namespace
@@ -902,16 +585,6 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
     return run(dev, a, swiglu ? 1 : (unsigned)count, rows);
 }
 
-// the stream-K kernel for 2..4 tokens unless DWIM_MV_STREAM=0 (the
-// tile-group kernel above, kept for comparison)
-static bool stream_tokens() {
-    static const bool on = [] {
-        const char *v = getenv("DWIM_MV_STREAM");
-        return !(v && v[0] == '0');
-    }();
-    return on;
-}
-
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                                      int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
                                      float *xn_out) {
@@ -950,7 +623,7 @@ hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws
             }
             a.swiglu = swiglu;
             e = run(dev, a, njobs, rows);
-        } else if (stream_tokens()) {
+        } else {
             const int8_t *xq[kMaxTok];
             const float *xs[kMaxTok];
             float *o[kMaxJobs];
@@ -961,24 +634,6 @@ hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws
             }
             for (int j = 0; j < count; j++) o[j] = outs[j] ? outs[j] + t0 * rows[j] : nullptr;
             e = run_mv_stream(dev, ws, o, adds, count, swiglu, nt, xq, xs);
-        } else {
-            TokArgs a{};
-            a.nb = (unsigned)(cols / 256);
-            for (int t = 0; t < kMaxTok; t++) {
-                const planes::View v = planes_area(dev, kBatchArea + t, cols);
-                a.xq[t] = v.q;
-                a.xstat[t] = v.stat;
-            }
-            for (int j = 0; j < count; j++) {
-                a.w[j] = (const uint8_t *)ws[j]->q;
-                a.out[j] = outs[j] ? outs[j] + t0 * rows[j] : nullptr;
-                a.rows[j] = (unsigned)rows[j];
-                if (adds && adds[j]) a.add_mask |= 1u << j;
-            }
-            a.swiglu = swiglu;
-            e = nt == 2 ? run_tokens<2>(dev, a, njobs, rows)
-                : nt == 3 ? run_tokens<3>(dev, a, njobs, rows)
-                          : run_tokens<4>(dev, a, njobs, rows);
         }
         if (e != hipSuccess) return e;
         t0 += nt;

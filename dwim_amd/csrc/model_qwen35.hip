@@ -269,70 +269,6 @@ struct dwim_model {
     // the next layer its input in area 0.  The RMS norms become scales the
     // consuming products apply to their results.
     bool handed = false;
-    // With chains (DWIM_CHAIN=1 in the environment), a layer's products run
-    // as chain launches (k_mv_chain.hip): its input products in one, and its
-    // mixer's output product, the SwiGLU pair, down and the next layer's input
-    // products in the next; `pending` holds the steps of a chain not launched
-    // yet.  By default every product is its own launch, which measures faster.
-    bool use_chain = false;
-    std::vector<ChainStep> pending;
-
-    int flush() {
-        if (pending.empty()) return 0;
-        DWIM_HIP(launch_mv_chain(dev, pending.data(), (int)pending.size()));
-        pending.clear();
-        return 0;
-    }
-    ChainStep step(const dwim_weight *w0, const dwim_weight *w1, float *out, int in_area, int dep) const {
-        ChainStep s;
-        s.w[0] = w0;
-        s.w[1] = w1;
-        s.out = out;
-        s.in_area = in_area;
-        s.dep = dep;
-        s.eps = c.eps;
-        return s;
-    }
-    // the layer's input products (area 0, RMS-scaled), after the steps pending
-    int chain_inputs(const Layer &l) {
-        const int dep = pending.empty() ? -1 : (int)pending.size() - 1;
-        const dwim_weight *ws[4] = {l.q, l.qgate, l.k, l.v};
-        dwim_buf *outs[4] = {q, gate, k, v};
-        const int count = l.attention ? 4 : 2;
-        if (!l.attention) {
-            ws[0] = l.qkv, ws[1] = l.z;
-            outs[0] = qkv, outs[1] = z;
-        }
-        for (int i = 0; i < count; i++) {
-            ChainStep s = step(ws[i], nullptr, outs[i]->data, 0, dep);
-            s.rms = 1;
-            pending.push_back(s);
-        }
-        return flush();
-    }
-    // the mixer's output product, the SwiGLU pair and down, left pending
-    void chain_tail(const Layer &l, const dwim_buf *next) {
-        ChainStep o = step(l.attention ? l.o : l.out, nullptr, x->data, 1, -1);
-        o.add = 1;
-        o.coherent_out = 1;
-        o.emit_area = 0;
-        o.emit_norm = l.mlp_norm->data;
-        pending.push_back(o);
-        ChainStep pr = step(l.gate, l.up, up->data, 0, 0);
-        pr.rms = 1;
-        pr.emit_area = 1;
-        pending.push_back(pr);
-        ChainStep d = step(l.down, nullptr, x->data, 1, 1);
-        d.add = 1;
-        d.coherent_out = 1;
-        if (next) {
-            d.emit_area = 0;
-            d.emit_norm = next->data;
-            d.emit_xw = xh->data;
-        }
-        pending.push_back(d);
-    }
-
     Rms rms0() const {
         const planes::View in = planes_area(dev, 0, c.hidden);
         return Rms{in.ss, (unsigned)(c.hidden / planes::kGroup), (float)c.hidden, c.eps};
@@ -384,11 +320,9 @@ struct dwim_model {
         TRY(dwim_resize(dev, xh, c.hidden));
         // the DeltaNet gate projection takes x·attn_norm in f32 (xh)
         if (!handed) {
-            TRY(flush());
             DWIM_HIP(launch_planes(dev, x->data, c.hidden, l.attn_norm->data, eps, l.attention ? nullptr : xh->data, 0, 1));
         }
         handed = false;
-        if (use_chain) return layer_one_chained(l, pos, next);
         if (l.attention) {
             TRY(dwim_resize(dev, q, q_dim()));
             TRY(dwim_resize(dev, gate, q_dim()));
@@ -438,50 +372,12 @@ struct dwim_model {
         return 0;
     }
 
-    // layer_one with the products in chain launches: the same launches of
-    // the mixer between them, the same arithmetic per product.
-    int layer_one_chained(const Layer &l, size_t pos, const dwim_buf *next) {
-        const float eps = c.eps;
-        if (l.attention) {
-            TRY(dwim_resize(dev, q, q_dim()));
-            TRY(dwim_resize(dev, gate, q_dim()));
-            TRY(dwim_resize(dev, k, kv_dim()));
-            TRY(dwim_resize(dev, v, kv_dim()));
-            TRY(dwim_resize(dev, att, q_dim()));
-        } else {
-            TRY(dwim_resize(dev, q, k_dim()));
-            TRY(dwim_resize(dev, k, k_dim()));
-            TRY(dwim_resize(dev, v, v_dim()));
-            TRY(dwim_resize(dev, att, v_dim()));
-        }
-        TRY(chain_inputs(l));
-        if (l.attention) {
-            dwim_cache *kc = seq.k_cache[l.cache], *vc = seq.v_cache[l.cache];
-            DWIM_HIP(launch_qk_prep(dev->stream, q->data, k->data, v->data, l.q_norm->data, l.k_norm->data,
-                                    rope->data, 1, pos, c.heads, c.kv_heads, c.head_dim, c.rot_dim, eps, kc, vc));
-            DWIM_HIP(launch_attention_gated(dev, att->data, q->data, kc, vc, 1, pos, c.heads, c.head_dim, c.kv_heads,
-                                            gate->data, 1));
-        } else {
-            auto &pair = seq.conv_state[l.slot];
-            dwim_buf *state = seq.parity ? pair[0] : pair[1];
-            dwim_buf *state_out = seq.parity ? pair[1] : pair[0];
-            DWIM_HIP(launch_gdn(dev, qkv->data, state->data, state_out->data, l.conv->data, l.ab, xh->data, rms0(),
-                                l.decay->data, seq.ssm_state[l.slot]->data, z->data, l.norm->data, eps, c.k_heads,
-                                c.v_heads, c.state_dim, 1));
-        }
-        chain_tail(l, next);
-        handed = next != nullptr;
-        if (!next) TRY(flush());
-        return 0;
-    }
-
     // Pass::layer (qwen35/mod.rs:541-655).  Verifying, the linear layers
     // save their inputs and run a copy of their recurrent state (:606-632).
     int layer(const Layer &l, size_t n, size_t pos, bool verify = false, const dwim_buf *next = nullptr) {
         const float eps = c.eps;
         const bool fused = fusable(l), one = fused && n == 1;
         if (one && !verify) return layer_one(l, pos, next);
-        TRY(flush());
         handed = false;
         TRY(dwim_resize(dev, xh, n * c.hidden));
         if (!fused) TRY(normalize(xh, x, l.attn_norm, n));
@@ -705,7 +601,7 @@ struct dwim_model {
             TRY(forward_batch(tokens + i * most, m, pos + i * most, false, last, last ? logits_out : nullptr,
                               last ? greedy : nullptr));
         }
-        return check_chains();
+        return 0;
     }
 
     // Greedy decoding of `steps` tokens from `token` at `pos`, as the reply
@@ -746,12 +642,6 @@ struct dwim_model {
         TRY(err);
         DWIM_HIP(hipMemcpyAsync(out, picks + 1, steps * 4, hipMemcpyDeviceToHost, dev->stream));
         DWIM_HIP(hipStreamSynchronize(dev->stream));
-        return check_chains();
-    }
-
-    // a chain launch that gave up waiting leaves its error word set
-    int check_chains() {
-        if (use_chain && chain_error(dev)) return dwim_fail("a chain launch timed out waiting for a product");
         return 0;
     }
 
@@ -1087,8 +977,6 @@ extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg
     m->c = c;
     m->seed = seed;
     m->most = dwim_batch(dev);
-    const char *chain = getenv("DWIM_CHAIN");
-    m->use_chain = chain && chain[0] == '1';
     for (size_t i = 0; i < c.layers; i++) {
         m->layers.emplace_back();
         if (m->load_layer(i, m->is_attention(i), body_format, m->layers.back())) return 1;

@@ -1,5 +1,5 @@
 // Helpers shared by the one-token Q4_K kernels on the int8 matrix cores
-// (k_mv_q4k_mfma.hip, k_mv_chain.hip): the block header decode and lane
+// (k_mv_q4k_mfma.hip): the block header decode and lane
 // broadcasts.
 #pragma once
 #include <hip/hip_runtime.h>

@@ -43,14 +43,6 @@ struct dwim_dev {
     // Split one-token Q4_K products (k_mv_q4k_mfma.hip): the partial sums of
     // up to mv_tiles_cap 16-row tiles (4 parts × 32 floats each) and a counter
     // per tile, zero between launches.
-    // The chain launches (k_mv_chain.hip): the error word, each workgroup's
-    // progress word, the parts' partial sums and a counter per split tile.
-    unsigned *chain_ctl = nullptr;                  // the error word
-    unsigned long long *chain_progress = nullptr;   // [kChainMaxGroups] progress words, zeroed once
-    unsigned long long chain_seq = 0;               // the last chain launch's sequence number
-    float *chain_partials = nullptr;
-    unsigned *chain_counters = nullptr;
-    unsigned chain_tiles_cap = 0;
     float *mv_partials = nullptr;
     unsigned *mv_counters = nullptr;
     unsigned mv_tiles_cap = 0;
@@ -256,28 +248,6 @@ size_t gemm_split_bytes(size_t n, size_t cols);
 size_t argmax_scratch_words(size_t rows);
 size_t gemm_parts_floats(size_t n, size_t rows, size_t cols);
 hipError_t gemm_reserve(dwim_dev *dev, size_t split_bytes, size_t parts_floats);
-// ---- a chain of one-token Q4_K products in one persistent launch (k_mv_chain.hip)
-constexpr int kMaxChain = 8;       // products a chain
-constexpr int kMaxChainParts = 4;  // parts a tile
-constexpr int kChainCtlWords = 4;
-constexpr size_t kChainMaxGroups = 1024;  // workgroups (CUs) a chain launch may have
-struct ChainStep {
-    const dwim_weight *w[2] = {nullptr, nullptr};  // w[1]: up of a SwiGLU pair (out = silu(w0·x)·(w1·x))
-    float *out = nullptr;
-    int in_area = 0;        // the planes area of the input
-    int dep = -1;           // the earlier step whose output the input is (-1: an earlier launch's)
-    int add = 0;            // out += W·in
-    int rms = 0;            // the input is x·w with per-group Σx²: results scale by 1/sqrt(Σ/cols + eps)
-    int coherent_out = 0;   // out is read by a later step of the chain
-    int emit_area = -1;     // the planes of out (of out·emit_norm with Σout², and that in f32 to emit_xw)
-    const float *emit_norm = nullptr;
-    float *emit_xw = nullptr;
-    float eps = 0.0f;
-};
-size_t chain_lds_bytes();
-hipError_t launch_mv_chain(dwim_dev *dev, const ChainStep *steps, int n);
-// nonzero when a chain launch gave up waiting (its results are then wrong)
-int chain_error(dwim_dev *dev);
 size_t attention_partials_floats(size_t n, size_t pos, size_t n_heads, size_t head_dim);
 hipError_t attention_reserve(dwim_dev *dev, size_t floats);
 size_t attention_kvx_bytes(size_t len, size_t n_kv_heads);
@@ -287,15 +257,9 @@ hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, con
                                   const dwim_cache *v, size_t n, size_t pos, size_t n_heads, size_t head_dim,
                                   size_t n_kv_heads, const float *gate, int area);
 
-// One token through a gated-DeltaNet mixer (k_gdn.hip): the gate logits
-// W_ab·xw (xw = x·attn_norm unscaled, scaled by rms), conv + SiLU of qkv with
-// its state carried to conv_state_out, l2 norms, the delta rule on `state`,
-// and z ← silu(z)·rmsnorm(o, norm_w) with its planes into `area` (>= 0).
-hipError_t launch_gdn(dwim_dev *dev, const float *qkv, const float *conv_state, float *conv_state_out,
-                      const float *conv_w, const dwim_weight *w_ab, const float *xw, const Rms &rms,
-                      const float *decay, float *state, float *z, const float *norm_w, float eps, size_t nk,
-                      size_t nv, size_t head_dim, int area);
-// The same step over 4 workgroups a head, from gate logits ab = W_ab ·
+// One token through a gated-DeltaNet mixer (k_gdn.hip): conv + SiLU of qkv
+// with its state carried to conv_state_out, l2 norms and the delta rule on
+// `state`, over 4 workgroups a head, from gate logits ab = W_ab ·
 // x·attn_norm computed beforehand (not yet RMS-scaled), the RMS norm of o
 // left to the product that reads the planes (area): each quarter's Σo² to
 // head_ss ([nv][4] floats), its columns' silu(z)·o·norm_w unnormalized as

@@ -66,20 +66,6 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
         dwim_dev_release_resources(dev);
         return dwim_fail("allocating the split-product scratch failed");
     }
-    // the chain launches' control words, partial sums and tile counters
-    dev->chain_tiles_cap = 4096;
-    if (hipMalloc(&dev->chain_ctl, kChainCtlWords * sizeof(unsigned)) != hipSuccess ||
-        hipMemset(dev->chain_ctl, 0, kChainCtlWords * sizeof(unsigned)) != hipSuccess ||
-        hipMalloc(&dev->chain_progress, kChainMaxGroups * sizeof(unsigned long long)) != hipSuccess ||
-        hipMemset(dev->chain_progress, 0, kChainMaxGroups * sizeof(unsigned long long)) != hipSuccess ||
-        hipMalloc(&dev->chain_partials, (size_t)dev->chain_tiles_cap * kMaxChainParts * 32 * sizeof(float)) !=
-            hipSuccess ||
-        hipMalloc(&dev->chain_counters, (size_t)dev->chain_tiles_cap * sizeof(unsigned)) != hipSuccess ||
-        hipMemset(dev->chain_counters, 0, (size_t)dev->chain_tiles_cap * sizeof(unsigned)) != hipSuccess) {
-        dev->refs = 0;
-        dwim_dev_release_resources(dev);
-        return dwim_fail("allocating the chain launches' control words failed");
-    }
     // the address of the scratch array dwim_attention_noalloc uses, on this device
     if (attention_scratch_init(dev) != hipSuccess) {
         dev->refs = 0;
@@ -120,10 +106,6 @@ void dwim_dev_release_resources(dwim_dev *dev) {
     if (dev->mv_partials) hipFree(dev->mv_partials);
     if (dev->mv_counters) hipFree(dev->mv_counters);
     if (dev->mv_stream) hipFree(dev->mv_stream);
-    if (dev->chain_ctl) hipFree(dev->chain_ctl);
-    if (dev->chain_progress) hipFree(dev->chain_progress);
-    if (dev->chain_partials) hipFree(dev->chain_partials);
-    if (dev->chain_counters) hipFree(dev->chain_counters);
     if (dev->partials) hipFree(dev->partials);
     if (dev->argmax_buf) hipFree(dev->argmax_buf);
     if (dev->tokens) hipFree(dev->tokens);

@@ -14,7 +14,7 @@ token wherever the gap exceeds the tolerance, and the logits it stores within
 The oracle (oracle/, the C restatement of dwim gpu/cpu.rs and
 inference/qwen35/mod.rs) runs on this container's CPUs: about 45 minutes for
 the prefill and 3 s a decode token on 8 cores.  Usage:
-    python tests/golden/make_qwen35_27b_tokens.py [decode_tokens]
+    python tests/golden/make_qwen35_27b_tokens.py [decode_tokens [output.npz]]
 """
 import os
 import sys
@@ -36,7 +36,8 @@ CFG = dict(hidden=5120, intermediate=17408, layers=64, heads=24, kv_heads=4, hea
 
 
 def main():
-    steps = int(sys.argv[1]) if len(sys.argv) > 1 else 128
+    steps = int(sys.argv[1]) if len(sys.argv) > 1 else 256
+    out = sys.argv[2] if len(sys.argv) > 2 else OUT
     V = CFG["vocab"]
     prompt = np.random.default_rng(PROMPT_SEED).integers(0, V, PROMPT).astype(np.uint32)
     sample = np.sort(np.random.default_rng(77).choice(V, 512, replace=False)).astype(np.uint32)
@@ -54,7 +55,7 @@ def main():
         top_ids.append(order.astype(np.uint32))
         top_vals.append(logits[order].astype(np.float32))
         sampled.append(logits[sample].astype(np.float32))
-        np.savez_compressed(OUT, model_seed=MODEL_SEED, prompt_seed=PROMPT_SEED, prompt=prompt, sample_ids=sample,
+        np.savez_compressed(out, model_seed=MODEL_SEED, prompt_seed=PROMPT_SEED, prompt=prompt, sample_ids=sample,
                             tokens=np.array(tokens, np.uint32), gaps=np.array(gaps, np.float32),
                             top_ids=np.array(top_ids), top_vals=np.array(top_vals), sampled=np.array(sampled))
 

@@ -363,33 +363,6 @@ def test_speculative_decode_is_greedy_decode():
 
 
 @pytest.mark.gpu
-def test_chained_one_token_path_agrees_with_cpu(monkeypatch):
-    """The one-token path with its products in persistent chain launches
-    (k_mv_chain.hip, DWIM_CHAIN=1: a layer's output product, SwiGLU pair and
-    down with the next layer's input products in one launch, weights copied
-    into LDS ahead of the arithmetic, parts of a tile merged in the last):
-    the 27B widths over four layers, and the tiny model with its drafter."""
-    monkeypatch.setenv("DWIM_CHAIN", "1")
-    cfg = M.config_27b(False)
-    cfg.layers, cfg.vocab = 4, 512
-    gpu = D.Hip(0)
-    g = M.Model(gpu, cfg, SEED + 2, max_len=32)
-    o = O.Model(cfg.as_dict(), SEED + 2)
-    _close(g.forward([3, 17, 42, 7, 9], 0), o.forward([3, 17, 42, 7, 9], 0), 2e-3, "5 tokens")
-    for i, t in enumerate([11, 400, 2, 77, 301, 5]):
-        _close(g.forward([t], 5 + i), o.forward([t], 5 + i), 2e-3, f"token {i}")
-    g.close()
-    cfg = _tiny(True)
-    g = M.Model(gpu, cfg, SEED, max_len=64)
-    o = O.Model(cfg.as_dict(), SEED)
-    _close(g.forward([3, 17, 42, 7, 9], 0), o.forward([3, 17, 42, 7, 9], 0), 2e-3, "tiny, 5 tokens")
-    for i, t in enumerate([11, 40, 2]):
-        _close(g.forward([t], 5 + i), o.forward([t], 5 + i), 2e-3, f"tiny, token {i}")
-    assert g.draft(8, 8, 3) == [int(t) for t in o.draft(8, 8, 3)]
-    g.close()
-
-
-@pytest.mark.gpu
 @pytest.mark.parametrize("shape", ["tiny", "tiny+drafter", "27b-widths"])
 def test_device_fed_decode_is_greedy_decode(shape):
     """dwim_model_decode_greedy (each step's pick handed to the next step's
