@@ -504,6 +504,8 @@ def _declare_model(L):
     L.or_model_restore.restype = ctypes.c_int
     L.or_model_restore.argtypes = [vp, ctypes.c_char_p, _sz, ctypes.POINTER(_sz)]
     L.or_model_zero_residual_writes.argtypes = [vp]
+    L.or_model_last_logits.restype = None
+    L.or_model_last_logits.argtypes = [vp, _f32p]
     L.or_model_verify.restype = None
     L.or_model_verify.argtypes = [vp, u32p, _sz, _sz, _f32p]
     L.or_model_rewind.restype = None
@@ -547,6 +549,13 @@ class Model:
         out = np.zeros(max(k, 1), np.uint32)
         n = self.L.or_model_draft(self.h, token, pos, k, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
         return list(out[:n])
+
+    def last_logits(self):
+        """The logits of the last single-token head product: after draft(),
+        those its last draft was picked from."""
+        out = np.empty(self.vocab, np.float32)
+        self.L.or_model_last_logits(self.h, _p(out, _f32p))
+        return out
 
     def verify(self, tokens, pos):
         t = np.ascontiguousarray(tokens, np.uint32)

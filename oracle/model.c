@@ -501,6 +501,10 @@ size_t or_model_draft(or_model *m, uint32_t token, size_t pos, size_t k, uint32_
     return k;
 }
 
+/* Test hook: the logits of the last single-token head product (after a
+ * draft, those of its last draft: qwen35/mod.rs:1064-1066). */
+void or_model_last_logits(const or_model *m, float *out) { memcpy(out, m->logits, m->c.vocab * 4); }
+
 /* LanguageModel::verify (qwen35/mod.rs:1073-1091): logits [n][vocab] */
 void or_model_verify(or_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits) {
     forward_batch(m, tokens, n, pos, 1, 1);

@@ -122,6 +122,7 @@ or_model *or_model_synthetic(const or_qwen35_config *cfg, uint64_t seed, int bod
 void or_model_free(or_model *m);
 void or_model_forward(or_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits);
 size_t or_model_draft(or_model *m, uint32_t token, size_t pos, size_t k, uint32_t *drafts);
+void or_model_last_logits(const or_model *m, float *out);
 void or_model_verify(or_model *m, const uint32_t *tokens, size_t n, size_t pos, float *logits);
 void or_model_rewind(or_model *m, size_t keep);
 void or_model_mark(or_model *m);
