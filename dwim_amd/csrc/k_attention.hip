@@ -632,12 +632,11 @@ hipError_t attention_run(dwim_dev *dev, float *partials, float *out, const float
                                                                 (unsigned)steps, (unsigned)n_kv_heads);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        static bool raised = false;
-        if (!raised) {
-            e = hipFuncSetAttribute((const void *)k_attn_flash, hipFuncAttributeMaxDynamicSharedMemorySize, kFlashLds);
-            if (e != hipSuccess) return e;
-            raised = true;
-        }
+        // once a process; a function-local static is initialized once even
+        // when host threads reach it together
+        static const hipError_t raised =
+            hipFuncSetAttribute((const void *)k_attn_flash, hipFuncAttributeMaxDynamicSharedMemorySize, kFlashLds);
+        if (raised != hipSuccess) return raised;
         const unsigned tiles = (unsigned)((n + kFQ - 1) / kFQ);
         FlashArgs fa{out, q, gate, kvx, (unsigned)n, (unsigned)pos, (unsigned)n_heads, (unsigned)n_kv_heads,
                      (unsigned)steps, tiles};

@@ -521,6 +521,14 @@ unsigned gemm_parts(unsigned tiles, unsigned nb) {
 
 constexpr size_t kLds = (size_t)16 * (2 * kRows * 8 + 4 * kToks * 8 + 2 * kRows * 2 + 2 * kToks * 2) + 2 * 4 * 2 * kRows;
 
+// The kernel's dynamic-LDS limit, raised once a process (a function-local
+// static is initialized once even when host threads reach it together).
+hipError_t raise_lds_limit() {
+    static const hipError_t raised =
+        hipFuncSetAttribute((const void *)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
+    return raised;
+}
+
 }  // namespace
 
 size_t gemm_split_bytes(size_t n, size_t cols) { return 2 * n * cols * sizeof(_Float16) + n * (cols / 256) * 32; }
@@ -555,12 +563,7 @@ hipError_t gemm_run(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, i
     if (w->fmt != DWIM_Q4_K || w->rows >= (1u << 31) || dev->split_n != n || dev->split_cols != w->cols)
         return hipErrorInvalidValue;
     hipError_t e;
-    static bool raised = false;
-    if (!raised) {
-        e = hipFuncSetAttribute((const void *)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
-        if (e != hipSuccess) return e;
-        raised = true;
-    }
+    if ((e = raise_lds_limit()) != hipSuccess) return e;
     _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * w->cols, *xm = xl + n * w->cols;
     GemmArgs a{};
     a.w = (const uint8_t *)w->q;
@@ -607,12 +610,7 @@ hipError_t gemm_run_swiglu_pair(dwim_dev *dev, const dwim_weight *gate, const dw
         if (e == hipSuccess) e = gemm_run(dev, up, u, n, kGemmStore);
         if (e != hipSuccess) return e;
     } else {
-        static bool raised = false;
-        if (!raised) {
-            e = hipFuncSetAttribute((const void *)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
-            if (e != hipSuccess) return e;
-            raised = true;
-        }
+        if ((e = raise_lds_limit()) != hipSuccess) return e;
         _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * gate->cols, *xm = xl + n * gate->cols;
         GemmArgs a{};
         a.w = (const uint8_t *)gate->q;

@@ -372,22 +372,43 @@ __global__ void __launch_bounds__(1024) k_mv_q4k_mfma(const Args a) {
     if (P > 1) {
         // the parts of a tile meet in the last workgroup to finish, which sums
         // them in part order (the same bits whichever finishes last) and
-        // clears the tile's counter for the next launch.  The partial sums go
-        // out as device-coherent stores (written through to the point where
-        // every XCD sees them) and are complete before the counter moves; the
-        // last workgroup reads them device-coherently.  No cache maintenance:
-        // a device-scope fence would write back and invalidate the whole L2
-        // of every workgroup's XCD.
+        // clears the tile's counter for the next launch.  The ordering is the
+        // one a release/acquire pair at agent scope would give, without its
+        // cache maintenance, which only non-atomic data needs:
+        //  * the partial sums are agent-scope atomic stores, which gfx950
+        //    issues with sc1 set: written through every XCD's L2 to the point
+        //    of device coherence;
+        //  * s_waitcnt vmcnt(0) waits until those stores are acknowledged
+        //    there (stores count in vmcnt on gfx9) before the counter's atomic
+        //    add issues; the compiler fences on both sides keep the compiler
+        //    from moving a store or the add across the wait;
+        //  * the partial loads issue only once the add has returned: they are
+        //    under a branch on its result (waited for with vmcnt(0) and read
+        //    with v_readfirstlane/readlane), the compiler does not speculate
+        //    atomic loads above a branch, and the GPU does not speculate;
+        //  * they are agent-scope atomic loads (sc1), which read the point of
+        //    coherence, not a stale L1 or L2 line, so no cache invalidate is
+        //    needed before them.
+        // A release fence would add buffer_wbl2 (write back the XCD's whole
+        // L2) and an acquire fence buffer_inv sc1 (drop the planes every
+        // workgroup of the XCD reads from it): measured at 87 against 14.6 µs
+        // a launch.  The emitted order (global_store ... sc1, s_waitcnt
+        // vmcnt(0), global_atomic_add ... sc0, s_waitcnt vmcnt(0), the branch,
+        // global_load ... sc1) is checked in this file's gfx950 assembly by
+        // tests/test_merge_order.py.
         float *pp = a.partials + ((size_t)gtile * kMaxParts + part) * 32;
         if (mine) {
             __hip_atomic_store(pp + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(pp + 16 + lane, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         unsigned old = 0;
         if (lane == 0) old = __hip_atomic_fetch_add(&a.counters[gtile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = __shfl(old, 0, 64);
         if (old != P - 1) return;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         v = 0.0f;
         u = 0.0f;
         const float *tp = a.partials + (size_t)gtile * kMaxParts * 32;
@@ -458,13 +479,12 @@ Plan plan(unsigned nb, unsigned tiles, bool swiglu) {
 template <int K>
 hipError_t go(dwim_dev *dev, const Args &a, unsigned grid, unsigned waves) {
     const size_t lds = (size_t)waves * Lds<K>::kChunks * 16;
-    static bool raised = false;  // past 64 KB (up to 16 waves) the launch needs the attribute
-    if (!raised) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_mv_q4k_mfma<K>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)(16 * Lds<K>::kChunks * 16));
-        if (e != hipSuccess) return e;
-        raised = true;
-    }
+    // past 64 KB (up to 16 waves) the launch needs the attribute, raised once
+    // a process (a function-local static is initialized once even when host
+    // threads reach it together)
+    static const hipError_t raised = hipFuncSetAttribute(
+        (const void *)k_mv_q4k_mfma<K>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(16 * Lds<K>::kChunks * 16));
+    if (raised != hipSuccess) return raised;
     k_mv_q4k_mfma<K><<<grid, waves * 64, lds, dev->stream>>>(a);
     return hipGetLastError();
 }

@@ -457,7 +457,12 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
             __hip_atomic_store(pp + ts * 32 + hf * 16 + row, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (ts + 2 < NT)
                 __hip_atomic_store(pp + (ts + 2) * 32 + hf * 16 + row, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // the same ordering as the one-token kernel's meeting
+            // (k_mv_q4k_mfma.hip): sc1 stores acknowledged before the
+            // counter's add, sc1 loads only under a branch on its result
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(kWaitVm0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
             unsigned n_c = 0;
             for (unsigned q = 0; q < P; q++) {
                 const unsigned ihq = sel(q, ih0, ih1, ih2, ih3), ipq = J * ihq;
@@ -469,6 +474,7 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
             if (lane == 0) old = __hip_atomic_fetch_add(&a.counters[T], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             old = __shfl(old, 0, 64);
             if (old != n_c - 1) continue;
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
             v0 = v1 = 0.0f;
             for (unsigned q = 0; q < P; q++) {
                 const unsigned ihq = sel(q, ih0, ih1, ih2, ih3), ipq = J * ihq;
@@ -593,14 +599,13 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
     const size_t lds = ((size_t)plane_cap * NT * (kBT + 8) + (size_t)K * NT * kBT + (size_t)kW * kHdrChunks) * 16 +
                        (size_t)items_cap * NT * 16 * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    static bool raised[kTok + 1] = {};
-    const void *fn = NT == 2 ? (const void *)k_mv_stream<2> : NT == 3 ? (const void *)k_mv_stream<3>
-                                                                       : (const void *)k_mv_stream<4>;
-    if (!raised[NT]) {
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
-        raised[NT] = true;
-    }
+    // raised once a process for each kernel (a function-local static is
+    // initialized once even when host threads reach it together)
+    static const hipError_t raised[3] = {
+        hipFuncSetAttribute((const void *)k_mv_stream<2>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
+        hipFuncSetAttribute((const void *)k_mv_stream<3>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
+        hipFuncSetAttribute((const void *)k_mv_stream<4>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)};
+    if (raised[NT - 2] != hipSuccess) return raised[NT - 2];
     if (NT == 2) k_mv_stream<2><<<G, kW * 64, lds, dev->stream>>>(a);
     else if (NT == 3) k_mv_stream<3><<<G, kW * 64, lds, dev->stream>>>(a);
     else k_mv_stream<4><<<G, kW * 64, lds, dev->stream>>>(a);

@@ -373,13 +373,11 @@ __global__ void __launch_bounds__(512) k_mv_q6k_tokens(const Q6TArgs a) {
 template <int NT>
 hipError_t go_tokens(dwim_dev *dev, const Q6TArgs &a, unsigned tiles) {
     const size_t lds = (size_t)a.S * Lds6T<NT>::kChunks * 16;
-    static bool raised = false;  // the attribute holds for the process
-    if (!raised) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_mv_q6k_tokens<NT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)(8 * Lds6T<NT>::kChunks * 16));
-        if (e != hipSuccess) return e;
-        raised = true;
-    }
+    // the attribute holds for the process, raised once (a function-local
+    // static is initialized once even when host threads reach it together)
+    static const hipError_t raised = hipFuncSetAttribute(
+        (const void *)k_mv_q6k_tokens<NT>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(8 * Lds6T<NT>::kChunks * 16));
+    if (raised != hipSuccess) return raised;
     k_mv_q6k_tokens<NT><<<tiles, a.S * 64, lds, dev->stream>>>(a);
     return hipGetLastError();
 }

@@ -821,7 +821,7 @@ struct dwim_model {
         const size_t cache_len = len * kv_dim(), cache_bytes = cache_len + cache_len / 32 * 2;
         for (int kv = 0; kv < 2; kv++)
             for (size_t i = 0; i < caches; i++) {
-                TRY(dwim_read_cache(dev, kv ? seq.v_cache[i] : seq.k_cache[i], cache_len, p));
+                TRY(dwim_read_cache(dev, kv ? seq.v_cache[i] : seq.k_cache[i], cache_len, p, cache_bytes));
                 p += cache_bytes;
             }
         for (size_t slot = 0; slot < slots; slot++) {

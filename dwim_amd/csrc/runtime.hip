@@ -267,6 +267,10 @@ extern "C" int dwim_copy(dwim_dev *dev, dwim_buf *dst, size_t dst_offset, const 
 
 extern "C" size_t dwim_cache_bytes(size_t len) { return len + len / 32 * 2; }
 
+extern "C" size_t dwim_cache_bytes_of(const dwim_cache *cache, size_t len) {
+    return cache->f16 ? 2 * len : dwim_cache_bytes(len);
+}
+
 extern "C" int dwim_store(dwim_dev *dev, dwim_cache *cache, size_t offset, const dwim_buf *src) {
     DWIM_CHECK(offset % 32 == 0 && src->len % 32 == 0, "stores are whole blocks of 32");
     DWIM_CHECK(offset + src->len <= cache->len, "storing past the end of a cache");
@@ -278,8 +282,10 @@ extern "C" int dwim_store(dwim_dev *dev, dwim_cache *cache, size_t offset, const
     return 0;
 }
 
-extern "C" int dwim_read_cache(dwim_dev *dev, const dwim_cache *cache, size_t len, uint8_t *out) {
+extern "C" int dwim_read_cache(dwim_dev *dev, const dwim_cache *cache, size_t len, uint8_t *out,
+                               size_t out_bytes) {
     DWIM_CHECK(len % 32 == 0 && len <= cache->len, "reading a cache past its end or mid-block");
+    DWIM_CHECK(out_bytes >= dwim_cache_bytes_of(cache, len), "read_cache: the output holds fewer bytes than the cache gives");
     if (len && cache->f16) {
         DWIM_HIP(hipMemcpyAsync(out, cache->q, 2 * len, hipMemcpyDeviceToHost, dev->stream));
     } else if (len) {

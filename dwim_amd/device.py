@@ -62,9 +62,10 @@ SIGNATURES = {
     "dwim_write": (_int, [_vp, _vp, _f32p, _sz]),
     "dwim_copy": (_int, [_vp, _vp, _sz, _vp, _sz, _sz]),
     "dwim_store": (_int, [_vp, _vp, _sz, _vp]),
-    "dwim_read_cache": (_int, [_vp, _vp, _sz, _u8p]),
+    "dwim_read_cache": (_int, [_vp, _vp, _sz, _u8p, _sz]),
     "dwim_write_cache": (_int, [_vp, _vp, _u8p, _sz]),
     "dwim_cache_bytes": (_sz, [_sz]),
+    "dwim_cache_bytes_of": (_sz, [_vp, _sz]),
     "dwim_matmul": (_int, [_vp, _vp, _vp, _vp]),
     "dwim_matmul_add": (_int, [_vp, _vp, _vp, _vp, _vp]),
     "dwim_swiglu": (_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
@@ -356,10 +357,14 @@ class Hip:
     def store(self, cache: Cache, offset: int, src: Buffer):
         _check(self.L.dwim_store(self.h, cache.h, offset, src.h))
 
-    def read_cache(self, cache: Cache, length: int) -> bytes:
-        out = np.empty(2 * length if cache.f16 else self.L.dwim_cache_bytes(length), np.uint8)
-        _check(self.L.dwim_read_cache(self.h, cache.h, length, _ptr(out, _u8p)))
-        return out.tobytes()
+    def read_cache(self, cache: Cache, length: int, out_bytes: int | None = None) -> bytes:
+        """The cache's first `length` activations as stored; `out_bytes` (for
+        tests) sizes the output below what the cache gives, to be refused."""
+        need = self.L.dwim_cache_bytes_of(cache.h, length)
+        out = np.empty(max(need, 1), np.uint8)
+        _check(self.L.dwim_read_cache(self.h, cache.h, length, _ptr(out, _u8p),
+                                      need if out_bytes is None else out_bytes))
+        return out[:need].tobytes()
 
     def write_cache(self, cache: Cache, data: bytes):
         a = np.frombuffer(data, np.uint8).copy()

@@ -97,12 +97,17 @@ int dwim_copy(dwim_dev *dev, dwim_buf *dst, size_t dst_offset, const dwim_buf *s
  * 32 at a time as gpu/quant.rs:161-180 does; offset and length whole blocks. */
 int dwim_store(dwim_dev *dev, dwim_cache *cache, size_t offset, const dwim_buf *src);
 /* Device::read_cache: the first `len` activations as stored, `len` int8 then
- * len/32 little-endian f16 scales: dwim_cache_bytes(len) bytes into `out`. */
-int dwim_read_cache(dwim_dev *dev, const dwim_cache *cache, size_t len, uint8_t *out);
+ * len/32 little-endian f16 scales (an f16 cache: 2·len bytes of f16), that is
+ * dwim_cache_bytes_of(cache, len) bytes, into `out`, which holds `out_bytes`;
+ * a smaller `out` is refused (status 1) with nothing written. */
+int dwim_read_cache(dwim_dev *dev, const dwim_cache *cache, size_t len, uint8_t *out, size_t out_bytes);
 /* Device::write_cache: sets the first activations from bytes as read_cache gives them. */
 int dwim_write_cache(dwim_dev *dev, dwim_cache *cache, const uint8_t *data, size_t bytes);
-/* gpu/mod.rs:404-407 */
+/* gpu/mod.rs:404-407: the bytes of `len` activations of a Q8 cache */
 size_t dwim_cache_bytes(size_t len);
+/* The bytes read_cache gives for `len` activations of this cache, of either
+ * format (Q8: dwim_cache_bytes(len); f16: 2·len). */
+size_t dwim_cache_bytes_of(const dwim_cache *cache, size_t len);
 /* An f16 key/value cache of `len` activations (the f16 KV-cache mode; the
  * reference has only Q8, gpu/mod.rs:39-41,183-186): dwim_store rounds each
  * value to the nearest f16 (ties to even), dwim_read_cache / dwim_write_cache

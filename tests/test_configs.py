@@ -103,6 +103,12 @@ def test_f16_cache_round_trips_and_refuses_mixed_formats():
     gpu.write_cache(c2, data)
     assert gpu.read_cache(c2, x.size) == data
     q8 = gpu.alloc_cache(x.size)
+    # a caller sizing its buffer for a Q8 cache (dwim_cache_bytes) is refused
+    # for an f16 cache, whose read_cache gives 2 bytes a value
+    assert gpu.L.dwim_cache_bytes_of(c.h, x.size) == 2 * x.size
+    assert gpu.L.dwim_cache_bytes_of(q8.h, x.size) == gpu.L.dwim_cache_bytes(x.size)
+    with pytest.raises(D.DwimError, match="fewer bytes"):
+        gpu.read_cache(c, x.size, out_bytes=gpu.L.dwim_cache_bytes(x.size))
     with pytest.raises(D.DwimError, match="different formats"):
         gpu.attention(gpu.alloc(256), gpu.buffer(rng.floats(256)), c, q8, 0, 1, 256, 1)
     gpu.close()
