@@ -40,47 +40,61 @@ def hip():
     return L
 
 
-def kernel_roofline(dev, D, iters=200, copies=8):
-    """The decode matvec (Q4_K, 17408×5120, one token) on its own: the token's
-    activations are prepared once (int8 planes), then `copies` distinct
-    weights (> 256 MB, past the Infinity Cache) are applied in turn, captured
-    in a HIP graph so the launches follow each other without host gaps, timed
-    with HIP events on the device's stream."""
+def graph_us(dev, launch, iters):
+    """Average µs of launch(i) for i < iters, captured in a HIP graph so the
+    launches follow each other without host gaps, timed with HIP events on
+    the device's stream (after two untimed replays)."""
     from dwim_amd.timing import Event
-    rows, cols = 17408, 5120
-    ws = [dev.upload_synthetic(D.Q4_K, rows, cols, seed=100 + i, sigma=0.02) for i in range(copies)]
-    x = dev.buffer(D.synthetic_values(9, 0, cols, 1.0))
-    out = dev.alloc(rows)
-    dev.prepare(x)
-    for i in range(2 * copies):
-        dev.matmul_prepared(out, ws[i % copies])
-    dev.sync()
     L = hip()
     st = ctypes.c_void_p(dev.stream())
     graph, execg = ctypes.c_void_p(), ctypes.c_void_p()
     if L.hipStreamBeginCapture(st, 0) != 0:
         raise RuntimeError("hipStreamBeginCapture failed")
     for i in range(iters):
-        dev.matmul_prepared(out, ws[i % copies])
+        launch(i)
     if L.hipStreamEndCapture(st, ctypes.byref(graph)) != 0:
         raise RuntimeError("hipStreamEndCapture failed")
     if L.hipGraphInstantiate(ctypes.byref(execg), graph, None, None, 0) != 0:
         raise RuntimeError("hipGraphInstantiate failed")
+    L.hipGraphLaunch(execg, st)
     L.hipGraphLaunch(execg, st)
     dev.sync()
     a, b = Event(), Event()
     a.record(st.value)
     L.hipGraphLaunch(execg, st)
     b.record(st.value)
-    ms = a.elapsed_ms(b) / iters
+    us = a.elapsed_ms(b) / iters * 1e3
     L.hipGraphExecDestroy(execg)
     L.hipGraphDestroy(graph)
-    # algorithmic bytes per launch: the Q4_K weights (144 B per 256), x and y in f32
+    return us
+
+
+def kernel_roofline(dev, D, iters=200, copies=8):
+    """The decode step's dominant kernel on its own: the feed-forward SwiGLU
+    pair (k_mv_q4k_mfma<5>, gate and up 17408x5120 Q4_K in one launch, the
+    result's planes handed on), the same launch and grid as in every layer of
+    the decode step, which spends about a third of a token in it.  Also the
+    single 17408x5120 product.  The token's activations are prepared once
+    (int8 planes), then `copies` distinct weights (past the 256 MB Infinity
+    Cache) are applied in turn, graph-launched and timed with HIP events.
+    Algorithmic bytes per launch: the Q4_K weights (144 B per 256), x and the
+    results in f32."""
+    rows, cols = 17408, 5120
+    x = dev.buffer(D.synthetic_values(9, 0, cols, 1.0))
+    out = dev.alloc(rows)
+    dev.prepare(x)
     weight_bytes = rows * cols // 256 * 144
-    algo = weight_bytes + 4 * cols + 4 * rows
-    achieved = algo / (ms * 1e-3) / 1e9
-    return {"kernel": "k_mv_q4k_mfma<5> Q4_K matvec 17408x5120 n=1 (int8 MFMA)", "us": ms * 1e3, "achieved": achieved,
-            "bytes": algo}
+    ws = [dev.upload_synthetic(D.Q4_K, rows, cols, seed=100 + i, sigma=0.02) for i in range(2 * copies)]
+    pair_us = graph_us(dev, lambda i: dev.swiglu_prepared(out, ws[2 * (i % copies)], ws[2 * (i % copies) + 1]), iters)
+    single_us = graph_us(dev, lambda i: dev.matmul_prepared(out, ws[i % copies]), iters)
+    del ws
+    pair_bytes = 2 * weight_bytes + 4 * cols + 4 * rows
+    single_bytes = weight_bytes + 4 * cols + 4 * rows
+    return {"kernel": "k_mv_q4k_mfma<5> SwiGLU pair: gate and up 17408x5120 Q4_K, n=1 (int8 MFMA), "
+                      "the decode step's feed-forward launch",
+            "us": pair_us, "achieved": pair_bytes / (pair_us * 1e-6) / 1e9, "bytes": pair_bytes,
+            "single": {"kernel": "k_mv_q4k_mfma<5> Q4_K matvec 17408x5120 n=1 (int8 MFMA)", "us": single_us,
+                       "achieved": single_bytes / (single_us * 1e-6) / 1e9, "bytes": single_bytes}}
 
 
 def stream_floor(dev, reps=50, copies=8, blocks=2048):
@@ -125,11 +139,11 @@ def copy_calibration(dev, mib=256, reps=8):
     return {"copy_bytes_per_launch": 4 * n}
 
 
-def measured_traffic():
-    """HBM bytes per launch of the roofline kernel, from the committed
-    rocprofv3 PMC passes (FETCH_SIZE, WRITE_SIZE, each scaled by the copy
-    calibration): profiles/q4k_matvec_17408x5120_traffic.json, or None."""
-    p = os.path.join(ROOT, "profiles", "q4k_matvec_17408x5120_traffic.json")
+def measured_traffic(name):
+    """HBM bytes per launch of a roofline kernel, from its committed rocprofv3
+    PMC passes (FETCH_SIZE, WRITE_SIZE, each scaled by the copy calibration):
+    profiles/<name>.json, or None."""
+    p = os.path.join(ROOT, "profiles", name + ".json")
     try:
         with open(p) as f:
             return json.load(f)["hbm_bytes_per_launch"]
@@ -165,7 +179,20 @@ def prefill_flops(cfg, tokens):
     return 2 * params * tokens + n_att * 4 * cfg.heads * cfg.head_dim * pairs + 2 * cfg.vocab * H
 
 
-def cpu_baseline(cfg, seed, state, tokens, pos0, steps=4):
+def cpu_prefill_record():
+    """The one-time CPU prefill of the same 4096-token prompt on the same
+    model, timed when the oracle wrote the config-4 fixture
+    (tests/golden/make_qwen35_27b_tokens.py): profiles/cpu_prefill_27b_4096.json,
+    or None.  Too long (most of an hour) to rerun in every bench."""
+    p = os.path.join(ROOT, "profiles", "cpu_prefill_27b_4096.json")
+    try:
+        with open(p) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(cfg, seed, state, tokens, pos0, steps=16):
     """The reference's CPU path on the same workload: the oracle (C
     restatement of dwim gpu/cpu.rs and inference/qwen35, OpenMP over rows and
     heads as rayon does) builds the same random-init model, restores the GPU
@@ -185,7 +212,14 @@ def cpu_baseline(cfg, seed, state, tokens, pos0, steps=4):
         agree += int(np.argmax(logits)) == int(tokens[i + 1])
     dt = time.perf_counter() - t0
     del o
-    return {"value": steps / dt, "unit": "tok/s", "cores": O.threads(), "kind": "port",
+    pre = cpu_prefill_record()
+    prefill = None
+    if pre:
+        prefill = {"value": pre["tokens"] / pre["seconds"], "unit": "tok/s", "seconds": pre["seconds"],
+                   "cores": pre["threads"], "host": pre["host"], "prompt_sha256": pre["prompt_sha256"],
+                   "source": "profiles/cpu_prefill_27b_4096.json: measured once, when the oracle wrote the "
+                             "config-4 fixture, not in this run"}
+    return {"value": steps / dt, "unit": "tok/s", "cores": O.threads(), "kind": "port", "prefill": prefill,
             "sample": f"C restatement of dwim gpu/cpu.rs + inference/qwen35 (OpenMP), the same 27B-shape model "
                       f"restored from the GPU's state after the 4096-token prefill, {steps} greedy decode tokens "
                       f"at 4k context (model built in {build_s:.0f} s, not timed)",
@@ -352,8 +386,11 @@ def main():
     prefill_roofline = {"bound": "mfma", "achieved": pf / prefill_s / 1e12, "peak": 2500.0, "unit": "TFLOP/s",
                         "frac": pf / prefill_s / 1e12 / 2500.0, "algorithmic_flops": pf,
                         "peak_note": "dense f16 MFMA peak of MI355X",
+                        # from the committed rocprofv3 PMC run, not measured in this run
                         "gemm_mfma_busy": counters["mfma_busy"] if counters else None,
-                        "gemm_mfma_flop_over_algorithmic": counters["mfma_flop_over_algorithmic"] if counters else None}
+                        "gemm_mfma_flop_over_algorithmic": counters["mfma_flop_over_algorithmic"] if counters else None,
+                        "gemm_mfma_source": "profiles/prefill_gemm_mfma.json (committed rocprofv3 --pmc run of "
+                                            "bench.py, not this run)" if counters else None}
     result = {
         "metric": "decode tok/s & prefill tok/s, 27B-shape Q4_K hybrid, 1xMI355X; % HBM peak",
         "value": decode_tps,
@@ -380,15 +417,19 @@ def main():
         "decode_bytes_per_token": token_bytes,
         "model_build_s": build_s,
         "roofline": {"bound": "hbm", "achieved": roof["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": roof["achieved"] / HBM_PEAK_GBS, "traffic": measured_traffic(), "kernel": roof["kernel"],
+                     "frac": roof["achieved"] / HBM_PEAK_GBS,
+                     "traffic": measured_traffic("q4k_swiglu_pair_17408x5120_traffic"), "kernel": roof["kernel"],
                      "kernel_us": roof["us"], "algorithmic_bytes": roof["bytes"],
-                     # the same bytes read and nothing else (dwim_measure_stream), measured in this run
-                     "stream_floor_gbs": floor_gbs, "frac_of_stream_floor": roof["achieved"] / floor_gbs},
+                     # a plain read of one 17408x5120 weight's bytes and nothing else
+                     # (dwim_measure_stream), measured in this run
+                     "stream_floor_gbs": floor_gbs, "frac_of_stream_floor": roof["achieved"] / floor_gbs,
+                     "single_matrix": dict(roof["single"], frac=roof["single"]["achieved"] / HBM_PEAK_GBS,
+                                           traffic=measured_traffic("q4k_matvec_17408x5120_traffic"))},
     }
     model.close()
     if args.mtp:
         result["mtp"] = mtp_leg(dev, D, M, prompt_len=args.mtp_prompt)
-    if not args.no_cpu and len(decoded) > 4:
+    if not args.no_cpu and len(decoded) > 16:
         result["cpu_baseline"] = cpu_baseline(cfg, 1234, state, decoded, args.prompt)
     print(json.dumps(result), flush=True)
 

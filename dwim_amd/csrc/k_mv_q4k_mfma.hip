@@ -598,7 +598,7 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
             a.emit = planes_area(dev, extra->emit_area, ws[0]->rows);
             a.emit_norm = extra->emit_norm;
             a.emit_xw = extra->emit_xw;
-            dev->prepared = 0;
+            if (extra->emit_area == 0) dev->prepared = 0;  // (dwim_prepare's planes are area 0's)
         }
     }
     // a swiglu workgroup takes gate's tile and reads up's beside it

@@ -483,6 +483,20 @@ extern "C" int dwim_matmul_prepared(dwim_dev *dev, dwim_buf *out, const dwim_wei
     return 0;
 }
 
+extern "C" int dwim_swiglu_prepared(dwim_dev *dev, dwim_buf *out, const dwim_weight *gate, const dwim_weight *up) {
+    DWIM_CHECK(gate->fmt == DWIM_Q4_K && up->fmt == DWIM_Q4_K, "swiglu_prepared: Q4_K weights");
+    DWIM_CHECK(up->rows == gate->rows && up->cols == gate->cols, "gate and up differ in shape");
+    DWIM_CHECK(dev->prepared == gate->cols, "swiglu_prepared: no activations of the weights' width prepared");
+    DWIM_CHECK(out->len == gate->rows, "swiglu_prepared: out must hold one row of results");
+    DWIM_CHECK(gate->rows % 256 == 0 && gate->rows <= 80 * 256, "swiglu_prepared: rows in whole planes groups");
+    const dwim_weight *ws[2] = {gate, up};
+    float *outs[2] = {out->data, nullptr};
+    MvExtra e;
+    e.emit_area = 1;
+    LAUNCH(launch_mv_q4k_mfma(dev, ws, outs, nullptr, 2, 1, 0, &e));
+    return 0;
+}
+
 extern "C" int dwim_swiglu(dwim_dev *dev, dwim_buf *out, const dwim_weight *gate, const dwim_weight *up,
                            const dwim_buf *x, dwim_buf *scratch) {
     size_t n;

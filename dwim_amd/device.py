@@ -86,6 +86,7 @@ SIGNATURES = {
     "dwim_argmax": (_int, [_vp, _vp, _sz, _u32p]),
     "dwim_prepare": (_int, [_vp, _vp]),
     "dwim_matmul_prepared": (_int, [_vp, _vp, _vp]),
+    "dwim_swiglu_prepared": (_int, [_vp, _vp, _vp, _vp]),
     "dwim_embed": (_int, [_vp, _vp, _vp, _u32p, _sz]),
     "dwim_quantize_q4_0_row": (None, [_f32p, _sz, _u16p, _u8p]),
     "dwim_quantize_q8_0_row": (None, [_f32p, _sz, _u16p, _i8p]),
@@ -441,6 +442,11 @@ class Hip:
 
     def matmul_prepared(self, out: Buffer, w: Weight):
         _check(self.L.dwim_matmul_prepared(self.h, out.h, w.h))
+
+    def swiglu_prepared(self, out: Buffer, gate: Weight, up: Weight):
+        """out = silu(gate·x)·(up·x) for the prepared x, as the decode step's
+        feed-forward pair launch."""
+        _check(self.L.dwim_swiglu_prepared(self.h, out.h, gate.h, up.h))
 
     def argmax(self, logits: Buffer, rows: int = 1) -> np.ndarray:
         out = np.empty(rows, np.uint32)

@@ -209,6 +209,12 @@ int dwim_argmax(dwim_dev *dev, const dwim_buf *logits, size_t rows, uint32_t *ou
  * dwim_matmul_add or dwim_swiglu, replaces them. */
 int dwim_prepare(dwim_dev *dev, const dwim_buf *x);
 int dwim_matmul_prepared(dwim_dev *dev, dwim_buf *out, const dwim_weight *w);
+/* Device::swiglu for one prepared token (gpu/mod.rs:274-285): out =
+ * silu(gate · x) * (up · x), gate and up Q4_K, in the one launch the decode
+ * step makes for a layer's feed-forward pair, which also writes the result's
+ * planes into the device's second planes area (replacing the planes of any
+ * other one-token product's output held there). */
+int dwim_swiglu_prepared(dwim_dev *dev, dwim_buf *out, const dwim_weight *gate, const dwim_weight *up);
 
 /* out[t] = row tokens[t] of `table` (a rows×cols weight of any format),
  * dequantized: the embedding lookup, which the reference does on the host from

@@ -255,6 +255,23 @@ def test_prepared_activations_serve_several_matrices(gpu):
         gpu.matmul_prepared(gpu.alloc(64), gws[0])
 
 
+def test_swiglu_prepared_matches_cpu_and_keeps_the_planes(gpu):
+    """dwim_swiglu_prepared (the decode step's feed-forward pair launch over
+    prepared activations): silu(gate·x)·(up·x) against the oracle, at the
+    27B shape and a small one; the prepared planes stay, so it repeats."""
+    for rows, cols, seed in ((17408, 5120, 63), (512, 1024, 64)):
+        make = _k_quantized(O.Q4_K, seed)
+        gate, up = make(rows, cols), make(rows, cols)
+        x = O.Rng(seed + 1).floats(cols)
+        want = O.silu_mul(O.matmul(gate, x), O.matmul(up, x))
+        gpu.prepare(gpu.buffer(x))
+        g, u = gpu.upload(to_tensor(gate)), gpu.upload(to_tensor(up))
+        for _ in range(2):
+            out = gpu.alloc(rows)
+            gpu.swiglu_prepared(out, g, u)
+            close(gpu.read(out), want, 1e-4)
+
+
 def test_q4_k_swiglu_and_matmul_add_match_cpu(gpu):
     rng = O.Rng(24)
     # n >= 16 runs the f16 GEMM: SwiGLU in the up product's epilogue, the add,
