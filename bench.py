@@ -6,7 +6,10 @@ A step is one decode token (batch 1) at 4k context: the model is random-init
 (synthetic weights of the 27B shape, Q4_K body, Q6_K head, generated on the
 device), a 4096-token prompt of uniform random ids is prefilled (timed, as
 prefill tok/s), then W untimed and K timed greedy decode steps run.
-`value` is decode tokens/s.
+`value` is decode tokens/s.  The line also carries BASELINE config 5 under
+"mtp" (the model with its MTP drafter: two sessions of 32768-token prompts,
+greedy speculative decoding against plain greedy decoding from the same
+state; --no-mtp skips it).
 
 Prints one JSON line.  --gpus above 1 is refused: this build runs on one GPU.
 """
@@ -307,8 +310,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-only", action="store_true", help="only the decode-matvec roofline leg")
-    ap.add_argument("--mtp", action="store_true",
-                    help="also the speculative-decoding leg (config 5: MTP drafter, 2 sessions of 32768-token prompts)")
+    ap.add_argument("--no-mtp", action="store_true",
+                    help="skip the speculative-decoding leg (config 5: MTP drafter, 2 sessions of 32768-token prompts)")
     ap.add_argument("--mtp-prompt", type=int, default=32768)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -427,7 +430,7 @@ def main():
                                            traffic=measured_traffic("q4k_matvec_17408x5120_traffic"))},
     }
     model.close()
-    if args.mtp:
+    if not args.no_mtp:
         result["mtp"] = mtp_leg(dev, D, M, prompt_len=args.mtp_prompt)
     if not args.no_cpu and len(decoded) > 16:
         result["cpu_baseline"] = cpu_baseline(cfg, 1234, state, decoded, args.prompt)
