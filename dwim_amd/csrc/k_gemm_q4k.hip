@@ -97,6 +97,169 @@ __global__ void k_split_swiglu(const float *__restrict__ g, const float *__restr
     }
 }
 
+// One float4 v of a row of the activations (float4 index i over [n][cols/4])
+// into the split: its f16 hi and lo parts, and (eight consecutive lanes
+// holding a 32-value sub-block) the sub-block's sum; every lane of the wave
+// active.
+DEV void split_put(float4 v, size_t i, size_t cols, _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+                   _Float16 *__restrict__ xm) {
+    const _Float16 h0 = (_Float16)v.x, h1 = (_Float16)v.y, h2 = (_Float16)v.z, h3 = (_Float16)v.w;
+    const _Float16 l0 = (_Float16)(v.x - (float)h0), l1 = (_Float16)(v.y - (float)h1);
+    const _Float16 l2 = (_Float16)(v.z - (float)h2), l3 = (_Float16)(v.w - (float)h3);
+    auto pk = [](_Float16 a, _Float16 b) {
+        return (uint32_t)__builtin_bit_cast(uint16_t, a) | (uint32_t)__builtin_bit_cast(uint16_t, b) << 16;
+    };
+    ((uint2 *)xh)[i] = make_uint2(pk(h0, h1), pk(h2, h3));
+    ((uint2 *)xl)[i] = make_uint2(pk(l0, l1), pk(l2, l3));
+    const float s = group_sum<8>((v.x + v.y) + (v.z + v.w));
+    if ((i & 7) == 0) {
+        const size_t sbi = i / 8, t = sbi / (cols / 32), sb = sbi % (cols / 32), b = sb / 8, j = sb % 8;
+        _Float16 *m = xm + (t * (cols / 256) + b) * 16;
+        const _Float16 sh = (_Float16)s;
+        m[j] = sh;
+        m[8 + j] = (_Float16)(s - (float)sh);
+    }
+}
+
+// k_split of rmsnorm(x)·w (gpu/cpu.rs:157-166) for rows of up to
+// kRmsMaxCols: a block a token, the sum of squares taken in k_rmsnorm's order
+// and the normalized values its bits (x·(scale·w)), passed through LDS from
+// the reduction's layout (element tid + 256k) to the split's (a float4 a
+// lane); with xn_out, the normalized row written there in f32 too.
+constexpr int kRmsMaxCols = 8192;
+
+__global__ void __launch_bounds__(256) k_split_rms(const float *__restrict__ x, const float *__restrict__ w, float eps,
+                                                   _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+                                                   _Float16 *__restrict__ xm, float *__restrict__ xn_out,
+                                                   size_t cols) {
+    __shared__ float red[4];
+    __shared__ float4 row[kRmsMaxCols / 4];
+    const size_t t = blockIdx.x;
+    const float *xr = x + t * cols;
+    const int tid = threadIdx.x, per = (int)(cols / 256);
+    float v[kRmsMaxCols / 256];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRmsMaxCols / 256; k++)
+        if (k < per) {
+            v[k] = xr[tid + 256 * k];
+            ss += v[k] * v[k];
+        }
+    ss = block_sum<256>(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)cols + eps);
+    float *rf = (float *)row;
+#pragma unroll
+    for (int k = 0; k < kRmsMaxCols / 256; k++)
+        if (k < per) rf[tid + 256 * k] = v[k] * (scale * w[tid + 256 * k]);
+    __syncthreads();
+    const size_t n4 = cols / 4;
+    for (size_t j = tid; j < n4; j += 256) {
+        const float4 y = row[j];
+        if (xn_out) ((float4 *)(xn_out + t * cols))[j] = y;
+        split_put(y, t * n4 + j, cols, xh, xl, xm);
+    }
+}
+
+// k_split of the DeltaNet output gate, silu(z)·rmsnorm(att)·w per head of
+// dim (gpu/cpu.rs:157-166, 238-242): k_gated_norm's values, bit for bit,
+// split as they are made (the gated z is not written).
+template <int LANES>  // dim / 4: the lanes of a head
+__global__ void __launch_bounds__(256) k_split_gated(const float *__restrict__ z, const float *__restrict__ att,
+                                                     const float *__restrict__ w, size_t total, size_t dim, float eps,
+                                                     _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+                                                     _Float16 *__restrict__ xm, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // a float4 of the [n][total] rows
+    if (i * 4 >= n * total) return;  // whole waves of float4s
+    const float4 a = ((const float4 *)att)[i];
+    const float ss = group_sum<LANES>((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w));
+    const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
+    const float4 nw = ((const float4 *)w)[(i * 4 % dim) / 4];
+    float4 g = ((const float4 *)z)[i];
+    g.x = g.x * sigmoidf_(g.x) * (a.x * (scale * nw.x));
+    g.y = g.y * sigmoidf_(g.y) * (a.y * (scale * nw.y));
+    g.z = g.z * sigmoidf_(g.z) * (a.z * (scale * nw.z));
+    g.w = g.w * sigmoidf_(g.w) * (a.w * (scale * nw.w));
+    split_put(g, i, total, xh, xl, xm);
+}
+
+// A small bf16 matrix (up to kBfRows rows: the DeltaNet gate projection's
+// 96) against a batch's prepared split, on the f16 matrix cores: every bf16
+// weight of f16 range is an f16 exactly (8 significant bits of 11; weights
+// under 2^-14 keep f16's subnormal spacing, 2^-24, far below the products'
+// rounding), so w·x = w·hi + w·lo as two MFMA chains in f32, the same
+// accuracy as the split's other products.  A workgroup of 4 waves takes 32
+// tokens and every row, its waves splitting the columns in 4 runs (the next
+// step's loads issued while the current one is multiplied) and meeting in
+// LDS, in wave order; out = or += the sums.
+constexpr int kBfRows = 96, kBfWaves = 4;
+
+__global__ void __launch_bounds__(64 * kBfWaves) k_bf16_split(const uint16_t *__restrict__ w, float *__restrict__ out,
+                                                              const _Float16 *__restrict__ xh,
+                                                              const _Float16 *__restrict__ xl, unsigned rows,
+                                                              unsigned cols, unsigned n, int add) {
+    __shared__ float part[kBfWaves][kBfRows / 32][32 * 33];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r32 = lane & 31, kh = lane >> 5;
+    const unsigned tok0 = blockIdx.x * 32, t = tok0 + r32;
+    const bool tlive = t < n;
+    const unsigned steps = cols / 16, s0 = wave * steps / kBfWaves, s1 = (wave + 1) * steps / kBfWaves;
+    // lane: A row r32 of each 32-row tile, B token r32, k = 16·step + 8·kh..+7
+    const uint4 *wr[kBfRows / 32];
+#pragma unroll
+    for (int i = 0; i < kBfRows / 32; i++) {
+        const unsigned r = 32 * i + r32 < rows ? 32 * i + r32 : 0;
+        wr[i] = (const uint4 *)(w + (size_t)r * cols + 8 * kh);
+    }
+    const size_t xo = (size_t)(tlive ? t : 0) * cols + 8 * kh;
+    const uint4 *ph = (const uint4 *)(xh + xo), *pl = (const uint4 *)(xl + xo);
+    float16v acc[kBfRows / 32];
+#pragma unroll
+    for (int i = 0; i < kBfRows / 32; i++) acc[i] = float16v{};
+    uint4 wa[kBfRows / 32], ha, la;
+    auto load = [&](unsigned s) {
+#pragma unroll
+        for (int i = 0; i < kBfRows / 32; i++) wa[i] = wr[i][2 * s];
+        ha = ph[2 * s];
+        la = pl[2 * s];
+    };
+    if (s0 < s1) load(s0);
+    for (unsigned s = s0; s < s1; s++) {
+        half8 a[kBfRows / 32];
+#pragma unroll
+        for (int i = 0; i < kBfRows / 32; i++) {
+            const uint32_t v[4] = {wa[i].x, wa[i].y, wa[i].z, wa[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                a[i][2 * e] = (_Float16)__uint_as_float(v[e] << 16);
+                a[i][2 * e + 1] = (_Float16)__uint_as_float(v[e] & 0xffff0000u);
+            }
+        }
+        const half8 bh = __builtin_bit_cast(half8, ha), bl = __builtin_bit_cast(half8, la);
+        if (s + 1 < s1) load(s + 1);
+#pragma unroll
+        for (int i = 0; i < kBfRows / 32; i++) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl, acc[i], 0, 0, 0);
+        }
+    }
+    // C tile i: lane holds rows 32i + 8g + 4kh + e of token r32
+#pragma unroll
+    for (int i = 0; i < kBfRows / 32; i++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) part[wave][i][r32 * 33 + 8 * g + 4 * kh + e] = acc[i][4 * g + e];
+    __syncthreads();
+    for (unsigned idx = threadIdx.x; idx < 32u * kBfRows; idx += 64 * kBfWaves) {
+        const unsigned tt = idx / kBfRows, r = idx % kBfRows;
+        if (r >= rows || tok0 + tt >= n) continue;
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kBfWaves; q++) v += part[q][r / 32][tt * 33 + r % 32];
+        float *o = out + (size_t)(tok0 + tt) * rows + r;
+        *o = add ? *o + v : v;
+    }
+}
+
 // what a product does with its result r and the output's old value o
 // (gpu/mod.rs:259 the add, gpu/cpu.rs:238-242 the SwiGLU's silu(gate)·up)
 DEV float gemm_out(int mode, float o, float r) {
@@ -642,6 +805,48 @@ hipError_t gemm_run_swiglu_pair(dwim_dev *dev, const dwim_weight *gate, const dw
     k_split_swiglu<<<(unsigned)((subs * 8 + 255) / 256), 256, 0, dev->stream>>>(g, u, xh, xl, xm, n, cols);
     dev->split_n = n;
     dev->split_cols = cols;
+    return hipGetLastError();
+}
+
+hipError_t gemm_prepare_rms(dwim_dev *dev, const float *x, const float *norm, float eps, size_t n, size_t cols,
+                            float *xn_out) {
+    if (cols % 256 || n >= (1u << 31)) return hipErrorInvalidValue;
+    if (cols > (size_t)kRmsMaxCols) {
+        float *xn = xn_out ? xn_out : dev_work(dev, n * cols);
+        if (!xn) return hipErrorOutOfMemory;
+        hipError_t e = launch_rmsnorm(dev->stream, xn, x, norm, n, cols, eps);
+        return e != hipSuccess ? e : gemm_prepare(dev, xn, n, cols);
+    }
+    hipError_t e = dev_grow(dev, &dev->split, &dev->split_cap, gemm_split_bytes(n, cols), 1);
+    if (e != hipSuccess) return e;
+    _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * cols, *xm = xl + n * cols;
+    k_split_rms<<<(unsigned)n, 256, 0, dev->stream>>>(x, norm, eps, xh, xl, xm, xn_out, cols);
+    dev->split_n = n;
+    dev->split_cols = cols;
+    return hipGetLastError();
+}
+
+hipError_t gemm_prepare_gated(dwim_dev *dev, const float *z, const float *att, const float *norm, float eps, size_t n,
+                              size_t total, size_t dim) {
+    if (total % 256 || (dim != 128 && dim != 256) || total % dim || n >= (1u << 31)) return hipErrorInvalidValue;
+    hipError_t e = dev_grow(dev, &dev->split, &dev->split_cap, gemm_split_bytes(n, total), 1);
+    if (e != hipSuccess) return e;
+    _Float16 *xh = (_Float16 *)dev->split, *xl = xh + n * total, *xm = xl + n * total;
+    const unsigned blocks = (unsigned)((n * total / 4 + 255) / 256);
+    if (dim == 128) k_split_gated<32><<<blocks, 256, 0, dev->stream>>>(z, att, norm, total, dim, eps, xh, xl, xm, n);
+    else k_split_gated<64><<<blocks, 256, 0, dev->stream>>>(z, att, norm, total, dim, eps, xh, xl, xm, n);
+    dev->split_n = n;
+    dev->split_cols = total;
+    return hipGetLastError();
+}
+
+hipError_t gemm_run_bf16(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, int add) {
+    if (w->fmt != DWIM_BF16 || w->rows > (size_t)kBfRows || w->cols % 16 || dev->split_n != n ||
+        dev->split_cols != w->cols || n >= (1u << 31))
+        return hipErrorInvalidValue;
+    const _Float16 *xh = (const _Float16 *)dev->split, *xl = xh + n * w->cols;
+    k_bf16_split<<<(unsigned)((n + 31) / 32), 64 * kBfWaves, 0, dev->stream>>>(
+        (const uint16_t *)w->q, out, xh, xl, (unsigned)w->rows, (unsigned)w->cols, (unsigned)n, add);
     return hipGetLastError();
 }
 

@@ -20,15 +20,8 @@ hipError_t launch_matvec_q4k_multi(dwim_dev *dev, const dwim_weight *const *ws, 
         if (ws[j]->cols != ws[0]->cols || ws[j]->fmt != DWIM_Q4_K) return hipErrorInvalidValue;
     if (n < kGemmTokens) return launch_mv_q4k_mfma_tokens(dev, ws, outs, nullptr, count, 0, x, n, norm, eps, xn_out);
     {
-        const float *in = x;
-        if (norm) {
-            float *xn = xn_out ? xn_out : dev_work(dev, n * ws[0]->cols);
-            if (!xn) return hipErrorOutOfMemory;
-            hipError_t e = launch_rmsnorm(dev->stream, xn, x, norm, n, ws[0]->cols, eps);
-            if (e != hipSuccess) return e;
-            in = xn;
-        }
-        hipError_t e = gemm_prepare(dev, in, n, ws[0]->cols);
+        hipError_t e = norm ? gemm_prepare_rms(dev, x, norm, eps, n, ws[0]->cols, xn_out)
+                            : gemm_prepare(dev, x, n, ws[0]->cols);
         for (int j = 0; j < count && e == hipSuccess; j++) e = gemm_run(dev, ws[j], outs[j], n, kGemmStore);
         return e;
     }
@@ -45,15 +38,7 @@ hipError_t launch_swiglu_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_
     {
         // x normalized, split once; gate·x into out, then out = silu(out)·(up·x)
         const size_t cols = gate->cols;
-        const float *in = x;
-        if (norm) {
-            float *xn = dev_work(dev, n * cols);
-            if (!xn) return hipErrorOutOfMemory;
-            hipError_t e = launch_rmsnorm(dev->stream, xn, x, norm, n, cols, eps);
-            if (e != hipSuccess) return e;
-            in = xn;
-        }
-        hipError_t e = gemm_prepare(dev, in, n, cols);
+        hipError_t e = norm ? gemm_prepare_rms(dev, x, norm, eps, n, cols, nullptr) : gemm_prepare(dev, x, n, cols);
         if (e == hipSuccess) e = gemm_run(dev, gate, out, n, kGemmStore);
         if (e == hipSuccess) e = gemm_run(dev, up, out, n, kGemmSiluGate);
         return e;
@@ -64,11 +49,7 @@ hipError_t launch_ffn_q4k(dwim_dev *dev, const dwim_weight *gate, const dwim_wei
                           float *x, size_t n, const float *norm, float eps, float *g, float *u) {
     if (n < kGemmTokens || gate->fmt != DWIM_Q4_K || down->fmt != DWIM_Q4_K || down->cols != gate->rows)
         return hipErrorInvalidValue;
-    const size_t cols = gate->cols;
-    float *xn = dev_work(dev, n * cols);
-    if (!xn) return hipErrorOutOfMemory;
-    hipError_t e = launch_rmsnorm(dev->stream, xn, x, norm, n, cols, eps);
-    if (e == hipSuccess) e = gemm_prepare(dev, xn, n, cols);
+    hipError_t e = gemm_prepare_rms(dev, x, norm, eps, n, gate->cols, nullptr);
     if (e == hipSuccess) e = gemm_run_swiglu_pair(dev, gate, up, g, u, n);
     if (e == hipSuccess) e = gemm_run(dev, down, x, n, kGemmAdd);
     return e;

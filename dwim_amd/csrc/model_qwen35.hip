@@ -432,8 +432,15 @@ struct dwim_model {
                 }
                 const dwim_weight *ws[2] = {l.qkv, l.z};
                 dwim_buf *outs[2] = {qkv_in, z};
-                TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
-                TRY(dwim_matmul(dev, ab_in, l.ab, xh));
+                if (n >= 16 && l.ab->fmt == DWIM_BF16 && l.ab->rows <= 96 && l.qkv->fmt == DWIM_Q4_K) {
+                    // the gate projection over the same split as qkv and z
+                    TRY(projections(ws, outs, 2, l.attn_norm, n, nullptr));
+                    TRY(dwim_resize(dev, ab_in, n * 2 * c.v_heads));
+                    DWIM_HIP(gemm_run_bf16(dev, l.ab, ab_in->data, n, 0));
+                } else {
+                    TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
+                    TRY(dwim_matmul(dev, ab_in, l.ab, xh));
+                }
                 TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv_in, state, l.conv, c.state_dim, eps));
                 if (verify) {
                     DWIM_HIP(launch_delta_net(dev, att->data, q->data, k->data, v->data, ab_in->data, l.decay->data,
@@ -443,8 +450,15 @@ struct dwim_model {
                     TRY(dwim_delta_net_unit_keys(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads,
                                                  c.state_dim));
                 }
-                DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps, -1));
-                TRY(dwim_matmul_add(dev, x, l.out, z, xb));
+                if (n >= 16 && l.out->fmt == DWIM_Q4_K) {
+                    // the gated norm made in the out product's split
+                    DWIM_HIP(gemm_prepare_gated(dev, z->data, att->data, l.norm->data, eps, n, v_dim(), c.state_dim));
+                    DWIM_HIP(gemm_run(dev, l.out, x->data, n, kGemmAdd));
+                } else {
+                    DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps,
+                                               -1));
+                    TRY(dwim_matmul_add(dev, x, l.out, z, xb));
+                }
             } else {
                 TRY(dwim_matmul(dev, qkv, l.qkv, xh));
                 TRY(dwim_matmul(dev, z, l.z, xh));

@@ -278,7 +278,18 @@ hipError_t launch_gemm_q4k(dwim_dev *dev, const dwim_weight *w, float *out, cons
 // gemm_run multiplies a weight of that many columns by them, out by the mode.
 enum GemmMode { kGemmStore = 0, kGemmAdd = 1, kGemmSiluGate = 2 /* out = silu(out)·(w·x) */ };
 hipError_t gemm_prepare(dwim_dev *dev, const float *x, size_t n, size_t cols);
+// gemm_prepare of rmsnorm(x)·norm (the values launch_rmsnorm gives, in one
+// pass over x), the normalized rows also to xn_out when given
+hipError_t gemm_prepare_rms(dwim_dev *dev, const float *x, const float *norm, float eps, size_t n, size_t cols,
+                            float *xn_out);
+// gemm_prepare of silu(z)·rmsnorm(att)·norm per head of dim (the values
+// launch_gated_norm gives; z is not written)
+hipError_t gemm_prepare_gated(dwim_dev *dev, const float *z, const float *att, const float *norm, float eps, size_t n,
+                              size_t total, size_t dim);
 hipError_t gemm_run(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, int mode);
+// out (+)= w · x for a bf16 matrix of up to 96 rows over the prepared split
+// (the DeltaNet gate projection of a batch), on the f16 matrix cores
+hipError_t gemm_run_bf16(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, int add);
 // gate and up over the prepared split in one launch, g and u written plain;
 // then the split of silu(g)·u prepared for the down product
 hipError_t gemm_run_swiglu_pair(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *g, float *u,
