@@ -122,10 +122,10 @@ DEV void split_put(float4 v, size_t i, size_t cols, _Float16 *__restrict__ xh, _
 }
 
 // k_split of rmsnorm(x)·w (gpu/cpu.rs:157-166) for rows of up to
-// kRmsMaxCols: a block a token, the sum of squares taken in k_rmsnorm's order
-// and the normalized values its bits (x·(scale·w)), passed through LDS from
-// the reduction's layout (element tid + 256k) to the split's (a float4 a
-// lane); with xn_out, the normalized row written there in f32 too.
+// kRmsMaxCols: a block a token, a float4 a lane in turn (the split's layout:
+// eight consecutive lanes hold a sub-block), its sum of squares reduced over
+// the block, y = x·(scale·w) as k_rmsnorm makes it; with xn_out, the
+// normalized row written there in f32 too.
 constexpr int kRmsMaxCols = 8192;
 
 __global__ void __launch_bounds__(256) k_split_rms(const float *__restrict__ x, const float *__restrict__ w, float eps,
@@ -133,28 +133,27 @@ __global__ void __launch_bounds__(256) k_split_rms(const float *__restrict__ x, 
                                                    _Float16 *__restrict__ xm, float *__restrict__ xn_out,
                                                    size_t cols) {
     __shared__ float red[4];
-    __shared__ float4 row[kRmsMaxCols / 4];
-    const size_t t = blockIdx.x;
-    const float *xr = x + t * cols;
-    const int tid = threadIdx.x, per = (int)(cols / 256);
-    float v[kRmsMaxCols / 256];
+    constexpr int kPer = kRmsMaxCols / 4 / 256;
+    const size_t t = blockIdx.x, n4 = cols / 4;
+    const float4 *xr = (const float4 *)(x + t * cols);
+    const int tid = threadIdx.x;
+    float4 v[kPer];
     float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kRmsMaxCols / 256; k++)
-        if (k < per) {
-            v[k] = xr[tid + 256 * k];
-            ss += v[k] * v[k];
-        }
+    for (int k = 0; k < kPer; k++) {
+        const size_t j = tid + 256 * k;
+        v[k] = j < n4 ? xr[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        ss += (v[k].x * v[k].x + v[k].y * v[k].y) + (v[k].z * v[k].z + v[k].w * v[k].w);
+    }
     ss = block_sum<256>(ss, red);
     const float scale = 1.0f / sqrtf(ss / (float)cols + eps);
-    float *rf = (float *)row;
 #pragma unroll
-    for (int k = 0; k < kRmsMaxCols / 256; k++)
-        if (k < per) rf[tid + 256 * k] = v[k] * (scale * w[tid + 256 * k]);
-    __syncthreads();
-    const size_t n4 = cols / 4;
-    for (size_t j = tid; j < n4; j += 256) {
-        const float4 y = row[j];
+    for (int k = 0; k < kPer; k++) {
+        const size_t j = tid + 256 * k;
+        if (j >= n4) break;  // (cols a multiple of 256: whole waves)
+        const float4 nw = ((const float4 *)w)[j];
+        const float4 y = make_float4(v[k].x * (scale * nw.x), v[k].y * (scale * nw.y), v[k].z * (scale * nw.z),
+                                     v[k].w * (scale * nw.w));
         if (xn_out) ((float4 *)(xn_out + t * cols))[j] = y;
         split_put(y, t * n4 + j, cols, xh, xl, xm);
     }
@@ -187,45 +186,46 @@ __global__ void __launch_bounds__(256) k_split_gated(const float *__restrict__ z
 // weight of f16 range is an f16 exactly (8 significant bits of 11; weights
 // under 2^-14 keep f16's subnormal spacing, 2^-24, far below the products'
 // rounding), so w·x = w·hi + w·lo as two MFMA chains in f32, the same
-// accuracy as the split's other products.  A workgroup of 4 waves takes 32
-// tokens and every row, its waves splitting the columns in 4 runs (the next
-// step's loads issued while the current one is multiplied) and meeting in
-// LDS, in wave order; out = or += the sums.
-constexpr int kBfRows = 96, kBfWaves = 4;
+// accuracy as the split's other products.  A workgroup of 4 waves takes 16
+// tokens and every row (v_mfma_f32_16x16x32_f16: 6 row tiles), its waves
+// splitting the columns in 4 runs (the next step's loads issued while the
+// current one is multiplied) and meeting in LDS, in wave order; out = or +=
+// the sums.
+constexpr int kBfRows = 96, kBfWaves = 4, kBfTiles = kBfRows / 16;
 
 __global__ void __launch_bounds__(64 * kBfWaves) k_bf16_split(const uint16_t *__restrict__ w, float *__restrict__ out,
                                                               const _Float16 *__restrict__ xh,
                                                               const _Float16 *__restrict__ xl, unsigned rows,
                                                               unsigned cols, unsigned n, int add) {
-    __shared__ float part[kBfWaves][kBfRows / 32][32 * 33];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r32 = lane & 31, kh = lane >> 5;
-    const unsigned tok0 = blockIdx.x * 32, t = tok0 + r32;
+    __shared__ float part[kBfWaves][16][kBfRows + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, kq = lane >> 4;
+    const unsigned tok0 = blockIdx.x * 16, t = tok0 + r16;
     const bool tlive = t < n;
-    const unsigned steps = cols / 16, s0 = wave * steps / kBfWaves, s1 = (wave + 1) * steps / kBfWaves;
-    // lane: A row r32 of each 32-row tile, B token r32, k = 16·step + 8·kh..+7
-    const uint4 *wr[kBfRows / 32];
+    const unsigned steps = cols / 32, s0 = wave * steps / kBfWaves, s1 = (wave + 1) * steps / kBfWaves;
+    // lane: A row r16 of each 16-row tile, B token r16, k = 32·step + 8·kq..+7
+    const uint4 *wr[kBfTiles];
 #pragma unroll
-    for (int i = 0; i < kBfRows / 32; i++) {
-        const unsigned r = 32 * i + r32 < rows ? 32 * i + r32 : 0;
-        wr[i] = (const uint4 *)(w + (size_t)r * cols + 8 * kh);
+    for (int i = 0; i < kBfTiles; i++) {
+        const unsigned r = 16 * i + r16 < rows ? 16 * i + r16 : 0;
+        wr[i] = (const uint4 *)(w + (size_t)r * cols + 8 * kq);
     }
-    const size_t xo = (size_t)(tlive ? t : 0) * cols + 8 * kh;
+    const size_t xo = (size_t)(tlive ? t : 0) * cols + 8 * kq;
     const uint4 *ph = (const uint4 *)(xh + xo), *pl = (const uint4 *)(xl + xo);
-    float16v acc[kBfRows / 32];
+    float4v acc[kBfTiles];
 #pragma unroll
-    for (int i = 0; i < kBfRows / 32; i++) acc[i] = float16v{};
-    uint4 wa[kBfRows / 32], ha, la;
+    for (int i = 0; i < kBfTiles; i++) acc[i] = float4v{};
+    uint4 wa[kBfTiles], ha, la;
     auto load = [&](unsigned s) {
 #pragma unroll
-        for (int i = 0; i < kBfRows / 32; i++) wa[i] = wr[i][2 * s];
-        ha = ph[2 * s];
-        la = pl[2 * s];
+        for (int i = 0; i < kBfTiles; i++) wa[i] = wr[i][4 * s];
+        ha = ph[4 * s];
+        la = pl[4 * s];
     };
     if (s0 < s1) load(s0);
     for (unsigned s = s0; s < s1; s++) {
-        half8 a[kBfRows / 32];
+        half8 a[kBfTiles];
 #pragma unroll
-        for (int i = 0; i < kBfRows / 32; i++) {
+        for (int i = 0; i < kBfTiles; i++) {
             const uint32_t v[4] = {wa[i].x, wa[i].y, wa[i].z, wa[i].w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -236,25 +236,23 @@ __global__ void __launch_bounds__(64 * kBfWaves) k_bf16_split(const uint16_t *__
         const half8 bh = __builtin_bit_cast(half8, ha), bl = __builtin_bit_cast(half8, la);
         if (s + 1 < s1) load(s + 1);
 #pragma unroll
-        for (int i = 0; i < kBfRows / 32; i++) {
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh, acc[i], 0, 0, 0);
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl, acc[i], 0, 0, 0);
+        for (int i = 0; i < kBfTiles; i++) {
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bh, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bl, acc[i], 0, 0, 0);
         }
     }
-    // C tile i: lane holds rows 32i + 8g + 4kh + e of token r32
+    // C tile i: lane holds rows 16i + 4kq + e of token r16
 #pragma unroll
-    for (int i = 0; i < kBfRows / 32; i++)
+    for (int i = 0; i < kBfTiles; i++)
 #pragma unroll
-        for (int g = 0; g < 4; g++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) part[wave][i][r32 * 33 + 8 * g + 4 * kh + e] = acc[i][4 * g + e];
+        for (int e = 0; e < 4; e++) part[wave][r16][16 * i + 4 * kq + e] = acc[i][e];
     __syncthreads();
-    for (unsigned idx = threadIdx.x; idx < 32u * kBfRows; idx += 64 * kBfWaves) {
+    for (unsigned idx = threadIdx.x; idx < 16u * kBfRows; idx += 64 * kBfWaves) {
         const unsigned tt = idx / kBfRows, r = idx % kBfRows;
         if (r >= rows || tok0 + tt >= n) continue;
         float v = 0.0f;
 #pragma unroll
-        for (int q = 0; q < kBfWaves; q++) v += part[q][r / 32][tt * 33 + r % 32];
+        for (int q = 0; q < kBfWaves; q++) v += part[q][tt][r];
         float *o = out + (size_t)(tok0 + tt) * rows + r;
         *o = add ? *o + v : v;
     }
@@ -841,11 +839,11 @@ hipError_t gemm_prepare_gated(dwim_dev *dev, const float *z, const float *att, c
 }
 
 hipError_t gemm_run_bf16(dwim_dev *dev, const dwim_weight *w, float *out, size_t n, int add) {
-    if (w->fmt != DWIM_BF16 || w->rows > (size_t)kBfRows || w->cols % 16 || dev->split_n != n ||
+    if (w->fmt != DWIM_BF16 || w->rows > (size_t)kBfRows || w->cols % 32 || dev->split_n != n ||
         dev->split_cols != w->cols || n >= (1u << 31))
         return hipErrorInvalidValue;
     const _Float16 *xh = (const _Float16 *)dev->split, *xl = xh + n * w->cols;
-    k_bf16_split<<<(unsigned)((n + 31) / 32), 64 * kBfWaves, 0, dev->stream>>>(
+    k_bf16_split<<<(unsigned)((n + 15) / 16), 64 * kBfWaves, 0, dev->stream>>>(
         (const uint16_t *)w->q, out, xh, xl, (unsigned)w->rows, (unsigned)w->cols, (unsigned)n, add);
     return hipGetLastError();
 }
