@@ -182,6 +182,8 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
 // at most 1 in size and the substitution is well conditioned.
 constexpr int kC = 64;
 // k_dn_prep's LDS for `ratio` value heads a key head
+constexpr size_t kPrepMaxLds = 160 * 1024;  // a workgroup's LDS on gfx950
+
 size_t prep_lds_bytes(int ratio) {
     return (size_t)ratio * kC * sizeof(double) + ((size_t)ratio * kC + (1 + (ratio < 4 ? ratio : 4)) * kC * kC) * sizeof(float);
 }
@@ -540,13 +542,13 @@ hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const flo
         if (e != hipSuccess) return e;
         float *X = dev->dn_work, *M = X + n_v_heads * nch * kC * kC, *dec = M + n_v_heads * nch * kC * kC;
         const size_t lds = prep_lds_bytes((int)(n_v_heads / n_k_heads));
-        static size_t lds_set = 0;
-        if (lds > lds_set) {
-            hipError_t e = hipFuncSetAttribute((const void *)k_dn_prep, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)lds);
-            if (e != hipSuccess) return e;
-            lds_set = lds;
-        }
+        // raised to the largest the kernel can take, once a process (a
+        // function-local static is initialized once even when host threads
+        // reach it together); a larger request is refused below
+        static const hipError_t raised = hipFuncSetAttribute(
+            (const void *)k_dn_prep, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrepMaxLds);
+        if (raised != hipSuccess) return raised;
+        if (lds > kPrepMaxLds) return hipErrorInvalidValue;
         k_dn_prep<<<dim3((unsigned)nch, (unsigned)n_k_heads), 256, lds, dev->stream>>>(q, k, gates, decay, X, M, dec, n,
                                                                                    (int)n_k_heads, (int)n_v_heads);
         k_dn_chunks<<<(unsigned)(8 * n_v_heads), 256, 0, dev->stream>>>(out, q, k, v, X, M, dec, state, n,
