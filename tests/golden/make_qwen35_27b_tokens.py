@@ -13,7 +13,7 @@ token wherever the gap exceeds the tolerance, and the logits it stores within
 
 The oracle (oracle/, the C restatement of dwim gpu/cpu.rs and
 inference/qwen35/mod.rs) runs on this container's CPUs: about 45 minutes for
-the prefill and 3 s a decode token on 8 cores.  Usage:
+the prefill and 3.6 s a decode token on 8 cores.  Usage:
     python tests/golden/make_qwen35_27b_tokens.py [decode_tokens [output.npz]]
 """
 import os
