@@ -162,6 +162,161 @@ __global__ void __launch_bounds__(kThreads) k_delta_net(float *__restrict__ out,
 }
 
 
+// ---- A small batch's whole mixer step --------------------------------------
+//
+// For batches of up to kSmallT tokens (speculative-decoding verify batches,
+// the rewind's re-run, small prompt pieces): the conv of 4 taps + SiLU over
+// the batch with its carried state (gpu/cpu.rs:250-296), the l2 norms of q
+// and k (:157-166 without weights) and the delta rule (:298-363), in one
+// launch of k_delta_net's blocks (16 value columns of one head a block, the
+// state slice in registers).  Each block makes its key head's q and k itself
+// (a channel a thread, the window sliding in registers, each token's norm a
+// block sum) and its own 16 value channels, straight into the LDS the token
+// loop reads; the conv state carried to the next batch is written by the key
+// head's first block (q and k channels) and by each block (its value
+// channels).  The same arithmetic as the three calls it replaces.
+constexpr int kSmallT = 16;
+
+__global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out, const float *__restrict__ qkv,
+                                                         const float *__restrict__ conv_state,
+                                                         float *__restrict__ conv_state_out,
+                                                         const float *__restrict__ conv_w,
+                                                         const float *__restrict__ gates,
+                                                         const float *__restrict__ decay, float *state,
+                                                         const float *state_in, int n, int n_k_heads, int n_v_heads,
+                                                         float eps) {
+    __shared__ float kqs[2][kSmallT][kD];          // normalized k, q of each token
+    __shared__ float tile[kD][kCols + 1];          // the state slice's staging
+    __shared__ float vs[kSmallT][kCols];
+    __shared__ float2 gb[kSmallT];
+    __shared__ float red[kSmallT][kThreads / 64];
+    const int h = blockIdx.y, c0 = blockIdx.x * kCols, tid = threadIdx.x;
+    const int ratio = n_v_heads / n_k_heads, kh = h / ratio;
+    const int c = tid / kParts, p = tid % kParts;
+    const size_t ch = (size_t)(2 * n_k_heads + n_v_heads) * kD;
+    float *S = state + (size_t)h * kD * kD;
+    const float *Sin = state_in + (size_t)h * kD * kD;
+
+    // ---- loads: the state slice, this thread's q or k channel over the
+    // batch (with its window and weights), the block's value channels, the
+    // gate logits
+    for (int e = tid; e < kD * kCols; e += kThreads) tile[e / kCols][e % kCols] = Sin[(e / kCols) * kD + c0 + e % kCols];
+    const size_t qk = tid < kD ? (size_t)kh * kD + tid : (size_t)(n_k_heads + kh) * kD + (tid - kD);
+    float win[kSmallT + 3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) win[j] = conv_state[(size_t)j * ch + qk];
+#pragma unroll
+    for (int t = 0; t < kSmallT; t++) win[3 + t] = t < n ? qkv[(size_t)t * ch + qk] : 0.0f;
+    const float4 w = ((const float4 *)conv_w)[qk];
+    const size_t vc = (size_t)(2 * n_k_heads + h) * kD + c0 + (tid % kCols);
+    const bool vlane = tid < kCols;
+    const float a = decay[h], dt = decay[n_v_heads + h];
+
+    // ---- q and k: conv + SiLU, each token's sum of squares a block sum
+    // over its half (q: waves 0-1, k: waves 2-3)
+    float y[kSmallT];
+#pragma unroll
+    for (int t = 0; t < kSmallT; t++) {
+        float acc = 0.0f;
+        acc += w.x * win[t];
+        acc += w.y * win[t + 1];
+        acc += w.z * win[t + 2];
+        acc += w.w * win[t + 3];
+        y[t] = acc * sigmoidf_(acc);
+        const float sq = group_sum<64>(y[t] * y[t]);
+        if ((tid & 63) == 0 && t < n) red[t][tid >> 6] = sq;
+    }
+    if (blockIdx.x == 0 && h % ratio == 0) {
+        // the last three inputs carry over (the state's rows when the batch
+        // is shorter), read again rather than indexed out of the registers
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const int tp = n - 3 + j;
+            conv_state_out[(size_t)j * ch + qk] = tp >= 0 ? qkv[(size_t)tp * ch + qk] : conv_state[(size_t)(3 + tp) * ch + qk];
+        }
+    }
+    if (vlane) {
+        float vw[kSmallT + 3];
+#pragma unroll
+        for (int j = 0; j < 3; j++) vw[j] = conv_state[(size_t)j * ch + vc];
+#pragma unroll
+        for (int t = 0; t < kSmallT; t++) vw[3 + t] = t < n ? qkv[(size_t)t * ch + vc] : 0.0f;
+        const float4 vwt = ((const float4 *)conv_w)[vc];
+#pragma unroll
+        for (int t = 0; t < kSmallT; t++) {
+            if (t >= n) break;
+            float acc = 0.0f;
+            acc += vwt.x * vw[t];
+            acc += vwt.y * vw[t + 1];
+            acc += vwt.z * vw[t + 2];
+            acc += vwt.w * vw[t + 3];
+            vs[t][tid] = acc * sigmoidf_(acc);
+        }
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const int tp = n - 3 + j;
+            conv_state_out[(size_t)j * ch + vc] = tp >= 0 ? qkv[(size_t)tp * ch + vc] : conv_state[(size_t)(3 + tp) * ch + vc];
+        }
+    }
+    // g = exp(a·softplus(alpha + dt_bias)), beta = sigmoid(beta_logit)
+    if (tid < n)
+        gb[tid] = make_float2(expf(a * softplusf_(gates[(size_t)tid * 2 * n_v_heads + h] + dt)),
+                              sigmoidf_(gates[(size_t)tid * 2 * n_v_heads + n_v_heads + h]));
+    __syncthreads();
+    {
+        const int half = tid >> 7;  // 0: q, 1: k
+#pragma unroll
+        for (int t = 0; t < kSmallT; t++) {
+            if (t >= n) break;
+            const float ss = red[t][2 * half] + red[t][2 * half + 1];
+            kqs[half ? 0 : 1][t][tid & (kD - 1)] = y[t] * (1.0f / sqrtf(ss + eps));
+        }
+    }
+    float s[kKeys];
+#pragma unroll
+    for (int i = 0; i < kKeys; i++) s[i] = tile[p * kKeys + i][c];
+    __syncthreads();
+
+    // ---- the token loop (k_delta_net's)
+    const float scale = 1.0f / sqrtf((float)kD);
+    for (int t = 0; t < n; t++) {
+        float kk[kKeys], qq[kKeys];
+#pragma unroll
+        for (int i = 0; i < kKeys; i++) {
+            kk[i] = kqs[0][t][p * kKeys + i];
+            qq[i] = kqs[1][t][p * kKeys + i];
+        }
+        const float2 g2 = gb[t];
+        const float g = g2.x, beta = g2.y;
+        float kv0 = 0.0f, kv1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kKeys; i += 2) {
+            s[i] *= g;
+            s[i + 1] *= g;
+            kv0 += s[i] * kk[i];
+            kv1 += s[i + 1] * kk[i + 1];
+        }
+        const float kv = sum16(kv0 + kv1);
+        const float ub = (vs[t][c] - kv) * beta;
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kKeys; i += 2) {
+            s[i] += kk[i] * ub;
+            s[i + 1] += kk[i + 1] * ub;
+            o0 += s[i] * qq[i];
+            o1 += s[i + 1] * qq[i + 1];
+        }
+        const float o = sum16(o0 + o1) * scale;
+        if (p == 0 && out) out[((size_t)t * n_v_heads + h) * kD + c0 + c] = o;
+    }
+
+    // ---- the state slice out, through LDS
+#pragma unroll
+    for (int i = 0; i < kKeys; i++) tile[p * kKeys + i][c] = s[i];
+    __syncthreads();
+    for (int e = tid; e < kD * kCols; e += kThreads) S[(e / kCols) * kD + c0 + e % kCols] = tile[e / kCols][e % kCols];
+}
+
 // ---- The chunked form, for batches of at least kC tokens -------------------
 //
 // Over a chunk of kC tokens with log decays lg_t and cumulative sums L_t (from
@@ -530,6 +685,19 @@ size_t delta_net_work_floats(size_t n, size_t n_v_heads) {
 hipError_t delta_net_reserve(dwim_dev *dev, size_t n, size_t n_v_heads) {
     return dev_grow(dev, (void **)&dev->dn_work, &dev->dn_work_cap, delta_net_work_floats(n, n_v_heads),
                     sizeof(float));
+}
+
+hipError_t launch_gdn_tokens(dwim_dev *dev, float *out, const float *qkv, const float *conv_state,
+                             float *conv_state_out, const float *conv_w, const float *gates, const float *decay,
+                             float *state, const float *state_in, size_t n, size_t n_k_heads, size_t n_v_heads,
+                             size_t head_dim, float eps) {
+    if (head_dim != kD || n < 1 || n > (size_t)kSmallT || n_k_heads == 0 || n_v_heads % n_k_heads)
+        return hipErrorInvalidValue;
+    dim3 grid(kD / kCols, (unsigned)n_v_heads);
+    k_gdn_tokens<<<grid, kThreads, 0, dev->stream>>>(out, qkv, conv_state, conv_state_out, conv_w, gates, decay, state,
+                                                     state_in ? state_in : state, (int)n, (int)n_k_heads,
+                                                     (int)n_v_heads, eps);
+    return hipGetLastError();
 }
 
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k, const float *v,

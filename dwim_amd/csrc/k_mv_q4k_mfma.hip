@@ -97,6 +97,33 @@ __global__ void __launch_bounds__(kPlanesThreads) k_planes(const float *__restri
     planes::write4x4(out, i, v, pair != 0);
 }
 
+// The planes of the DeltaNet layer's output gate, silu(z)·rmsnorm(att)·w per
+// head of 128 (gpu/cpu.rs:157-166, 238-242, as k_gated_norm computes it), in
+// pair mode, for the tokens of a batch (blockIdx.y): the gated norm made
+// where the output product's planes are made, one launch instead of two.  A
+// head is 32 lanes of float4s.
+__global__ void __launch_bounds__(kPlanesThreads) k_planes_gated(const float *__restrict__ z,
+                                                                 const float *__restrict__ att,
+                                                                 const float *__restrict__ w, float eps,
+                                                                 planes::View out) {
+    const unsigned n4 = (unsigned)(out.cols / 4);
+    z += (size_t)blockIdx.y * out.cols;
+    att += (size_t)blockIdx.y * out.cols;
+    if (blockIdx.y) out = planes::view(out.q + blockIdx.y * planes::kAreaBytes, out.cols);
+    const unsigned i = blockIdx.x * kPlanesThreads + threadIdx.x;
+    if (i >= n4) return;  // (cols / 4 is whole waves)
+    const float4 a = ((const float4 *)att)[i];
+    const float ss = group_sum<32>((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w));
+    const float scale = 1.0f / sqrtf(ss / 128.0f + eps);
+    const float4 nw = ((const float4 *)w)[i % 32];
+    float4 g = ((const float4 *)z)[i];
+    g.x = g.x * sigmoidf_(g.x) * (a.x * (scale * nw.x));
+    g.y = g.y * sigmoidf_(g.y) * (a.y * (scale * nw.y));
+    g.z = g.z * sigmoidf_(g.z) * (a.z * (scale * nw.z));
+    g.w = g.w * sigmoidf_(g.w) * (a.w * (scale * nw.w));
+    planes::write4x4(out, i, g, true);
+}
+
 constexpr int kMaxJobs = 4;
 constexpr int kMaxParts = 4;
 constexpr int kMaxTok = 4;     // tokens of a several-token launch (a verify batch: 1 + 3 drafts)
@@ -607,7 +634,7 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
 
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                                      int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
-                                     float *xn_out) {
+                                     float *xn_out, const float *gate_z) {
     if (count < 1 || count > kMaxJobs || (swiglu && count != 2) || n < 1) return hipErrorInvalidValue;
     const size_t cols = ws[0]->cols;
     if (cols > planes::kMaxCols || cols % 256) return hipErrorInvalidValue;
@@ -617,6 +644,7 @@ hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws
         rows[j] = ws[j]->rows;
     }
     if (swiglu && ws[0]->rows != ws[1]->rows) return hipErrorInvalidValue;
+    if (gate_z && (!norm || cols % 128)) return hipErrorInvalidValue;
     dev->prepared = 0;
     const unsigned njobs = swiglu ? 1 : (unsigned)count;
     const unsigned blocks = (unsigned)((cols / 4 + kPlanesThreads - 1) / kPlanesThreads);
@@ -624,9 +652,13 @@ hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws
     const size_t runs = (n + kMaxTok - 1) / kMaxTok;
     for (size_t r = 0, t0 = 0; r < runs; r++) {
         const size_t nt = (n - t0) / (runs - r);
-        k_planes<<<dim3(blocks, (unsigned)nt), kPlanesThreads, 0, dev->stream>>>(
-            x + t0 * cols, norm, eps, 0, norm && xn_out ? xn_out + t0 * cols : nullptr,
-            planes_area(dev, kBatchArea, cols), 1);
+        if (gate_z)
+            k_planes_gated<<<dim3(blocks, (unsigned)nt), kPlanesThreads, 0, dev->stream>>>(
+                gate_z + t0 * cols, x + t0 * cols, norm, eps, planes_area(dev, kBatchArea, cols));
+        else
+            k_planes<<<dim3(blocks, (unsigned)nt), kPlanesThreads, 0, dev->stream>>>(
+                x + t0 * cols, norm, eps, 0, norm && xn_out ? xn_out + t0 * cols : nullptr,
+                planes_area(dev, kBatchArea, cols), 1);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         if (nt == 1) {

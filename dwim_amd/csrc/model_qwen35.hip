@@ -441,19 +441,34 @@ struct dwim_model {
                     TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
                     TRY(dwim_matmul(dev, ab_in, l.ab, xh));
                 }
-                TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv_in, state, l.conv, c.state_dim, eps));
-                if (verify) {
-                    DWIM_HIP(launch_delta_net(dev, att->data, q->data, k->data, v->data, ab_in->data, l.decay->data,
-                                              ssm->data, n, c.k_heads, c.v_heads, c.state_dim, nullptr, true,
-                                              seq.ssm_state[l.slot]->data));
+                if (n <= 16 && c.state_dim == 128) {
+                    // conv, key norms and delta rule in one launch (verifying:
+                    // from the real state into the scratch)
+                    DWIM_HIP(launch_gdn_tokens(dev, att->data, qkv_in->data, state->data, state_out->data,
+                                               l.conv->data, ab_in->data, l.decay->data, ssm->data,
+                                               verify ? seq.ssm_state[l.slot]->data : nullptr, n, c.k_heads,
+                                               c.v_heads, c.state_dim, eps));
                 } else {
-                    TRY(dwim_delta_net_unit_keys(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads,
-                                                 c.state_dim));
+                    TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv_in, state, l.conv, c.state_dim, eps));
+                    if (verify) {
+                        DWIM_HIP(launch_delta_net(dev, att->data, q->data, k->data, v->data, ab_in->data,
+                                                  l.decay->data, ssm->data, n, c.k_heads, c.v_heads, c.state_dim,
+                                                  nullptr, true, seq.ssm_state[l.slot]->data));
+                    } else {
+                        TRY(dwim_delta_net_unit_keys(dev, att, q, k, v, ab, l.decay, ssm, c.k_heads, c.v_heads,
+                                                     c.state_dim));
+                    }
                 }
                 if (n >= 16 && l.out->fmt == DWIM_Q4_K) {
                     // the gated norm made in the out product's split
                     DWIM_HIP(gemm_prepare_gated(dev, z->data, att->data, l.norm->data, eps, n, v_dim(), c.state_dim));
                     DWIM_HIP(gemm_run(dev, l.out, x->data, n, kGemmAdd));
+                } else if (l.out->fmt == DWIM_Q4_K && c.state_dim == 128) {
+                    // the gated norm made with the out product's planes
+                    const int add = 1;
+                    float *o = x->data;
+                    DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, &l.out, &o, &add, 1, 0, att->data, n, l.norm->data, eps,
+                                                       nullptr, z->data));
                 } else {
                     DWIM_HIP(launch_gated_norm(dev, z->data, att->data, l.norm->data, n, v_dim(), c.state_dim, eps,
                                                -1));
@@ -722,6 +737,14 @@ struct dwim_model {
                     // saved inputs read where they lie
                     TRY(dwim_resize(dev, qkv_saved[l.slot], keep * (2 * k_dim() + v_dim())));
                     TRY(dwim_resize(dev, ab_saved[l.slot], keep * 2 * c.v_heads));
+                    if (keep <= 16 && c.state_dim == 128) {
+                        // conv, key norms and delta rule in one launch
+                        DWIM_HIP(launch_gdn_tokens(dev, nullptr, qkv_saved[l.slot]->data, state->data,
+                                                   state_out->data, l.conv->data, ab_saved[l.slot]->data,
+                                                   l.decay->data, seq.ssm_state[l.slot]->data, nullptr, keep,
+                                                   c.k_heads, c.v_heads, c.state_dim, c.eps));
+                        continue;
+                    }
                     TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv_saved[l.slot], state, l.conv, c.state_dim,
                                          c.eps));
                     TRY(dwim_delta_net_unit_keys(dev, att, q, k, v, ab_saved[l.slot], l.decay,

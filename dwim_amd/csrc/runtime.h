@@ -176,9 +176,11 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
 // read once (k_mv_q4k_stream.hip)
 hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds, int count,
                          int swiglu, size_t nt, const int8_t *const *xq, const float *const *xstat);
+// (gate_z given: the input is the DeltaNet output gate silu(gate_z)·
+// rmsnorm(x)·norm over heads of 128, made with the planes; xn_out unused)
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                                      int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
-                                     float *xn_out);
+                                     float *xn_out, const float *gate_z = nullptr);
 // The planes of nt <= 4 rows of x ([nt][cols]) in the batch areas, one launch;
 // views[t] is token t's (pair: per-32 scales)
 hipError_t launch_planes_batch(dwim_dev *dev, const float *x, size_t cols, size_t nt, int pair, planes::View *views);
@@ -208,6 +210,15 @@ struct Rms {
 // unit_keys (keys of unit length), 64 tokens and more take the chunked form;
 // with state_in (fewer tokens only), the state is read from there and the
 // updated one written to `state`
+// A batch of up to 16 tokens through a DeltaNet mixer's conv, l2 norms and
+// delta rule in one launch (k_delta_net.hip): qkv raw [n][2·nk·D + nv·D],
+// the conv state carried from conv_state to conv_state_out, the gate logits
+// [n][2·nv] final (no RMS scale), the state read from state_in (null: state)
+// and written to state, o to out [n][nv·D] (null: not written).
+hipError_t launch_gdn_tokens(dwim_dev *dev, float *out, const float *qkv, const float *conv_state,
+                             float *conv_state_out, const float *conv_w, const float *gates, const float *decay,
+                             float *state, const float *state_in, size_t n, size_t n_k_heads, size_t n_v_heads,
+                             size_t head_dim, float eps);
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k,
                             const float *v, const float *gates, const float *decay, float *state,
                             size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim, const Rms *rms = nullptr,
