@@ -4,14 +4,17 @@
 // the reference's Q8 (int8 with an f16 scale per block of 32) or f16 (each
 // kernel a template on the format, F16; an f16 key or value is read as is).
 //
-// Pass 1, one block per (chunk, key/value head, token): the G query heads
-// sharing the key/value head score the chunk's positions (a Q8 block of 32 per
-// lane, its f16 scale applied to the block's sum, the 8 lanes of a position
-// summed by shuffles), take the chunk's softmax numerator and weight the
-// chunk's values.  Every cache load of the block is issued before any
-// arithmetic.  It writes, per query head, the chunk's max, sum of
+// Pass 1, one block per (chunk, key/value head, token; or group of up to 4
+// tokens of a small batch, such as a speculative verify step): the G query
+// heads sharing the key/value head score the chunk's positions (a Q8 block of
+// 32 per lane, its f16 scale applied to the block's sum, the 8 lanes of a
+// position summed by shuffles), take the chunk's softmax numerator and weight
+// the chunk's values, for each of the block's tokens in turn over the keys
+// and values read once.  Every cache load of the block is issued before any
+// arithmetic.  It writes, per token and query head, the chunk's max, sum of
 // exponentials and weighted values.  Pass 2, one block per (query head,
-// token), merges the chunks.  Each cache byte is read once per token.
+// token), merges the chunks.  Each cache byte is read once per token (once
+// per 4 tokens of a small batch).
 //
 // A batch of 16 tokens or more (head_dim 256) runs flash attention on the
 // f16 matrix cores over a copy of the cache expanded to f16 hi + lo parts in
@@ -28,6 +31,12 @@ constexpr int kMaxD = 256;
 constexpr int kPos = 64;        // positions a partial block scores
 constexpr int kPThreads = 512;  // 8 lanes a position
 constexpr int kQPer = kMaxG * kMaxD / kPThreads;
+constexpr int kTok = 4;         // tokens a block of a several-token batch
+
+typedef _Float16 ahalf8 __attribute__((ext_vector_type(8)));
+typedef float afloat4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFD = 256, kFQ = 128, kFP = 32, kFThreads = 512;
 
 
 struct Shape {
@@ -46,7 +55,7 @@ DEV float half_of(uint32_t word, int hi) {
 }
 DEV uint32_t word_of(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
-template <int G, bool F16>
+template <int G, bool F16, int T>
 __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ partials, const float *__restrict__ q,
                                                             const int8_t *__restrict__ kq,
                                                             const uint16_t *__restrict__ ks,
@@ -54,35 +63,46 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
                                                             const uint16_t *__restrict__ vs, Shape sh) {
     // queries, each Q8 block of 32 padded to 36 floats: the 8 lanes of a
     // position, reading blocks 0..7 at once, then hit 8 different banks
-    __shared__ float q_s[kMaxG * kMaxD / 32 * 36];
-    __shared__ float p_s[kMaxG * kPos];
-    __shared__ float stat_s[kMaxG * 2];
-    const size_t chunk = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+    __shared__ float q_s[T * G * kMaxD / 32 * 36];
+    __shared__ float p_s[T * G * kPos];
+    __shared__ float stat_s[T * G * 2];
+    const size_t chunk = blockIdx.x, kvh = blockIdx.y, t0 = blockIdx.z * (size_t)T;
+    const int nt = (int)min((size_t)T, sh.n - t0);  // the block's tokens: t0 .. t0 + nt - 1
     const int D = (int)sh.head_dim;
     const size_t kv_dim = sh.n_kv_heads * sh.head_dim;
-    const size_t len = sh.pos + t + 1;  // the token attends up to its own position
     const size_t p0 = chunk * kPos;
     const size_t head0 = kvh * G;
-    float *part = partials + ((t * sh.n_heads + head0) * sh.chunks + chunk) * (size_t)(D + 2);
     const size_t part_stride = sh.chunks * (size_t)(D + 2);  // next head
-    if (p0 >= len) {
-        // a chunk past this token's last position: empty
-        if (threadIdx.x < (unsigned)G) {
-            part[threadIdx.x * part_stride + D] = -INFINITY;
-            part[threadIdx.x * part_stride + D + 1] = 0.0f;
+    // token t0 + tt attends up to its own position: cnt_of(tt) of the
+    // chunk's positions (0 past its last)
+    auto cnt_of = [&](int tt) -> int {
+        const size_t len = sh.pos + t0 + tt + 1;
+        return p0 >= len ? 0 : (int)min((size_t)kPos, len - p0);
+    };
+    auto part_of = [&](int tt) -> float * {
+        return partials + (((t0 + tt) * sh.n_heads + head0) * sh.chunks + chunk) * (size_t)(D + 2);
+    };
+    const int cnt = cnt_of(nt - 1);  // the last token's: the most
+    if (cnt == 0) {
+        // a chunk past every token's last position: empty
+        if (threadIdx.x < (unsigned)(nt * G)) {
+            float *part = part_of((int)threadIdx.x / G) + (threadIdx.x % G) * part_stride;
+            part[D] = -INFINITY;
+            part[D + 1] = 0.0f;
         }
         return;
     }
-    const int cnt = (int)min((size_t)kPos, len - p0);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // the queries first: in-order completion then lets the scores wait for
     // the queries and keys alone, and the values arrive meanwhile
-    float qr[kQPer];
+    float qr[T][kQPer];
 #pragma unroll
-    for (int k = 0; k < kQPer; k++) {
-        const size_t i = threadIdx.x + k * kPThreads;
-        qr[k] = i < (size_t)(G * D) ? q[(t * sh.n_heads + head0) * D + i] : 0.0f;
-    }
+    for (int tt = 0; tt < T; tt++)
+#pragma unroll
+        for (int k = 0; k < kQPer; k++) {
+            const size_t i = threadIdx.x + k * kPThreads;
+            qr[tt][k] = tt < nt && i < (size_t)(G * D) ? q[((t0 + tt) * sh.n_heads + head0) * D + i] : 0.0f;
+        }
     // key and value loads, unconditional (positions past the chunk's end read
     // its last position, masked later) and unconverted, so that every load is
     // in flight before the first wait
@@ -121,10 +141,12 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
         }
     }
     // (the query loads were issued first, so this waits for them alone)
-    for (int k = 0; k < kQPer; k++) {
-        const unsigned i = threadIdx.x + k * kPThreads;
-        if (i < (unsigned)(G * D)) q_s[(i / 32) * 36 + i % 32] = qr[k];
-    }
+#pragma unroll
+    for (int tt = 0; tt < T; tt++)
+        for (int k = 0; k < kQPer; k++) {
+            const unsigned i = threadIdx.x + k * kPThreads;
+            if (i < (unsigned)(G * D)) q_s[(tt * G * nblk + i / 32) * 36 + i % 32] = qr[tt][k];
+        }
     __syncthreads();
 
     const float scale = 1.0f / sqrtf((float)D);
@@ -140,95 +162,401 @@ __global__ void __launch_bounds__(kPThreads) k_attn_partial(float *__restrict__ 
                 kv[i] = (float)(int8_t)((w >> (8 * (i & 3))) & 0xff);
             }
         }
+        // every token's G heads against the keys read once
 #pragma unroll
-        for (int g = 0; g < G; g++) {
+        for (int r = 0; r < T * G; r++) {
+            if (T > 1 && r >= nt * G) continue;  // (uniform)
             float sc = 0.0f;
             if (klive) {
-                const float *qg = q_s + (g * nblk + b) * 36;
+                const float *qg = q_s + (r * nblk + b) * 36;
 #pragma unroll
                 for (int i = 0; i < 32; i++) sc += qg[i] * kv[i];
             }
             sc = group_sum<8>(sc * ksc);
-            if (b == 0 && kp < cnt) p_s[g * kPos + kp] = scale * sc;
+            if (b == 0 && kp < cnt) p_s[r * kPos + kp] = scale * sc;
         }
     }
     __syncthreads();
-    // softmax numerators: wave g takes head g, a lane per position
-    for (int g = wave; g < G; g += kPThreads / 64) {
-        const float sc = lane < cnt ? p_s[g * kPos + lane] : -INFINITY;
+    // softmax numerators: wave w takes rows (token, head) w, w + 8, ..., a
+    // lane per position
+    for (int r = wave; r < nt * G; r += kPThreads / 64) {
+        const int c = cnt_of(r / G);
+        const float sc = lane < c ? p_s[r * kPos + lane] : -INFINITY;
         const float m = group_max<64>(sc);
-        const float e = lane < cnt ? expf(sc - m) : 0.0f;
+        const float e = lane < c ? expf(sc - m) : 0.0f;
         const float l = group_sum<64>(e);
-        if (lane < cnt) p_s[g * kPos + lane] = e;
+        if (lane < cnt) p_s[r * kPos + lane] = e;  // (0 past the token's last position)
         if (lane == 0) {
-            stat_s[2 * g] = m;
-            stat_s[2 * g + 1] = l;
+            stat_s[2 * r] = c ? m : -INFINITY;
+            stat_s[2 * r + 1] = l;
         }
     }
     __syncthreads();
     if (vlive) {
-        float acc[G][4];
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[g][e] = 0.0f;
+        float vv[kPos / 8][4];
 #pragma unroll
         for (int i = 0; i < kPos / 8; i++) {
-            const int vp = (lane >> 3) + 8 * i;
-            float v0, v1, v2, v3;
             if constexpr (F16) {
-                v0 = half_of(vw[i][0], 0);
-                v1 = half_of(vw[i][0], 1);
-                v2 = half_of(vw[i][F16 ? 1 : 0], 0);
-                v3 = half_of(vw[i][F16 ? 1 : 0], 1);
+                vv[i][0] = half_of(vw[i][0], 0);
+                vv[i][1] = half_of(vw[i][0], 1);
+                vv[i][2] = half_of(vw[i][F16 ? 1 : 0], 0);
+                vv[i][3] = half_of(vw[i][F16 ? 1 : 0], 1);
             } else {
                 const uint32_t w = vw[i][0];
                 const float vsc = dq::from_f16(vbits[i]);
-                v0 = (float)(int8_t)(w & 0xff) * vsc;
-                v1 = (float)(int8_t)((w >> 8) & 0xff) * vsc;
-                v2 = (float)(int8_t)((w >> 16) & 0xff) * vsc;
-                v3 = (float)(int8_t)(w >> 24) * vsc;
-            }
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float pr = vp < cnt ? p_s[g * kPos + vp] : 0.0f;
-                acc[g][0] += pr * v0;
-                acc[g][1] += pr * v1;
-                acc[g][2] += pr * v2;
-                acc[g][3] += pr * v3;
+                vv[i][0] = (float)(int8_t)(w & 0xff) * vsc;
+                vv[i][1] = (float)(int8_t)((w >> 8) & 0xff) * vsc;
+                vv[i][2] = (float)(int8_t)((w >> 16) & 0xff) * vsc;
+                vv[i][3] = (float)(int8_t)(w >> 24) * vsc;
             }
         }
-        // the 8 position groups (lanes 8 apart) meet: lanes l, l ^ 8 by a
-        // row rotation, l ^ 16 and l ^ 32 by permlane swaps
+        for (int tt = 0; tt < nt; tt++) {
+            float acc[G][4];
 #pragma unroll
-        for (int g = 0; g < G; g++)
+            for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float v = acc[g][e];
-                v += xlane::mov<0x128>(v);
-                float x, y;
-                xlane::swap16(v, x, y);
-                v = x + y;
-                xlane::swap32(v, x, y);
-                acc[g][e] = x + y;
+                for (int e = 0; e < 4; e++) acc[g][e] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kPos / 8; i++) {
+                const int vp = (lane >> 3) + 8 * i;
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float pr = vp < cnt ? p_s[(tt * G + g) * kPos + vp] : 0.0f;
+                    acc[g][0] += pr * vv[i][0];
+                    acc[g][1] += pr * vv[i][1];
+                    acc[g][2] += pr * vv[i][2];
+                    acc[g][3] += pr * vv[i][3];
+                }
             }
-        // position group pg stores head pg's four values (a partial row is
-        // (D + 2) floats: 8-byte alignment only)
-        const int pg = lane >> 3;
-        float o[4] = {acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+            // the 8 position groups (lanes 8 apart) meet: lanes l, l ^ 8 by a
+            // row rotation, l ^ 16 and l ^ 32 by permlane swaps
 #pragma unroll
-        for (int g = 1; g < G; g++)
+            for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = pg == g ? acc[g][e] : o[e];
-        if (pg < G) {
-            float2 *dst = (float2 *)(part + pg * part_stride + 32 * wave + 4 * (lane & 7));
-            dst[0] = make_float2(o[0], o[1]);
-            dst[1] = make_float2(o[2], o[3]);
+                for (int e = 0; e < 4; e++) {
+                    float v = acc[g][e];
+                    v += xlane::mov<0x128>(v);
+                    float x, y;
+                    xlane::swap16(v, x, y);
+                    v = x + y;
+                    xlane::swap32(v, x, y);
+                    acc[g][e] = x + y;
+                }
+            // position group pg stores head pg's four values (a partial row
+            // is (D + 2) floats: 8-byte alignment only)
+            const int pg = lane >> 3;
+            float o[4] = {acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+#pragma unroll
+            for (int g = 1; g < G; g++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = pg == g ? acc[g][e] : o[e];
+            if (pg < G) {
+                float2 *dst = (float2 *)(part_of(tt) + pg * part_stride + 32 * wave + 4 * (lane & 7));
+                dst[0] = make_float2(o[0], o[1]);
+                dst[1] = make_float2(o[2], o[3]);
+            }
         }
     }
-    if (threadIdx.x < (unsigned)G) {
-        part[threadIdx.x * part_stride + D] = stat_s[2 * threadIdx.x];
-        part[threadIdx.x * part_stride + D + 1] = stat_s[2 * threadIdx.x + 1];
+    if (threadIdx.x < (unsigned)(nt * G)) {
+        float *part = part_of((int)threadIdx.x / G) + (threadIdx.x % G) * part_stride;
+        part[D] = stat_s[2 * threadIdx.x];
+        part[D + 1] = stat_s[2 * threadIdx.x + 1];
+    }
+}
+
+// ---------------------------------------------------------------- decode, matrix cores
+//
+// The same partial rows for head_dim 256 with the scores and the weighted
+// values on the f16 matrix cores (v_mfma_f32_16x16x32_f16).  A block of 4
+// waves takes a run of sh.ch positions (64 a step) of one key/value head and
+// its query rows, a row a (token, head) pair: the G heads of one token, or
+// of up to kTok tokens of a small batch, in RT tiles of 16 rows.
+//   * Scores, wave w the step's positions 16w..16w+15: for each Q8 block of
+//     32 dimensions, the queries' f16 hi and lo parts (staged in LDS once) as
+//     A against the keys as B, exact in f16 (int8, or the f16 cache as is),
+//     then times the block's per-position scale, in f32.
+//   * Softmax over the step, a running max and sum per row (flash style).
+//   * Values, wave w the dimensions 64w..64w+63: the probabilities times the
+//     values' per-position scale of the dimension's Q8 block, split into f16
+//     hi and lo parts, as A against the values as B (transposed into LDS,
+//     8 positions of one dimension a lane).
+// Every product is exact up to the hi/lo split (2^-22 relative) and summed
+// in f32.
+constexpr int kMStep = 64;       // positions a step
+constexpr int kMThreads = 256;
+constexpr int kQStride = 256 + 8;  // halfs a staged query row (bank spread)
+constexpr int kPStride = kMStep + 4;
+constexpr int kVStride = kMStep + 8;  // elements of a transposed value row
+
+// LDS of k_attn_mfma: queries hi and lo, probabilities, value scales, the
+// rows' max / sum / rescale, the transposed values
+constexpr size_t mfma_lds(int rt, bool f16) {
+    return (size_t)16 * rt * kQStride * 2 * 2 + (size_t)16 * rt * kPStride * 4 + (size_t)(kFD / 32) * kMStep * 4 +
+           (size_t)16 * rt * 3 * 4 + (size_t)kFD * kVStride * (f16 ? 2 : 1);
+}
+
+template <int RT, bool F16>
+__global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ partials, const float *__restrict__ q,
+                                                         const int8_t *__restrict__ kq,
+                                                         const uint16_t *__restrict__ ks,
+                                                         const int8_t *__restrict__ vq,
+                                                         const uint16_t *__restrict__ vs, Shape sh, int G, int T) {
+    constexpr int NR = 16 * RT;  // rows, padded
+    constexpr int D = kFD;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
+    _Float16 *q_hi = (_Float16 *)lds_raw, *q_lo = q_hi + NR * kQStride;
+    float *p_s = (float *)(q_lo + NR * kQStride);
+    float(*vsc_s)[kMStep] = (float(*)[kMStep])(p_s + NR * kPStride);
+    float *m_s = (float *)(vsc_s + D / 32), *l_s = m_s + NR, *a_s = l_s + NR;
+    uint8_t *vt_raw = (uint8_t *)(a_s + NR);
+    const size_t chunk = blockIdx.x, kvh = blockIdx.y, t0 = blockIdx.z * (size_t)T;
+    const int nt = (int)min((size_t)T, sh.n - t0), R = nt * G;
+    const size_t kv_dim = sh.n_kv_heads * D, head0 = kvh * G;
+    const size_t c0 = chunk * sh.ch;
+    const size_t len_last = sh.pos + t0 + nt;  // positions the group's last token sees
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, kq4 = lane >> 4;
+    auto part_of = [&](int r) -> float * {
+        return partials + (((t0 + r / G) * sh.n_heads + head0 + r % G) * sh.chunks + chunk) * (size_t)(D + 2);
+    };
+    if (c0 >= len_last) {
+        if (threadIdx.x < (unsigned)R) {
+            float *part = part_of((int)threadIdx.x);
+            part[D] = -INFINITY;
+            part[D + 1] = 0.0f;
+        }
+        return;
+    }
+    // the queries, hi and lo parts (rows past R zero)
+    for (int r = wave; r < NR; r += kMThreads / 64) {
+        float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < R) x = *(const float4 *)(q + ((t0 + r / G) * sh.n_heads + head0 + r % G) * D + 4 * lane);
+        const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const _Float16 h = (_Float16)xs[e];
+            q_hi[r * kQStride + 4 * lane + e] = h;
+            q_lo[r * kQStride + 4 * lane + e] = (_Float16)(xs[e] - (float)h);
+        }
+    }
+    if (threadIdx.x < (unsigned)NR) {
+        m_s[threadIdx.x] = -INFINITY;
+        l_s[threadIdx.x] = 0.0f;
+    }
+    afloat4 o[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) o[rt][j] = afloat4{0.0f, 0.0f, 0.0f, 0.0f};
+    const float scale = 1.0f / 16.0f;  // 1 / sqrt(256)
+    const int steps = (int)(sh.ch / kMStep);
+    // ---- loads: this wave's keys (position 16w + r16, 8 dimensions of each
+    // Q8 block) and their scales; a 4-dimension x 16-position patch of the
+    // values and (wave 0) the value scales.  A step's loads are issued while
+    // the previous step computes: the values' once they are in LDS, the
+    // keys' once the scores are taken.
+    // the value patch: Q8, dimensions 16·(t % 16).. of positions 4·(t / 16)..;
+    // f16, dimensions 8·(t % 32).. of positions 8·(t / 32)..
+    constexpr int VP = F16 ? 8 : 4;                                   // positions a thread
+    const int vd = F16 ? 8 * (threadIdx.x & 31) : 16 * (threadIdx.x & 15);
+    const int vp0 = F16 ? 8 * (threadIdx.x >> 5) : 4 * (threadIdx.x >> 4);
+    uint4 kf[F16 ? 8 : 4];  // Q8: two blocks a uint4
+    uint4 kscale = make_uint4(0, 0, 0, 0);
+    uint4 vw[VP];
+    uint4 vscale = make_uint4(0, 0, 0, 0);
+    auto load_keys = [&](size_t ps, int cnt) {
+        const size_t kpos = ps + min(16 * wave + r16, cnt - 1);
+        const size_t kbase = kpos * kv_dim + kvh * D + 8 * kq4;
+        if constexpr (F16) {
+#pragma unroll
+            for (int b = 0; b < 8; b++) kf[b] = *(const uint4 *)((const uint16_t *)kq + kbase + 32 * b);
+        } else {
+#pragma unroll
+            for (int b = 0; b < 8; b += 2) {
+                const uint2 x = *(const uint2 *)(kq + kbase + 32 * b), y = *(const uint2 *)(kq + kbase + 32 * (b + 1));
+                kf[b / 2] = make_uint4(x.x, x.y, y.x, y.y);
+            }
+            kscale = *(const uint4 *)(ks + kpos * (kv_dim / 32) + kvh * 8);
+        }
+    };
+    auto load_values = [&](size_t ps, int cnt) {
+#pragma unroll
+        for (int j = 0; j < VP; j++) {
+            const size_t off = (ps + min(vp0 + j, cnt - 1)) * kv_dim + kvh * D + vd;
+            vw[j] = F16 ? *(const uint4 *)((const uint16_t *)vq + off) : *(const uint4 *)(vq + off);
+        }
+        if (!F16 && threadIdx.x < kMStep)
+            vscale = *(const uint4 *)(vs + (ps + min((int)threadIdx.x, cnt - 1)) * (kv_dim / 32) + kvh * 8);
+    };
+    auto count = [&](size_t ps) { return (int)min((size_t)kMStep, len_last - ps); };
+    load_keys(c0, count(c0));
+    load_values(c0, count(c0));
+    for (int s = 0; s < steps; s++) {
+        const size_t ps = c0 + (size_t)s * kMStep;
+        if (ps >= len_last) break;
+        const size_t pn = ps + kMStep;  // the next step
+        const bool next = s + 1 < steps && pn < len_last;
+        __syncthreads();  // (the previous step is done with vt, p_s and vsc_s; the queries are staged)
+        // ---- the values, transposed: vt[d][position]
+        if constexpr (F16) {
+            uint16_t *vt = (uint16_t *)vt_raw;
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+#pragma unroll
+                for (int j = 0; j < VP; j += 2) {
+                    const uint32_t a = (word_of(vw[j], e / 2) >> (16 * (e % 2))) & 0xffffu;
+                    const uint32_t b = (word_of(vw[j + 1], e / 2) >> (16 * (e % 2))) & 0xffffu;
+                    *(uint32_t *)(vt + (vd + e) * kVStride + vp0 + j) = a | (b << 16);
+                }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int sh8 = 8 * (e % 4);
+                const uint32_t x = ((word_of(vw[0], e / 4) >> sh8) & 0xffu) |
+                                   (((word_of(vw[1], e / 4) >> sh8) & 0xffu) << 8) |
+                                   (((word_of(vw[2], e / 4) >> sh8) & 0xffu) << 16) |
+                                   (((word_of(vw[3], e / 4) >> sh8) & 0xffu) << 24);
+                *(uint32_t *)(vt_raw + (vd + e) * kVStride + vp0) = x;
+            }
+            if (threadIdx.x < kMStep) {
+                const uint32_t w4[4] = {vscale.x, vscale.y, vscale.z, vscale.w};
+#pragma unroll
+                for (int b = 0; b < 8; b++) vsc_s[b][threadIdx.x] = dq::from_f16((uint16_t)(w4[b / 2] >> (16 * (b % 2))));
+            }
+        }
+        if (next) load_values(pn, count(pn));
+        // ---- scores: rows 4·kq4 + e of each tile, position 16w + r16
+        {
+            afloat4 sc[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) sc[rt] = afloat4{0.0f, 0.0f, 0.0f, 0.0f};
+            const uint32_t ksw[4] = {kscale.x, kscale.y, kscale.z, kscale.w};
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                ahalf8 kb;
+                if constexpr (F16) {
+                    kb = __builtin_bit_cast(ahalf8, kf[b]);
+                } else {
+                    const uint4 &x = kf[b / 2];
+                    const uint32_t w0 = (b % 2) ? x.z : x.x, w1 = (b % 2) ? x.w : x.y;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        kb[i] = (_Float16)(int8_t)((w0 >> (8 * i)) & 0xffu);
+                        kb[4 + i] = (_Float16)(int8_t)((w1 >> (8 * i)) & 0xffu);
+                    }
+                }
+                const float kscl = F16 ? 1.0f : dq::from_f16((uint16_t)(ksw[b / 2] >> (16 * (b % 2))));
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) {
+                    const int qo = (rt * 16 + r16) * kQStride + 32 * b + 8 * kq4;
+                    const ahalf8 ah = *(const ahalf8 *)(q_hi + qo), al = *(const ahalf8 *)(q_lo + qo);
+                    afloat4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, kb, afloat4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, kb, c, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) sc[rt][e] += c[e] * kscl;
+                }
+                // (a block at a time: the scheduler would otherwise hoist every
+                // block's query reads, and their registers cost a block a CU)
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const int p = 16 * wave + r16;
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int r = rt * 16 + 4 * kq4 + e;
+                    // row r's token sees positions up to sh.pos + t0 + r / G
+                    const bool live = r < R && ps + p <= sh.pos + t0 + r / G;
+                    p_s[r * kPStride + p] = live ? sc[rt][e] * scale : -INFINITY;
+                }
+        }
+        if (next) load_keys(pn, count(pn));
+        __syncthreads();
+        // ---- softmax numerators with a running max and sum: wave w takes
+        // rows w, w + 4, ..., a lane per position
+        for (int r = wave; r < NR; r += kMThreads / 64) {
+            const float x = p_s[r * kPStride + lane];
+            const float mo = m_s[r];
+            const float mn = fmaxf(mo, group_max<64>(x));
+            const float e = mn == -INFINITY ? 0.0f : expf(x - mn);
+            const float l = group_sum<64>(e);
+            p_s[r * kPStride + lane] = e;
+            if (lane == 0) {
+                const float a = mn == -INFINITY ? 1.0f : expf(mo - mn);
+                a_s[r] = a;
+                m_s[r] = mn;
+                l_s[r] = l_s[r] * a + l;
+            }
+        }
+        __syncthreads();
+        // ---- values: dimensions 64w + 16j + r16 (j < 4: Q8 blocks 2w, 2w + 1)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            float a[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) a[e] = a_s[rt * 16 + 4 * kq4 + e];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[rt][j][e] *= a[e];
+        }
+#pragma unroll
+        for (int k2 = 0; k2 < 2; k2++) {
+            const int pp = 32 * k2 + 8 * kq4;  // this lane's 8 positions
+            ahalf8 vb[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = 64 * wave + 16 * j + r16;
+                if constexpr (F16) {
+                    vb[j] = *(const ahalf8 *)((const uint16_t *)vt_raw + d * kVStride + pp);
+                } else {
+                    const uint2 x = *(const uint2 *)(vt_raw + d * kVStride + pp);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        vb[j][i] = (_Float16)(int8_t)((x.x >> (8 * i)) & 0xffu);
+                        vb[j][4 + i] = (_Float16)(int8_t)((x.y >> (8 * i)) & 0xffu);
+                    }
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                const float4 pa = *(const float4 *)(p_s + (rt * 16 + r16) * kPStride + pp);
+                const float4 pb = *(const float4 *)(p_s + (rt * 16 + r16) * kPStride + pp + 4);
+                const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+                for (int h = 0; h < 2; h++) {  // Q8 block 2w + h: tiles j = 2h, 2h + 1
+                    ahalf8 ph, pl;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const float x = F16 ? pr[i] : pr[i] * vsc_s[2 * wave + h][pp + i];
+                        const _Float16 hh = (_Float16)x;
+                        ph[i] = hh;
+                        pl[i] = (_Float16)(x - (float)hh);
+                    }
+#pragma unroll
+                    for (int jj = 0; jj < 2; jj++) {
+                        const int j = 2 * h + jj;
+                        o[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb[j], o[rt][j], 0, 0, 0);
+                        o[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb[j], o[rt][j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // ---- the partial rows: row 4·kq4 + e of tile rt, dimension 64w + 16j + r16
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int r = rt * 16 + 4 * kq4 + e;
+            if (r >= R) continue;
+            float *part = part_of(r);
+#pragma unroll
+            for (int j = 0; j < 4; j++) part[64 * wave + 16 * j + r16] = o[rt][j][e];
+        }
+    if (threadIdx.x < (unsigned)R) {
+        float *part = part_of((int)threadIdx.x);
+        part[D] = m_s[threadIdx.x];
+        part[D + 1] = l_s[threadIdx.x];
     }
 }
 
@@ -335,10 +663,6 @@ __global__ void __launch_bounds__(kCThreads) k_attn_combine(float *__restrict__ 
 
 // ---------------------------------------------------------------- prefill
 
-typedef _Float16 ahalf8 __attribute__((ext_vector_type(8)));
-typedef float afloat4 __attribute__((ext_vector_type(4)));
-
-constexpr int kFD = 256, kFQ = 128, kFP = 32, kFThreads = 512;
 
 DEV ahalf8 hi8(const float *v) {
     ahalf8 h;
@@ -614,6 +938,24 @@ hipError_t attention_reserve(dwim_dev *dev, size_t floats) {
 
 namespace {
 
+constexpr size_t kMBlocks = 512;  // blocks the matrix-core pass aims for
+// one token over at most this many positions: the one-chunk VALU pass, whose
+// single round of blocks has less latency (4k positions: 14.0 against 15.0
+// us with the merge; 32k: 47.8 against 38.1)
+constexpr size_t kValuLen = 6144;
+
+template <int RT, bool F16>
+hipError_t mfma_pass(dwim_dev *dev, dim3 grid, float *partials, const float *q, const dwim_cache *k,
+                     const dwim_cache *v, const Shape &sh, int G, int T) {
+    constexpr size_t lds = mfma_lds(RT, F16);
+    // once a process (thread-safe: a function-local static)
+    static const hipError_t raised =
+        hipFuncSetAttribute((const void *)k_attn_mfma<RT, F16>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (raised != hipSuccess) return raised;
+    k_attn_mfma<RT, F16><<<grid, kMThreads, lds, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh, G, T);
+    return hipGetLastError();
+}
+
 // Both entry points' launches: the batch path on the matrix cores (no
 // scratch), or the chunked decode path with its partial results in
 // `partials` (at least attention_partials_floats).
@@ -643,18 +985,45 @@ hipError_t attention_run(dwim_dev *dev, float *partials, float *out, const float
         k_attn_flash<<<tiles * (unsigned)n_heads, kFThreads, kFlashLds, dev->stream>>>(fa);
         return hipGetLastError();
     }
-    const size_t len = pos + n, ch = kPos, chunks = (len + ch - 1) / ch;
+    const size_t len = pos + n;
+    if (head_dim == (size_t)kFD && (n > 1 || len > kValuLen)) {
+        // the matrix-core pass: a run of 64-position steps a block, as many
+        // as leave about two blocks a CU
+        const int G = (int)(n_heads / n_kv_heads), T = n > 1 ? kTok : 1;
+        const size_t groups = (n + T - 1) / T, base = (len + kMStep - 1) / kMStep * n_kv_heads * groups;
+        const size_t ch = kMStep * std::max<size_t>(1, base / kMBlocks), chunks = (len + ch - 1) / ch;
+        Shape sh{n, pos, n_heads, head_dim, n_kv_heads, ch, chunks};
+        dim3 g1((unsigned)chunks, (unsigned)n_kv_heads, (unsigned)groups);
+        hipError_t e = T * G <= 16 ? (k->f16 ? mfma_pass<1, true>(dev, g1, partials, q, k, v, sh, G, T)
+                                             : mfma_pass<1, false>(dev, g1, partials, q, k, v, sh, G, T))
+                                   : (k->f16 ? mfma_pass<2, true>(dev, g1, partials, q, k, v, sh, G, T)
+                                             : mfma_pass<2, false>(dev, g1, partials, q, k, v, sh, G, T));
+        if (e != hipSuccess) return e;
+        dim3 g2((unsigned)n_heads * (unsigned)(head_dim / 64), (unsigned)n);
+        k_attn_combine<<<g2, kCThreads, 0, dev->stream>>>(out, partials, sh, gate, pv);
+        return hipGetLastError();
+    }
+    const size_t ch = kPos, chunks = (len + ch - 1) / ch;
     Shape sh{n, pos, n_heads, head_dim, n_kv_heads, ch, chunks};
-    dim3 g1((unsigned)chunks, (unsigned)n_kv_heads, (unsigned)n);
+    // one token a block, or a few tokens' queries against the chunk read once
+    const bool grouped = n > 1;
+    dim3 g1((unsigned)chunks, (unsigned)n_kv_heads, (unsigned)(grouped ? (n + kTok - 1) / kTok : n));
     switch (n_heads / n_kv_heads) {
+#define DWIM_PARTIAL_T(G, T)                                                                                    \
+    if (k->f16) k_attn_partial<G, true, T><<<g1, kPThreads, 0, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh); \
+    else k_attn_partial<G, false, T><<<g1, kPThreads, 0, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh);
 #define DWIM_PARTIAL(G)                                                                                        \
     case G:                                                                                                    \
-        if (k->f16) k_attn_partial<G, true><<<g1, kPThreads, 0, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh); \
-        else k_attn_partial<G, false><<<g1, kPThreads, 0, dev->stream>>>(partials, q, k->q, k->s, v->q, v->s, sh);      \
+        if (grouped) {                                                                                         \
+            DWIM_PARTIAL_T(G, kTok)                                                                            \
+        } else {                                                                                               \
+            DWIM_PARTIAL_T(G, 1)                                                                               \
+        }                                                                                                      \
         break;
         DWIM_PARTIAL(1) DWIM_PARTIAL(2) DWIM_PARTIAL(3) DWIM_PARTIAL(4) DWIM_PARTIAL(5) DWIM_PARTIAL(6)
         DWIM_PARTIAL(7) DWIM_PARTIAL(8)
 #undef DWIM_PARTIAL
+#undef DWIM_PARTIAL_T
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

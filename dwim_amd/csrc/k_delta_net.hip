@@ -217,6 +217,7 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
     float y[kSmallT];
 #pragma unroll
     for (int t = 0; t < kSmallT; t++) {
+        if (t >= n) break;  // (uniform: the batch's tokens only)
         float acc = 0.0f;
         acc += w.x * win[t];
         acc += w.y * win[t + 1];

@@ -72,6 +72,30 @@ def test_attention_decode_at_depth_for_two_sessions(depth, f16):
 
 
 @pytest.mark.parametrize("f16", [False, True], ids=["q8", "f16"])
+@pytest.mark.parametrize("n", [2, 4, 7, 15])
+def test_attention_small_batch_at_depth(n, f16):
+    """A verify step's batch (config 5: 4 tokens at 32k): a partial block
+    takes up to 4 tokens against the chunk read once; the last chunk holds
+    positions of only some of them."""
+    heads, hd, kvh = 24, 256, 4
+    kv_dim = kvh * hd
+    gpu = D.Hip(0)
+    for pos in (61, 32766 - n):
+        rng = O.Rng(77 * n + pos)
+        q = rng.floats(n * heads * hd)
+        kd = rng.floats((pos + n) * kv_dim)
+        vd = rng.floats((pos + n) * kv_dim)
+        kc, vc, (ok, ov) = _caches(gpu, kd, vd, f16)
+        want = _oracle_attention(f16, q, ok, ov, pos, heads, hd, kvh)
+        out = gpu.alloc(q.size)
+        gpu.attention(out, gpu.buffer(q), kc, vc, pos, heads, hd, kvh)
+        e = _err(gpu.read(out), want)
+        print(f"n {n} pos {pos} {'f16' if f16 else 'q8'}: max err {e:.2e}", flush=True)
+        assert e <= 1e-4
+    gpu.close()
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["q8", "f16"])
 def test_attention_prefill_of_2048_tokens(f16):
     heads, hd, kvh, n = 24, 256, 4, 2048
     kv_dim = kvh * hd

@@ -386,6 +386,8 @@ ATTENTION_CASES = [
     (3, 96, 1, 2, 9, 1.0), (2, 128, 1, 1, 0, 1e-3), (24, 256, 4, 3, 1000, 1e-3), (32, 128, 4, 64, 32704, 1.0),
     (24, 256, 4, 64, 470, 1.0), (24, 256, 4, 700, 470, 1.0), (24, 256, 4, 1, 5000, 1.0),
     (24, 256, 4, 1, 40000, 1.0), (16, 128, 8, 1, 3000, 1.0),
+    # small batches: a block takes up to 4 tokens (some past a chunk's start, some not)
+    (24, 256, 4, 4, 62, 1.0), (24, 256, 4, 9, 60, 1.0), (8, 64, 2, 5, 0, 1.0), (16, 128, 8, 15, 3001, 1.0),
     # batches through the prefill kernel (head_dim 256, 16 tokens or more)
     (24, 256, 4, 33, 0, 1e-3), (4, 256, 1, 100, 5, 1.0), (24, 256, 4, 300, 1500, 1.0), (8, 256, 8, 16, 31, 1.0),
 ]
