@@ -184,7 +184,7 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
                                                          const float *__restrict__ gates,
                                                          const float *__restrict__ decay, float *state,
                                                          const float *state_in, int n, int n_k_heads, int n_v_heads,
-                                                         float eps) {
+                                                         float eps, GdnSteps steps) {
     __shared__ float kqs[2][kSmallT][kD];          // normalized k, q of each token
     __shared__ float tile[kD][kCols + 1];          // the state slice's staging
     __shared__ float vs[kSmallT][kCols];
@@ -227,14 +227,20 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
         const float sq = group_sum<64>(y[t] * y[t]);
         if ((tid & 63) == 0 && t < n) red[t][tid >> 6] = sq;
     }
-    if (blockIdx.x == 0 && h % ratio == 0) {
-        // the last three inputs carry over (the state's rows when the batch
-        // is shorter), read again rather than indexed out of the registers
+    // the last three inputs carry over (the state's rows when the batch is
+    // shorter), read again rather than indexed out of the registers; with
+    // steps, also after each earlier token t (the conv state of t + 1 kept)
+    auto carry = [&](float *dst, size_t idx, int upto) {
 #pragma unroll
         for (int j = 0; j < 3; j++) {
-            const int tp = n - 3 + j;
-            conv_state_out[(size_t)j * ch + qk] = tp >= 0 ? qkv[(size_t)tp * ch + qk] : conv_state[(size_t)(3 + tp) * ch + qk];
+            const int tp = upto - 3 + j;
+            dst[(size_t)j * ch + idx] = tp >= 0 ? qkv[(size_t)tp * ch + idx] : conv_state[(size_t)(3 + tp) * ch + idx];
         }
+    };
+    if (blockIdx.x == 0 && h % ratio == 0) {
+        carry(conv_state_out, qk, n);
+        for (int t = 0; t + 1 < n && t < kMaxSteps; t++)
+            if (steps.conv[t]) carry(steps.conv[t], qk, t + 1);
     }
     if (vlane) {
         float vw[kSmallT + 3];
@@ -253,11 +259,9 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
             acc += vwt.w * vw[t + 3];
             vs[t][tid] = acc * sigmoidf_(acc);
         }
-#pragma unroll
-        for (int j = 0; j < 3; j++) {
-            const int tp = n - 3 + j;
-            conv_state_out[(size_t)j * ch + vc] = tp >= 0 ? qkv[(size_t)tp * ch + vc] : conv_state[(size_t)(3 + tp) * ch + vc];
-        }
+        carry(conv_state_out, vc, n);
+        for (int t = 0; t + 1 < n && t < kMaxSteps; t++)
+            if (steps.conv[t]) carry(steps.conv[t], vc, t + 1);
     }
     // g = exp(a·softplus(alpha + dt_bias)), beta = sigmoid(beta_logit)
     if (tid < n)
@@ -309,6 +313,12 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
         }
         const float o = sum16(o0 + o1) * scale;
         if (p == 0 && out) out[((size_t)t * n_v_heads + h) * kD + c0 + c] = o;
+        if (t + 1 < n && t < kMaxSteps && steps.state[t]) {
+            // the state after token t, for a rewind that keeps t + 1 tokens
+            float *St = steps.state[t] + (size_t)h * kD * kD;
+#pragma unroll
+            for (int i = 0; i < kKeys; i++) St[(size_t)(p * kKeys + i) * kD + c0 + c] = s[i];
+        }
     }
 
     // ---- the state slice out, through LDS
@@ -691,13 +701,13 @@ hipError_t delta_net_reserve(dwim_dev *dev, size_t n, size_t n_v_heads) {
 hipError_t launch_gdn_tokens(dwim_dev *dev, float *out, const float *qkv, const float *conv_state,
                              float *conv_state_out, const float *conv_w, const float *gates, const float *decay,
                              float *state, const float *state_in, size_t n, size_t n_k_heads, size_t n_v_heads,
-                             size_t head_dim, float eps) {
+                             size_t head_dim, float eps, const GdnSteps *steps) {
     if (head_dim != kD || n < 1 || n > (size_t)kSmallT || n_k_heads == 0 || n_v_heads % n_k_heads)
         return hipErrorInvalidValue;
     dim3 grid(kD / kCols, (unsigned)n_v_heads);
     k_gdn_tokens<<<grid, kThreads, 0, dev->stream>>>(out, qkv, conv_state, conv_state_out, conv_w, gates, decay, state,
                                                      state_in ? state_in : state, (int)n, (int)n_k_heads,
-                                                     (int)n_v_heads, eps);
+                                                     (int)n_v_heads, eps, steps ? *steps : GdnSteps{});
     return hipGetLastError();
 }
 

@@ -107,6 +107,9 @@ struct dwim_model {
     // verifying: the linear layers' states run through the batch, and their
     // inputs, apart from the real ones (with a drafter only)
     std::vector<dwim_buf *> ssm_scratch, qkv_saved, ab_saved;
+    // verifying in one launch a layer: the states after each of the batch's
+    // first tokens (step t: after token t), which a rewind takes as they are
+    std::vector<dwim_buf *> ssm_step[kMaxSteps], conv_step[kMaxSteps];
     // the mark: linear layers' states and the carried hidden state
     std::vector<dwim_buf *> mark_conv, mark_ssm;
     dwim_buf *mark_hidden = nullptr;
@@ -241,6 +244,15 @@ struct dwim_model {
     // fused kernels take.  One token goes through the int8 matrix cores, the
     // activations of each product handed over as planes (plane area 0);
     // several tokens through the f32 matrix kernels.
+    // a verified batch of n whose linear layers all ran in one launch each,
+    // keeping the states after its first tokens
+    bool steps_kept(size_t n) const {
+        if (!has_draft || n < 2 || n - 1 > (size_t)kMaxSteps || n > 16 || c.state_dim != 128) return false;
+        for (const Layer &l : layers)
+            if (!l.attention && !fusable(l)) return false;
+        return true;
+    }
+
     bool fusable(const Layer &l) const {
         const bool shapes = c.hidden % 256 == 0 && c.hidden <= 10240 && c.intermediate % 256 == 0 &&
                             c.intermediate <= 80 * 256 && (c.state_dim == 128 || c.state_dim == 256) &&
@@ -443,11 +455,18 @@ struct dwim_model {
                 }
                 if (n <= 16 && c.state_dim == 128) {
                     // conv, key norms and delta rule in one launch (verifying:
-                    // from the real state into the scratch)
+                    // from the real state into the scratch, the states after
+                    // the first tokens kept for a rewind)
+                    GdnSteps st{};
+                    if (verify && steps_kept(n))
+                        for (size_t t = 0; t + 1 < n; t++) {
+                            st.state[t] = ssm_step[t][l.slot]->data;
+                            st.conv[t] = conv_step[t][l.slot]->data;
+                        }
                     DWIM_HIP(launch_gdn_tokens(dev, att->data, qkv_in->data, state->data, state_out->data,
                                                l.conv->data, ab_in->data, l.decay->data, ssm->data,
                                                verify ? seq.ssm_state[l.slot]->data : nullptr, n, c.k_heads,
-                                               c.v_heads, c.state_dim, eps));
+                                               c.v_heads, c.state_dim, eps, &st));
                 } else {
                     TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv_in, state, l.conv, c.state_dim, eps));
                     if (verify) {
@@ -721,6 +740,16 @@ struct dwim_model {
         seq.verified.clear();
         if (keep == n) {
             for (size_t slot = 0; slot < slots; slot++) std::swap(seq.ssm_state[slot], ssm_scratch[slot]);
+        } else if (steps_kept(n)) {
+            // the states after token keep - 1, as the batch left them (the
+            // same arithmetic as running the kept tokens again)
+            for (const Layer &l : layers) {
+                if (l.attention) continue;
+                auto &pair = seq.conv_state[l.slot];
+                dwim_buf *&conv_out = seq.parity ? pair[1] : pair[0];
+                std::swap(seq.ssm_state[l.slot], ssm_step[keep - 1][l.slot]);
+                std::swap(conv_out, conv_step[keep - 1][l.slot]);
+            }
         } else {
             TRY(batch(keep));
             TRY(dwim_resize(dev, q, keep * k_dim()));
@@ -1069,6 +1098,13 @@ extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg
             m->ssm_scratch.push_back(sc);
             m->qkv_saved.push_back(qs);
             m->ab_saved.push_back(as);
+            if (c.state_dim == 128)
+                for (int t = 0; t < kMaxSteps; t++) {
+                    dwim_buf *ss, *cs;
+                    if (m->buf(m->ssm_width(), &ss) || m->buf(m->conv_width(), &cs)) return 1;
+                    m->ssm_step[t].push_back(ss);
+                    m->conv_step[t].push_back(cs);
+                }
         }
     }
     if (m->buf(c.hidden, &m->mark_hidden)) return 1;

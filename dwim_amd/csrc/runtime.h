@@ -215,10 +215,18 @@ struct Rms {
 // the conv state carried from conv_state to conv_state_out, the gate logits
 // [n][2·nv] final (no RMS scale), the state read from state_in (null: state)
 // and written to state, o to out [n][nv·D] (null: not written).
+// Where k_gdn_tokens also writes the recurrent state and the conv state
+// after each token t < min(n - 1, kMaxSteps) (null: not kept), so that a
+// rewind keeping t + 1 tokens of a verified batch takes them as they are.
+constexpr int kMaxSteps = 8;
+struct GdnSteps {
+    float *state[kMaxSteps];
+    float *conv[kMaxSteps];
+};
 hipError_t launch_gdn_tokens(dwim_dev *dev, float *out, const float *qkv, const float *conv_state,
                              float *conv_state_out, const float *conv_w, const float *gates, const float *decay,
                              float *state, const float *state_in, size_t n, size_t n_k_heads, size_t n_v_heads,
-                             size_t head_dim, float eps);
+                             size_t head_dim, float eps, const GdnSteps *steps = nullptr);
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k,
                             const float *v, const float *gates, const float *decay, float *state,
                             size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim, const Rms *rms = nullptr,
