@@ -237,6 +237,8 @@ def mtp_leg(dev, D, M, prompt_len=32768, sessions=2, tokens=64, k=3):
     batch: the batch matvecs run on the int8 matrix cores), timed, and from
     the same state (mark / rewind_to_mark) `tokens` tokens of plain greedy
     decoding, timed; the two sequences must be equal (qwen35/mod.rs:2100-2149).
+    A step's draft and its verify + rewind are timed apart (the device
+    synchronized after the rewind), against a plain token.
     The loop is the reference's Local::step with a greedy sampler
     (inference/local.rs:320-368)."""
     cfg = M.config_27b(drafter=True)
@@ -244,7 +246,7 @@ def mtp_leg(dev, D, M, prompt_len=32768, sessions=2, tokens=64, k=3):
     rng = np.random.default_rng(55)
     seqs = [0] + [model.add_sequence() for _ in range(sessions - 1)]
     out = {"sessions": sessions, "prompt": prompt_len, "tokens": tokens, "drafts_per_step": k}
-    prefill_s = spec_s = plain_s = 0.0
+    prefill_s = spec_s = plain_s = draft_s = verify_s = 0.0
     accepted = drafted = steps = 0
     match = True
     for seq in seqs:
@@ -261,7 +263,10 @@ def mtp_leg(dev, D, M, prompt_len=32768, sessions=2, tokens=64, k=3):
         spec, token, pos = [], first, prompt_len
         while len(spec) < tokens:
             spec.append(token)
-            drafts = model.draft(token, pos, k)
+            t1 = time.perf_counter()
+            drafts = model.draft(token, pos, k)  # (returns the drafts: synchronous)
+            t2 = time.perf_counter()
+            draft_s += t2 - t1
             steps += 1
             if not drafts:
                 token = model.forward_greedy([token], pos)
@@ -277,6 +282,8 @@ def mtp_leg(dev, D, M, prompt_len=32768, sessions=2, tokens=64, k=3):
                 keep += 1
                 accepted += 1
             model.rewind(keep)
+            dev.sync()
+            verify_s += time.perf_counter() - t2
             pos += keep
             token = picks[keep - 1]
         dev.sync()
@@ -296,6 +303,9 @@ def mtp_leg(dev, D, M, prompt_len=32768, sessions=2, tokens=64, k=3):
     out.update({"prefill_tok_s": sessions * prompt_len / prefill_s,
                 "speculative_tok_s": sessions * tokens / spec_s, "plain_tok_s": sessions * tokens / plain_s,
                 "verify_steps": steps, "drafted": drafted, "accepted": accepted,
+                "draft_ms": draft_s / steps * 1e3, "verify_rewind_ms": verify_s / steps * 1e3,
+                "plain_token_ms": plain_s / (sessions * tokens) * 1e3,
+                "verify_over_plain": (verify_s / steps) / (plain_s / (sessions * tokens)),
                 "acceptance": accepted / drafted if drafted else 0.0,
                 "speculative_equals_greedy": bool(match),
                 "note": "random-init drafter: acceptance near zero, so each step yields about one token"})

@@ -3,6 +3,7 @@
     python -m dwim_amd.kernel_workloads attention [--reps N]
     python -m dwim_amd.kernel_workloads tokens [--reps N]
     python -m dwim_amd.kernel_workloads stream [--reps N]
+    python -m dwim_amd.kernel_workloads verify [--reps N]
 
 `attention`: first a device copy of 256 MiB (four times), the calibration
 of the FETCH_SIZE / WRITE_SIZE counters; then one-token GQA decode (24 query heads, 4 key/value heads of 256,
@@ -14,6 +15,12 @@ same over f16 caches.  Every call goes through the C ABI (dwim_attention).
 `tokens`: the 4-token Q4_K product (a speculative-decoding verify batch,
 k_planes then k_mv_stream<4>) on the 27B shape's 17408x5120 and 5120x17408
 matrices (synthetic weights), `reps` calls each, through dwim_matmul.
+
+`verify`: config 5's verify step.  The 27B-shape model with its MTP drafter
+(random-init, Q4_K body, Q6_K head) prefilled with a 32768-token uniform
+prompt, then `reps` verify steps of 4 tokens at position 32768, each
+rewound to its first token and the model back to its mark (dwim_model_verify,
+dwim_model_rewind, dwim_model_rewind_to_mark).
 
 `stream`: the HBM streaming floor the decode products are measured against.
 A read and nothing else (dwim_measure_stream, 16 bytes a lane, eight loads
@@ -98,12 +105,33 @@ def stream(reps: int) -> None:
     dev.close()
 
 
+def verify(reps: int) -> None:
+    import numpy as np
+
+    from . import model as M
+    dev = D.Hip(0)
+    prompt_len = 32768
+    cfg = M.config_27b(drafter=True)
+    model = M.Model(dev, cfg, seed=4321, body_format=D.Q4_K, head_format=D.Q6_K, max_len=prompt_len + 64)
+    prompt = np.random.default_rng(55).integers(0, cfg.vocab, prompt_len).astype(np.uint32)
+    token = model.forward_greedy(prompt, 0)
+    model.mark()
+    for _ in range(reps):
+        model.verify([token, 1, 2, 3], prompt_len, want_logits=False)
+        model.rewind(1)
+        model.rewind_to_mark()
+    dev.sync()
+    print(f"verify: {reps} steps of 4 tokens at {prompt_len}", flush=True)
+    model.close()
+    dev.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=["attention", "tokens", "stream"])
+    ap.add_argument("workload", choices=["attention", "tokens", "stream", "verify"])
     ap.add_argument("--reps", type=int, default=20)
     a = ap.parse_args()
-    {"attention": attention, "tokens": tokens, "stream": stream}[a.workload](a.reps)
+    {"attention": attention, "tokens": tokens, "stream": stream, "verify": verify}[a.workload](a.reps)
 
 
 if __name__ == "__main__":
