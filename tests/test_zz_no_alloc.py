@@ -1,8 +1,9 @@
 """dwim_attention_noalloc (no counterpart in the reference: dwim_attention for
 callers that cannot allocate) against dwim_attention through the C ABI: the
 same bits, on two calls in a row, the second smaller than the first, then a
-batch on the matrix-core path; and a call past its fixed scratch array is
-refused with a clear error."""
+batch on the matrix-core path and decode calls on the matrix-core decode
+pass; and a call past its fixed scratch array is refused with a clear
+error."""
 import numpy as np
 import pytest
 
@@ -22,8 +23,11 @@ def _case(gpu, rng, n, pos, heads, kvh, hd):
 def test_noalloc_attention_equals_attention():
     gpu = D.Hip(0)
     rng = np.random.default_rng(7)
+    # one token over the VALU pass; a few tokens over it (head_dim 128); a
+    # batch through the flash kernel; one token and a verify-sized group past
+    # 6144 positions through the decode pass on the matrix cores
     for n, pos, heads, kvh, hd in ((1, 4095, 24, 4, 256), (3, 100, 4, 2, 128), (20, 70, 24, 4, 256),
-                                   (1, 5, 6, 6, 64)):
+                                   (1, 5, 6, 6, 64), (1, 9000, 24, 4, 256), (4, 20000, 24, 4, 256)):
         print(f"noalloc case n={n} pos={pos} heads={heads}/{kvh} hd={hd}", flush=True)
         kc, vc, q = _case(gpu, rng, n, pos, heads, kvh, hd)
         want, got = gpu.alloc(n * heads * hd), gpu.alloc(n * heads * hd)
