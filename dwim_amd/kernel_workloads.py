@@ -9,8 +9,9 @@
 of the FETCH_SIZE / WRITE_SIZE counters; then one-token GQA decode (24 query heads, 4 key/value heads of 256,
 the 27B shape's attention layer) over Q8 caches filled with N(0, 1) keys and
 values at context depths 4096, 32768 and 131072, `reps` calls at each depth
-(k_attn_partial + k_attn_combine), each depth's caches distinct; then the
-same over f16 caches.  Every call goes through the C ABI (dwim_attention).
+(k_attn_partial + k_attn_combine at 4096, k_attn_mfma + k_attn_combine past
+6144 positions), and at 32768 `reps` calls of 4 tokens (a verify batch),
+each depth's caches distinct; then the same over f16 caches.  Every call goes through the C ABI (dwim_attention).
 
 `tokens`: the 4-token Q4_K product (a speculative-decoding verify batch,
 k_planes then k_mv_stream<4>) on the 27B shape's 17408x5120 and 5120x17408
@@ -57,6 +58,12 @@ def attention(reps: int) -> None:
             out = dev.alloc(heads * hd)
             for _ in range(reps):
                 dev.attention(out, q, kc, vc, depth - 1, heads, hd, kvh)
+            if depth == 32768:
+                # a verify batch's 4 tokens at the cache's end
+                q4 = dev.buffer(D.synthetic_values(8, 0, 4 * heads * hd, 1.0))
+                out4 = dev.alloc(4 * heads * hd)
+                for _ in range(reps):
+                    dev.attention(out4, q4, kc, vc, depth - 4, heads, hd, kvh)
             dev.sync()
             print(f"attention {'f16' if f16 else 'q8'} depth {depth}: {reps} calls", flush=True)
             del kc, vc
