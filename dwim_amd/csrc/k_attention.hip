@@ -286,13 +286,28 @@ constexpr int kMStep = 64;       // positions a step
 constexpr int kMThreads = 256;
 constexpr int kQStride = 256 + 8;  // halfs a staged query row (bank spread)
 constexpr int kPStride = kMStep + 4;
-constexpr int kVStride = kMStep + 8;  // elements of a transposed value row
+constexpr int kVStride = kMStep + 8;  // f16: elements of a transposed value row
+constexpr int kVRow = kFD + 16;         // Q8: bytes of a value row as the cache holds it (bank spread)
+
+// Eight int8 values (two little-endian words) as f16, exactly: each byte
+// biased to u = b + 128 and placed under the f16 exponent of 1024
+// (0x64uu = 1024 + u), then 1152 subtracted, two values a packed op.
+DEV ahalf8 i8x8_to_f16(uint32_t w0, uint32_t w1) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 bias = h2{(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
+    const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) - bias;
+    const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) - bias;
+    const h2 c = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) - bias;
+    const h2 d = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) - bias;
+    return ahalf8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
 
 // LDS of k_attn_mfma: queries hi and lo, probabilities, value scales, the
 // rows' max / sum / rescale, the transposed values
 constexpr size_t mfma_lds(int rt, bool f16) {
     return (size_t)16 * rt * kQStride * 2 * 2 + (size_t)16 * rt * kPStride * 4 + (size_t)(kFD / 32) * kMStep * 4 +
-           (size_t)16 * rt * 3 * 4 + (size_t)kFD * kVStride * (f16 ? 2 : 1);
+           (size_t)16 * rt * 3 * 4 + (f16 ? (size_t)kFD * kVStride * 2 : (size_t)kMStep * kVRow);
 }
 
 template <int RT, bool F16>
@@ -363,7 +378,7 @@ __global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ 
     uint4 kscale = make_uint4(0, 0, 0, 0);
     uint4 vw[VP];
     uint4 vscale = make_uint4(0, 0, 0, 0);
-    auto load_keys = [&](size_t ps, int cnt) {
+    auto load_keys = [&](size_t ps, int cnt) __attribute__((always_inline)) {
         const size_t kpos = ps + min(16 * wave + r16, cnt - 1);
         const size_t kbase = kpos * kv_dim + kvh * D + 8 * kq4;
         if constexpr (F16) {
@@ -378,7 +393,7 @@ __global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ 
             kscale = *(const uint4 *)(ks + kpos * (kv_dim / 32) + kvh * 8);
         }
     };
-    auto load_values = [&](size_t ps, int cnt) {
+    auto load_values = [&](size_t ps, int cnt) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < VP; j++) {
             const size_t off = (ps + min(vp0 + j, cnt - 1)) * kv_dim + kvh * D + vd;
@@ -408,15 +423,12 @@ __global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ 
                     *(uint32_t *)(vt + (vd + e) * kVStride + vp0 + j) = a | (b << 16);
                 }
         } else {
+            // Q8: the rows as the cache holds them (read transposed below)
+            // (as a native vector: a uint4 struct copy would keep vw in memory)
+            typedef unsigned u4n __attribute__((ext_vector_type(4)));
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int sh8 = 8 * (e % 4);
-                const uint32_t x = ((word_of(vw[0], e / 4) >> sh8) & 0xffu) |
-                                   (((word_of(vw[1], e / 4) >> sh8) & 0xffu) << 8) |
-                                   (((word_of(vw[2], e / 4) >> sh8) & 0xffu) << 16) |
-                                   (((word_of(vw[3], e / 4) >> sh8) & 0xffu) << 24);
-                *(uint32_t *)(vt_raw + (vd + e) * kVStride + vp0) = x;
-            }
+            for (int j = 0; j < VP; j++)
+                *(u4n *)(vt_raw + (vp0 + j) * kVRow + vd) = u4n{vw[j].x, vw[j].y, vw[j].z, vw[j].w};
             if (threadIdx.x < kMStep) {
                 const uint32_t w4[4] = {vscale.x, vscale.y, vscale.z, vscale.w};
 #pragma unroll
@@ -437,12 +449,7 @@ __global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ 
                     kb = __builtin_bit_cast(ahalf8, kf[b]);
                 } else {
                     const uint4 &x = kf[b / 2];
-                    const uint32_t w0 = (b % 2) ? x.z : x.x, w1 = (b % 2) ? x.w : x.y;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        kb[i] = (_Float16)(int8_t)((w0 >> (8 * i)) & 0xffu);
-                        kb[4 + i] = (_Float16)(int8_t)((w1 >> (8 * i)) & 0xffu);
-                    }
+                    kb = (b % 2) ? i8x8_to_f16(x.z, x.w) : i8x8_to_f16(x.x, x.y);
                 }
                 const float kscl = F16 ? 1.0f : dq::from_f16((uint16_t)(ksw[b / 2] >> (16 * (b % 2))));
 #pragma unroll
@@ -509,12 +516,16 @@ __global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ 
                 if constexpr (F16) {
                     vb[j] = *(const ahalf8 *)((const uint16_t *)vt_raw + d * kVStride + pp);
                 } else {
-                    const uint2 x = *(const uint2 *)(vt_raw + d * kVStride + pp);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        vb[j][i] = (_Float16)(int8_t)((x.x >> (8 * i)) & 0xffu);
-                        vb[j][4 + i] = (_Float16)(int8_t)((x.y >> (8 * i)) & 0xffu);
-                    }
+                    // ds_read_b64_tr_b8: lane 16g + 2b + h names the row of
+                    // position pp_g + b at dimensions d0 + 8h..+7; lane 16g +
+                    // 8h + i receives byte i of the 8 rows of its h, i.e.
+                    // dimension d0 + r16 of positions pp_g..pp_g + 7
+                    const int tb = (lane & 15) >> 1, th = lane & 1;
+                    typedef int v2i_ __attribute__((ext_vector_type(2)));
+                    const v2i_ x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                        (__attribute__((address_space(3))) v2i_ *)(vt_raw + (pp + tb) * kVRow + 64 * wave + 16 * j +
+                                                                     8 * th));
+                    vb[j] = i8x8_to_f16((uint32_t)x[0], (uint32_t)x[1]);
                 }
             }
 #pragma unroll
