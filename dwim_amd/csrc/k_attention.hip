@@ -950,9 +950,9 @@ hipError_t attention_reserve(dwim_dev *dev, size_t floats) {
 namespace {
 
 constexpr size_t kMBlocks = 512;  // blocks the matrix-core pass aims for
-// one token over at most this many positions: the one-chunk VALU pass, whose
-// single round of blocks has less latency (4k positions: 14.0 against 15.0
-// us with the merge; 32k: 47.8 against 38.1)
+// one token over at most this many positions: the one-chunk VALU pass, a
+// single round of blocks (4k positions: 14.1 against 14.2 us with the merge;
+// 32k: 47.8 against 31.2)
 constexpr size_t kValuLen = 6144;
 
 template <int RT, bool F16>
