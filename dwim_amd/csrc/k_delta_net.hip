@@ -217,15 +217,17 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
     float y[kSmallT];
 #pragma unroll
     for (int t = 0; t < kSmallT; t++) {
-        if (t >= n) break;  // (uniform: the batch's tokens only)
-        float acc = 0.0f;
-        acc += w.x * win[t];
-        acc += w.y * win[t + 1];
-        acc += w.z * win[t + 2];
-        acc += w.w * win[t + 3];
-        y[t] = acc * sigmoidf_(acc);
-        const float sq = group_sum<64>(y[t] * y[t]);
-        if ((tid & 63) == 0 && t < n) red[t][tid >> 6] = sq;
+        y[t] = 0.0f;
+        if (t < n) {  // (uniform: the batch's tokens only)
+            float acc = 0.0f;
+            acc += w.x * win[t];
+            acc += w.y * win[t + 1];
+            acc += w.z * win[t + 2];
+            acc += w.w * win[t + 3];
+            y[t] = acc * sigmoidf_(acc);
+            const float sq = group_sum<64>(y[t] * y[t]);
+            if ((tid & 63) == 0) red[t][tid >> 6] = sq;
+        }
     }
     // the last three inputs carry over (the state's rows when the batch is
     // shorter), read again rather than indexed out of the registers; with
@@ -251,13 +253,14 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
         const float4 vwt = ((const float4 *)conv_w)[vc];
 #pragma unroll
         for (int t = 0; t < kSmallT; t++) {
-            if (t >= n) break;
-            float acc = 0.0f;
-            acc += vwt.x * vw[t];
-            acc += vwt.y * vw[t + 1];
-            acc += vwt.z * vw[t + 2];
-            acc += vwt.w * vw[t + 3];
-            vs[t][tid] = acc * sigmoidf_(acc);
+            if (t < n) {
+                float acc = 0.0f;
+                acc += vwt.x * vw[t];
+                acc += vwt.y * vw[t + 1];
+                acc += vwt.z * vw[t + 2];
+                acc += vwt.w * vw[t + 3];
+                vs[t][tid] = acc * sigmoidf_(acc);
+            }
         }
         carry(conv_state_out, vc, n);
         for (int t = 0; t + 1 < n && t < kMaxSteps; t++)
@@ -272,9 +275,10 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
         const int half = tid >> 7;  // 0: q, 1: k
 #pragma unroll
         for (int t = 0; t < kSmallT; t++) {
-            if (t >= n) break;
-            const float ss = red[t][2 * half] + red[t][2 * half + 1];
-            kqs[half ? 0 : 1][t][tid & (kD - 1)] = y[t] * (1.0f / sqrtf(ss + eps));
+            if (t < n) {
+                const float ss = red[t][2 * half] + red[t][2 * half + 1];
+                kqs[half ? 0 : 1][t][tid & (kD - 1)] = y[t] * (1.0f / sqrtf(ss + eps));
+            }
         }
     }
     float s[kKeys];
@@ -719,6 +723,7 @@ hipError_t launch_gdn_tokens(dwim_dev *dev, float *out, const float *qkv, const 
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k, const float *v,
                             const float *gates, const float *decay, float *state, size_t n, size_t n_k_heads,
                             size_t n_v_heads, size_t head_dim, const Rms *rms, bool unit_keys, const float *state_in) {
+    if (head_dim != (size_t)kD || n_k_heads == 0 || n_v_heads % n_k_heads) return hipErrorInvalidValue;
     if (unit_keys && n >= (size_t)kC && !(rms && rms->ss)) {
         if (state_in && state_in != state) return hipErrorInvalidValue;  // (the token loop reads one state, writes another)
         const size_t nch = (n + kC - 1) / kC;

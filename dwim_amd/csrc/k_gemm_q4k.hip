@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(64 * kBfWaves) k_bf16_split(const uint16_t *__
     const uint4 *wr[kBfTiles];
 #pragma unroll
     for (int i = 0; i < kBfTiles; i++) {
-        const unsigned r = 16 * i + r16 < rows ? 16 * i + r16 : 0;
+        const unsigned r = (unsigned)(16 * i + r16) < rows ? (unsigned)(16 * i + r16) : 0u;
         wr[i] = (const uint4 *)(w + (size_t)r * cols + 8 * kq);
     }
     const size_t xo = (size_t)(tlive ? t : 0) * cols + 8 * kq;

@@ -61,7 +61,6 @@ struct Fmt;
 
 template <>
 struct Fmt<DWIM_Q6_K> {
-    static constexpr int kPerChunk = 64;
     __host__ __device__ static size_t chunks(size_t cols) { return cols / 256 * 4; }
     DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
         size_t nb = w.cols / 256;
@@ -97,7 +96,6 @@ struct Fmt<DWIM_Q6_K> {
 
 template <>
 struct Fmt<DWIM_Q4_0> {
-    static constexpr int kPerChunk = 32;
     __host__ __device__ static size_t chunks(size_t cols) { return cols / 32; }
     DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
         size_t nb = w.cols / 32;
@@ -118,7 +116,6 @@ struct Fmt<DWIM_Q4_0> {
 
 template <>
 struct Fmt<DWIM_Q8_0> {
-    static constexpr int kPerChunk = 16;
     __host__ __device__ static size_t chunks(size_t cols) { return cols / 16; }
     DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
         const uint4 q = ((const uint4 *)w.q)[r * (w.cols / 16) + c];
@@ -137,7 +134,6 @@ struct Fmt<DWIM_Q8_0> {
 
 template <>
 struct Fmt<DWIM_BF16> {
-    static constexpr int kPerChunk = 8;
     __host__ __device__ static size_t chunks(size_t cols) { return cols / 8; }
     DEV static float dot(const Weights &w, size_t r, size_t c, const float *x) {
         const uint4 q = ((const uint4 *)w.q)[r * (w.cols / 8) + c];

@@ -1009,8 +1009,8 @@ struct dwim_model {
 
     ~dwim_model() {
         if (picks) {
-            hipStreamSynchronize(dev->stream);
-            hipFree(picks);
+            (void)hipStreamSynchronize(dev->stream);
+            (void)hipFree(picks);
         }
         for (auto *b : bufs) dwim_free_buffer(b);
         for (auto *w : weights) dwim_free_weight(w);

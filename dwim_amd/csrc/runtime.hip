@@ -51,8 +51,8 @@ extern "C" int dwim_open(int index, dwim_dev **out) {
     // the activation planes of one-token matrix products (its zero bytes stay zero)
     if (hipMalloc(&dev->planes, planes_scratch_bytes()) != hipSuccess ||
         hipMemset(dev->planes, 0, planes_scratch_bytes()) != hipSuccess) {
-        if (dev->planes) hipFree(dev->planes);
-        hipStreamDestroy(dev->stream);
+        if (dev->planes) (void)hipFree(dev->planes);
+        (void)hipStreamDestroy(dev->stream);
         delete dev;
         return dwim_fail("allocating the activation planes failed");
     }
@@ -82,7 +82,7 @@ hipError_t dev_grow(dwim_dev *dev, void **ptr, size_t *cap, size_t need, size_t 
         // whatever is queued may still read the old buffer
         hipError_t e = hipStreamSynchronize(dev->stream);
         if (e != hipSuccess) return e;
-        hipFree(*ptr);
+        (void)hipFree(*ptr);
     }
     *ptr = nullptr;
     *cap = 0;
@@ -101,21 +101,21 @@ float *dev_work(dwim_dev *dev, size_t floats) {
 }
 
 void dwim_dev_release_resources(dwim_dev *dev) {
-    hipSetDevice(dev->index);
-    hipStreamSynchronize(dev->stream);
-    if (dev->mv_partials) hipFree(dev->mv_partials);
-    if (dev->mv_counters) hipFree(dev->mv_counters);
-    if (dev->mv_stream) hipFree(dev->mv_stream);
-    if (dev->partials) hipFree(dev->partials);
-    if (dev->argmax_buf) hipFree(dev->argmax_buf);
-    if (dev->tokens) hipFree(dev->tokens);
-    if (dev->planes) hipFree(dev->planes);
-    if (dev->split) hipFree(dev->split);
-    if (dev->work) hipFree(dev->work);
-    if (dev->gemm_parts) hipFree(dev->gemm_parts);
-    if (dev->dn_work) hipFree(dev->dn_work);
-    if (dev->kvx) hipFree(dev->kvx);
-    hipStreamDestroy(dev->stream);
+    (void)hipSetDevice(dev->index);
+    (void)hipStreamSynchronize(dev->stream);
+    if (dev->mv_partials) (void)hipFree(dev->mv_partials);
+    if (dev->mv_counters) (void)hipFree(dev->mv_counters);
+    if (dev->mv_stream) (void)hipFree(dev->mv_stream);
+    if (dev->partials) (void)hipFree(dev->partials);
+    if (dev->argmax_buf) (void)hipFree(dev->argmax_buf);
+    if (dev->tokens) (void)hipFree(dev->tokens);
+    if (dev->planes) (void)hipFree(dev->planes);
+    if (dev->split) (void)hipFree(dev->split);
+    if (dev->work) (void)hipFree(dev->work);
+    if (dev->gemm_parts) (void)hipFree(dev->gemm_parts);
+    if (dev->dn_work) (void)hipFree(dev->dn_work);
+    if (dev->kvx) (void)hipFree(dev->kvx);
+    (void)hipStreamDestroy(dev->stream);
     delete dev;
 }
 
@@ -126,7 +126,7 @@ void dwim_dev_release(dwim_dev *dev) {
 
 extern "C" void dwim_close(dwim_dev *dev) {
     if (!dev) return;
-    hipStreamSynchronize(dev->stream);
+    (void)hipStreamSynchronize(dev->stream);
     dwim_dev_release(dev);
 }
 
@@ -166,7 +166,7 @@ extern "C" int dwim_alloc(dwim_dev *dev, size_t len, dwim_buf **out) {
     float *p = nullptr;
     DWIM_HIP(hipMalloc(&p, std::max<size_t>(len, 1) * sizeof(float)));
     if (hipMemsetAsync(p, 0, std::max<size_t>(len, 1) * sizeof(float), dev->stream) != hipSuccess) {
-        hipFree(p);
+        (void)hipFree(p);
         return dwim_fail("zeroing a buffer failed");
     }
     dev->refs++;
@@ -177,8 +177,8 @@ extern "C" int dwim_alloc(dwim_dev *dev, size_t len, dwim_buf **out) {
 extern "C" void dwim_free_buffer(dwim_buf *buf) {
     if (!buf) return;
     dwim_dev *dev = buf->dev;
-    hipStreamSynchronize(dev->stream);
-    hipFree(buf->data);
+    (void)hipStreamSynchronize(dev->stream);
+    (void)hipFree(buf->data);
     delete buf;
     dwim_dev_release(dev);
 }
@@ -190,13 +190,13 @@ extern "C" int dwim_alloc_cache(dwim_dev *dev, size_t len, dwim_cache **out) {
     uint16_t *s = nullptr;
     DWIM_HIP(hipMalloc(&q, std::max<size_t>(len, 32)));
     if (hipMalloc(&s, std::max<size_t>(len / 32, 1) * 2) != hipSuccess) {
-        hipFree(q);
+        (void)hipFree(q);
         return dwim_fail("allocating a cache failed");
     }
     if (hipMemsetAsync(q, 0, std::max<size_t>(len, 32), dev->stream) != hipSuccess ||
         hipMemsetAsync(s, 0, std::max<size_t>(len / 32, 1) * 2, dev->stream) != hipSuccess) {
-        hipFree(q);
-        hipFree(s);
+        (void)hipFree(q);
+        (void)hipFree(s);
         return dwim_fail("clearing a new cache failed");
     }
     dev->refs++;
@@ -210,7 +210,7 @@ extern "C" int dwim_alloc_cache_f16(dwim_dev *dev, size_t len, dwim_cache **out)
     int8_t *q = nullptr;
     DWIM_HIP(hipMalloc(&q, std::max<size_t>(len, 32) * 2));
     if (hipMemsetAsync(q, 0, std::max<size_t>(len, 32) * 2, dev->stream) != hipSuccess) {
-        hipFree(q);
+        (void)hipFree(q);
         return dwim_fail("clearing a new cache failed");
     }
     dev->refs++;
@@ -221,9 +221,9 @@ extern "C" int dwim_alloc_cache_f16(dwim_dev *dev, size_t len, dwim_cache **out)
 extern "C" void dwim_free_cache(dwim_cache *c) {
     if (!c) return;
     dwim_dev *dev = c->dev;
-    hipStreamSynchronize(dev->stream);
-    hipFree(c->q);
-    hipFree(c->s);
+    (void)hipStreamSynchronize(dev->stream);
+    (void)hipFree(c->q);
+    (void)hipFree(c->s);
     delete c;
     dwim_dev_release(dev);
 }
@@ -326,9 +326,9 @@ static int alloc_copy(dwim_dev *dev, void **dst, const void *src, size_t bytes) 
 extern "C" void dwim_free_weight(dwim_weight *w) {
     if (!w) return;
     dwim_dev *dev = w->dev;
-    hipStreamSynchronize(dev->stream);
+    (void)hipStreamSynchronize(dev->stream);
     for (void *p : {w->q, w->s, w->s2, w->s3})
-        if (p) hipFree(p);
+        if (p) (void)hipFree(p);
     delete w;
     dwim_dev_release(dev);
 }
