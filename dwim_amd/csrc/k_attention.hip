@@ -286,8 +286,8 @@ constexpr int kMStep = 64;       // positions a step
 constexpr int kMThreads = 256;
 constexpr int kQStride = 256 + 8;  // halfs a staged query row (bank spread)
 constexpr int kPStride = kMStep + 4;
-constexpr int kVStride = kMStep + 8;  // f16: elements of a transposed value row
-constexpr int kVRow = kFD + 16;         // Q8: bytes of a value row as the cache holds it (bank spread)
+constexpr int kVRow = kFD + 16;           // Q8: bytes of a value row as the cache holds it (bank spread)
+constexpr int kVRow16 = 2 * kFD + 32;     // f16: bytes of such a row
 
 // Eight int8 values (two little-endian words) as f16, exactly: each byte
 // biased to u = b + 128 and placed under the f16 exponent of 1024
@@ -307,7 +307,7 @@ DEV ahalf8 i8x8_to_f16(uint32_t w0, uint32_t w1) {
 // rows' max / sum / rescale, the transposed values
 constexpr size_t mfma_lds(int rt, bool f16) {
     return (size_t)16 * rt * kQStride * 2 * 2 + (size_t)16 * rt * kPStride * 4 + (size_t)(kFD / 32) * kMStep * 4 +
-           (size_t)16 * rt * 3 * 4 + (f16 ? (size_t)kFD * kVStride * 2 : (size_t)kMStep * kVRow);
+           (size_t)16 * rt * 3 * 4 + (size_t)kMStep * (f16 ? kVRow16 : kVRow);
 }
 
 template <int RT, bool F16>
@@ -411,17 +411,12 @@ __global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ 
         const size_t pn = ps + kMStep;  // the next step
         const bool next = s + 1 < steps && pn < len_last;
         __syncthreads();  // (the previous step is done with vt, p_s and vsc_s; the queries are staged)
-        // ---- the values, transposed: vt[d][position]
+        // ---- the values, in LDS as the cache holds them (read transposed below)
         if constexpr (F16) {
-            uint16_t *vt = (uint16_t *)vt_raw;
+            typedef unsigned u4n __attribute__((ext_vector_type(4)));
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-#pragma unroll
-                for (int j = 0; j < VP; j += 2) {
-                    const uint32_t a = (word_of(vw[j], e / 2) >> (16 * (e % 2))) & 0xffffu;
-                    const uint32_t b = (word_of(vw[j + 1], e / 2) >> (16 * (e % 2))) & 0xffffu;
-                    *(uint32_t *)(vt + (vd + e) * kVStride + vp0 + j) = a | (b << 16);
-                }
+            for (int j = 0; j < VP; j++)
+                *(u4n *)(vt_raw + (vp0 + j) * kVRow16 + 2 * vd) = u4n{vw[j].x, vw[j].y, vw[j].z, vw[j].w};
         } else {
             // Q8: the rows as the cache holds them (read transposed below)
             // (as a native vector: a uint4 struct copy would keep vw in memory)
@@ -512,9 +507,24 @@ __global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ 
             ahalf8 vb[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int d = 64 * wave + 16 * j + r16;
                 if constexpr (F16) {
-                    vb[j] = *(const ahalf8 *)((const uint16_t *)vt_raw + d * kVStride + pp);
+                    // ds_read_b64_tr_b16, twice (positions pp.., pp + 4..):
+                    // lane 16g + m + 4b names the row of position b at
+                    // dimensions d0 + 4m..+3; lane 16g + 4m + i receives
+                    // element i of its m's 4 rows, i.e. dimension d0 + r16
+                    const int tb = (lane & 15) >> 2, tm = lane & 3;
+                    typedef short v4s_ __attribute__((ext_vector_type(4)));
+                    const uint8_t *row = vt_raw + 2 * (64 * wave + 16 * j + 4 * tm);
+                    const v4s_ x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s_ *)(row + (pp + tb) * kVRow16));
+                    const v4s_ x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s_ *)(row + (pp + 4 + tb) * kVRow16));
+                    // (whole words: assembled element by element, the
+                    // compiler took x0[2..3] for copies of x0[0..1])
+                    typedef unsigned u2n_ __attribute__((ext_vector_type(2)));
+                    typedef unsigned u4n_ __attribute__((ext_vector_type(4)));
+                    const u2n_ a0 = __builtin_bit_cast(u2n_, x0), a1 = __builtin_bit_cast(u2n_, x1);
+                    vb[j] = __builtin_bit_cast(ahalf8, u4n_{a0.x, a0.y, a1.x, a1.y});
                 } else {
                     // ds_read_b64_tr_b8: lane 16g + 2b + h names the row of
                     // position pp_g + b at dimensions d0 + 8h..+7; lane 16g +
