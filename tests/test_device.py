@@ -388,6 +388,9 @@ ATTENTION_CASES = [
     (24, 256, 4, 1, 40000, 1.0), (16, 128, 8, 1, 3000, 1.0),
     # small batches: a block takes up to 4 tokens (some past a chunk's start, some not)
     (24, 256, 4, 4, 62, 1.0), (24, 256, 4, 9, 60, 1.0), (8, 64, 2, 5, 0, 1.0), (16, 128, 8, 15, 3001, 1.0),
+    # the matrix-core decode pass (head_dim 256): 8 heads a key/value head and 4 tokens (32 query rows), one
+    # head a key/value head past 6144 positions, a ragged last group of tokens
+    (8, 256, 1, 4, 7000, 1.0), (8, 256, 8, 1, 9000, 1.0), (16, 256, 2, 9, 300, 1.0), (24, 256, 4, 2, 6143, 1e-3),
     # batches through the prefill kernel (head_dim 256, 16 tokens or more)
     (24, 256, 4, 33, 0, 1e-3), (4, 256, 1, 100, 5, 1.0), (24, 256, 4, 300, 1500, 1.0), (8, 256, 8, 16, 31, 1.0),
 ]
