@@ -200,7 +200,15 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
     // ---- loads: the state slice, this thread's q or k channel over the
     // batch (with its window and weights), the block's value channels, the
     // gate logits
-    for (int e = tid; e < kD * kCols; e += kThreads) tile[e / kCols][e % kCols] = Sin[(e / kCols) * kD + c0 + e % kCols];
+    // (every load of the block issues before any is waited for: the slice
+    // into registers here, into LDS once the others are issued)
+    constexpr int kTileLoads = kD * kCols / kThreads;
+    float tl[kTileLoads];
+#pragma unroll
+    for (int u = 0; u < kTileLoads; u++) {
+        const int e = tid + u * kThreads;
+        tl[u] = Sin[(e / kCols) * kD + c0 + e % kCols];
+    }
     const size_t qk = tid < kD ? (size_t)kh * kD + tid : (size_t)(n_k_heads + kh) * kD + (tid - kD);
     float win[kSmallT + 3];
 #pragma unroll
@@ -211,6 +219,22 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
     const size_t vc = (size_t)(2 * n_k_heads + h) * kD + c0 + (tid % kCols);
     const bool vlane = tid < kCols;
     const float a = decay[h], dt = decay[n_v_heads + h];
+    // the value lanes' channels (loaded by all of wave 0, so that the loads
+    // issue here, unconditionally within the wave) and the gate logits
+    float vw[kSmallT + 3];
+    float4 vwt = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (tid < 64) {
+#pragma unroll
+        for (int j = 0; j < 3; j++) vw[j] = conv_state[(size_t)j * ch + vc];
+#pragma unroll
+        for (int t = 0; t < kSmallT; t++) vw[3 + t] = t < n ? qkv[(size_t)t * ch + vc] : 0.0f;
+        vwt = ((const float4 *)conv_w)[vc];
+    }
+    float g_alpha = 0.0f, g_beta = 0.0f;
+    if (tid < n) {
+        g_alpha = gates[(size_t)tid * 2 * n_v_heads + h];
+        g_beta = gates[(size_t)tid * 2 * n_v_heads + n_v_heads + h];
+    }
 
     // ---- q and k: conv + SiLU, each token's sum of squares a block sum
     // over its half (q: waves 0-1, k: waves 2-3)
@@ -229,28 +253,34 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
             if ((tid & 63) == 0) red[t][tid >> 6] = sq;
         }
     }
-    // the last three inputs carry over (the state's rows when the batch is
-    // shorter), read again rather than indexed out of the registers; with
-    // steps, also after each earlier token t (the conv state of t + 1 kept)
-    auto carry = [&](float *dst, size_t idx, int upto) {
-#pragma unroll
-        for (int j = 0; j < 3; j++) {
-            const int tp = upto - 3 + j;
-            dst[(size_t)j * ch + idx] = tp >= 0 ? qkv[(size_t)tp * ch + idx] : conv_state[(size_t)(3 + tp) * ch + idx];
-        }
-    };
-    if (blockIdx.x == 0 && h % ratio == 0) {
-        carry(conv_state_out, qk, n);
-        for (int t = 0; t + 1 < n && t < kMaxSteps; t++)
-            if (steps.conv[t]) carry(steps.conv[t], qk, t + 1);
+    // the last three inputs carry over: after the batch, window entries
+    // n..n+2 (the state's rows when the batch is shorter); with steps, also
+    // after each earlier token t, entries t+1..t+3 (the conv state of t + 1
+    // kept).  Stored from the window's registers, every index a constant (a
+    // branch per batch size), so that no store waits for a load of its own.
+    // (a macro rather than a lambda over the array, which would put the
+    // window in scratch memory)
+#define DWIM_GDN_CARRY(WV, IDX)                                                                   \
+    {                                                                                            \
+        float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f;                                                   \
+        _Pragma("unroll") for (int m = 1; m <= kSmallT; m++) if (m == n) {                       \
+            c0 = WV[m];                                                                          \
+            c1 = WV[m + 1];                                                                      \
+            c2 = WV[m + 2];                                                                      \
+        }                                                                                        \
+        conv_state_out[(IDX)] = c0;                                                              \
+        conv_state_out[ch + (IDX)] = c1;                                                         \
+        conv_state_out[2 * ch + (IDX)] = c2;                                                     \
+        _Pragma("unroll") for (int t = 0; t < kMaxSteps && t + 1 < kSmallT; t++) {               \
+            if (t + 1 < n && steps.conv[t]) {                                                    \
+                steps.conv[t][(IDX)] = WV[t + 1];                                                \
+                steps.conv[t][ch + (IDX)] = WV[t + 2];                                           \
+                steps.conv[t][2 * ch + (IDX)] = WV[t + 3];                                       \
+            }                                                                                    \
+        }                                                                                        \
     }
+    if (blockIdx.x == 0 && h % ratio == 0) DWIM_GDN_CARRY(win, qk)
     if (vlane) {
-        float vw[kSmallT + 3];
-#pragma unroll
-        for (int j = 0; j < 3; j++) vw[j] = conv_state[(size_t)j * ch + vc];
-#pragma unroll
-        for (int t = 0; t < kSmallT; t++) vw[3 + t] = t < n ? qkv[(size_t)t * ch + vc] : 0.0f;
-        const float4 vwt = ((const float4 *)conv_w)[vc];
 #pragma unroll
         for (int t = 0; t < kSmallT; t++) {
             if (t < n) {
@@ -262,14 +292,15 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
                 vs[t][tid] = acc * sigmoidf_(acc);
             }
         }
-        carry(conv_state_out, vc, n);
-        for (int t = 0; t + 1 < n && t < kMaxSteps; t++)
-            if (steps.conv[t]) carry(steps.conv[t], vc, t + 1);
+        DWIM_GDN_CARRY(vw, vc)
     }
     // g = exp(a·softplus(alpha + dt_bias)), beta = sigmoid(beta_logit)
-    if (tid < n)
-        gb[tid] = make_float2(expf(a * softplusf_(gates[(size_t)tid * 2 * n_v_heads + h] + dt)),
-                              sigmoidf_(gates[(size_t)tid * 2 * n_v_heads + n_v_heads + h]));
+    if (tid < n) gb[tid] = make_float2(expf(a * softplusf_(g_alpha + dt)), sigmoidf_(g_beta));
+#pragma unroll
+    for (int u = 0; u < kTileLoads; u++) {
+        const int e = tid + u * kThreads;
+        tile[e / kCols][e % kCols] = tl[u];
+    }
     __syncthreads();
     {
         const int half = tid >> 7;  // 0: q, 1: k
@@ -318,24 +349,23 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
         const float o = sum16(o0 + o1) * scale;
         if (p == 0 && out) out[((size_t)t * n_v_heads + h) * kD + c0 + c] = o;
         if (t + 1 < n && t < kMaxSteps && steps.state[t]) {
-            // the state after token t, for a rewind that keeps t + 1 tokens
-            // (through LDS, a row's 16 columns in one run, as at the end)
-            float *St = steps.state[t] + (size_t)h * kD * kD;
-            __syncthreads();  // (the previous step's copy is done with the tile)
+            // the state after token t, for a rewind that keeps t + 1 tokens,
+            // straight from the registers (no barrier: the token loop goes on
+            // while the stores drain)
+            float *St = steps.state[t] + (size_t)h * kD * kD + c0 + c;
 #pragma unroll
-            for (int i = 0; i < kKeys; i++) tile[p * kKeys + i][c] = s[i];
-            __syncthreads();
-            for (int e = tid; e < kD * kCols; e += kThreads) St[(e / kCols) * kD + c0 + e % kCols] = tile[e / kCols][e % kCols];
+            for (int i = 0; i < kKeys; i++) St[(size_t)(p * kKeys + i) * kD] = s[i];
         }
     }
 
-    // ---- the state slice out, through LDS
-    __syncthreads();  // (a step's copy may still read the tile)
+    // ---- the state slice out, through LDS (every read of the tile was
+    // before the barrier ahead of the token loop)
 #pragma unroll
     for (int i = 0; i < kKeys; i++) tile[p * kKeys + i][c] = s[i];
     __syncthreads();
     for (int e = tid; e < kD * kCols; e += kThreads) S[(e / kCols) * kD + c0 + e % kCols] = tile[e / kCols][e % kCols];
 }
+#undef DWIM_GDN_CARRY
 
 // ---- The chunked form, for batches of at least kC tokens -------------------
 //

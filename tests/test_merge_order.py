@@ -7,9 +7,9 @@ release/acquire fence (whose cache maintenance would write back or drop the
 XCD's L2), the ordering rests on this sequence, which the test asserts for
 every counter add of every kernel:
   * the partial sums are stored device-coherently (`global_store ... sc1`);
-  * `s_waitcnt vmcnt(0)` lies between the last such store and the counter's
+  * an `s_waitcnt` with `vmcnt(0)` lies between the last such store and the counter's
     `global_atomic_add ... sc0` (the add with its old value returned);
-  * after the add, `s_waitcnt vmcnt(0)` and a branch on its result come
+  * after the add, such a wait and a branch on its result come
     before the first device-coherent load of the partial sums
     (`global_load ... sc1`).
 Compiles with hipcc (no GPU needed).
@@ -48,14 +48,20 @@ def _check_meetings(body):
     for i in adds:
         stores = [j for j in range(i) if l_is(body[j], "global_store") and "sc1" in body[j].split()]
         assert stores, "no device-coherent partial store before the counter add"
-        assert "s_waitcnt vmcnt(0)" in body[stores[-1] + 1:i], "the add may issue before the stores complete"
+        assert any(_vm0(l) for l in body[stores[-1] + 1:i]), "the add may issue before the stores complete"
         loads = [j for j in range(i + 1, len(body)) if l_is(body[j], "global_load") and "sc1" in body[j].split()]
         assert loads, "no device-coherent partial load after the counter add"
         between = body[i + 1:loads[0]]
-        w = between.index("s_waitcnt vmcnt(0)") if "s_waitcnt vmcnt(0)" in between else None
+        w = next((k for k, l in enumerate(between) if _vm0(l)), None)
         assert w is not None, "the partial loads may issue before the add returns"
         assert any(l.startswith("s_cbranch") for l in between[w:]), "no branch on the add's result"
     return len(adds)
+
+
+def _vm0(line):
+    """An s_waitcnt that waits for every vector memory operation (vmcnt(0),
+    alone or with other counters)."""
+    return line.startswith("s_waitcnt") and "vmcnt(0)" in line.split()
 
 
 def l_is(line, op):
