@@ -127,7 +127,7 @@ __global__ void __launch_bounds__(kPlanesThreads) k_planes_gated(const float *__
 constexpr int kMaxJobs = 4;
 constexpr int kMaxParts = 4;
 constexpr int kMaxTok = 4;     // tokens of a several-token launch (a verify batch: 1 + 3 drafts)
-constexpr int kBatchArea = 2;  // planes areas kBatchArea.. hold the tokens of such a launch
+static_assert(kBatchArea2 == kBatchArea + kMaxTok, "the two sets of batch areas lie one after the other");
 // RMS partial sums a lane loads up front: 6 · 64 groups of 16 cover 6144
 // columns (the rest, if any, are loaded at the end)
 constexpr int kRmsLoads = 6;
@@ -552,7 +552,7 @@ hipError_t run(dwim_dev *dev, Args a, unsigned njobs, const size_t *rows) {
 
 }  // namespace
 
-size_t planes_scratch_bytes() { return (kBatchArea + kMaxTok) * planes::kAreaBytes; }
+size_t planes_scratch_bytes() { return (kBatchArea2 + kMaxTok) * planes::kAreaBytes; }
 
 planes::View planes_area(dwim_dev *dev, int area, size_t cols) {
     return planes::view((int8_t *)dev->planes + area * planes::kAreaBytes, cols);
@@ -634,8 +634,43 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
 
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                                      int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
-                                     float *xn_out, const float *gate_z) {
+                                     float *xn_out, const float *gate_z, const StreamExtra *se) {
     if (count < 1 || count > kMaxJobs || (swiglu && count != 2) || n < 1) return hipErrorInvalidValue;
+    if (se) {
+        // one launch of 2..4 tokens, its planes handed over (in_area) or made
+        // here into the first batch set, its results' planes handed on
+        const int in = se->in_area >= 0 ? se->in_area : kBatchArea;
+        if (n < 2 || n > (size_t)kMaxTok || (in != kBatchArea && in != kBatchArea2) || (se->rms && se->in_area < 0) ||
+            (se->emit_area >= 0 && se->emit_area != kBatchArea && se->emit_area != kBatchArea2) ||
+            se->emit_area == in)
+            return hipErrorInvalidValue;
+        const size_t cols = ws[0]->cols;
+        if (cols > planes::kMaxCols || cols % 256) return hipErrorInvalidValue;
+        for (int j = 0; j < count; j++)
+            if (ws[j]->cols != cols || ws[j]->fmt != DWIM_Q4_K || ws[j]->rows >= (1u << 31)) return hipErrorInvalidValue;
+        if (swiglu && ws[0]->rows != ws[1]->rows) return hipErrorInvalidValue;
+        dev->prepared = 0;
+        if (se->in_area < 0) {
+            if (!x || (gate_z && (!norm || cols % 128))) return hipErrorInvalidValue;
+            const unsigned blocks = (unsigned)((cols / 4 + kPlanesThreads - 1) / kPlanesThreads);
+            if (gate_z)
+                k_planes_gated<<<dim3(blocks, (unsigned)n), kPlanesThreads, 0, dev->stream>>>(
+                    gate_z, x, norm, eps, planes_area(dev, kBatchArea, cols));
+            else
+                k_planes<<<dim3(blocks, (unsigned)n), kPlanesThreads, 0, dev->stream>>>(
+                    x, norm, eps, 0, norm ? xn_out : nullptr, planes_area(dev, kBatchArea, cols), 1);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        const int8_t *xq[kMaxTok];
+        const float *xs[kMaxTok];
+        for (size_t t = 0; t < n; t++) {
+            const planes::View v = planes_area(dev, in + (int)t, cols);
+            xq[t] = v.q;
+            xs[t] = v.stat;
+        }
+        return run_mv_stream(dev, ws, outs, adds, count, swiglu, n, xq, xs, se);
+    }
     const size_t cols = ws[0]->cols;
     if (cols > planes::kMaxCols || cols % 256) return hipErrorInvalidValue;
     size_t rows[kMaxJobs];

@@ -87,6 +87,20 @@ struct StreamArgs {
     const float *xstat[kTok];    // [cols/64][8]
     float *partials;             // [tile][part][cmax][NT][32]
     unsigned *counters;          // [tile], zero between launches
+    // given: the planes are x·w with Σx² per group (rss[t], [cols/16]), and
+    // token t's results scale by 1/sqrt(Σ rss[t] / cols + eps) (workgroup 0
+    // writes the scales to rms_out[t] when that is given)
+    const float *rss[kTok];
+    float eps;
+    float *rms_out;
+    // given (one matrix or a SwiGLU pair, rows whole 256-blocks): token t's
+    // planes of the results, after the add or the SwiGLU, into the plane area
+    // at emit + t·kAreaBytes; of results·emit_norm with Σ results² per group
+    // when emit_norm is given (and results·emit_norm in f32 to emit_xw,
+    // [NT][rows], when that is given)
+    int8_t *emit;
+    const float *emit_norm;
+    float *emit_xw;
 };
 
 // Kernel-argument arrays are copied once, with constant indices, each
@@ -158,15 +172,18 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
     const unsigned cols = nb * 256;
 
     // LDS: planes [block][token][51 chunks], statistics [block][token][8],
-    // the zero region, per wave the decoded scales, the items' sums
+    // the zero region, per wave the decoded scales, the tokens' RMS scales
+    // (one chunk), the items' sums
     const unsigned kStat = a.plane_cap * NT * kBT;
     const unsigned kZero = kStat + a.plane_cap * NT * 8;
     const unsigned kHdr = kZero + kK * NT * kBT;
-    const unsigned kSlots = kHdr + kW * kHdrChunks;
+    const unsigned kTsc = kHdr + kW * kHdrChunks;
+    const unsigned kSlots = kTsc + 1;
     v4i *lv = (v4i *)lds;
     const float4 *stl = (const float4 *)(lds + kStat);
     float *hdr = (float *)(lds + kHdr + wave * kHdrChunks);
     float *slots = (float *)(lds + kSlots);  // [item - i0][NT][16]
+    float *tsc = (float *)(lds + kTsc);
 
     auto item_of = [=](unsigned i) {
         Item it;
@@ -241,19 +258,26 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
                 const v4u q0 = R.q[u][0], q1 = R.q[u][1];
                 const v4i a0 = {(int)(q0.x & mask), (int)(q0.y & mask), (int)(q0.z & mask), (int)(q0.w & mask)};
                 const v4i a1 = {(int)(q1.x & mask), (int)(q1.y & mask), (int)(q1.z & mask), (int)(q1.w & mask)};
-                v4i C[3];
+                // the sub-block's two groups of 16 (its two MFMAs, m = 0, 1)
+                // each with its own activation scale
+                v4i C[3], E[3];
 #pragma unroll
                 for (int r = 0; r < 3; r++) {
                     const v4i *bp = bbase + r * kPStride + 2 * h;
                     C[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
-                    C[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bp[1], C[r], 0, 0, 0);
+                    E[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bp[1], v4i{0, 0, 0, 0}, 0, 0, 0);
                 }
-                // the digits meet (weights 1, 256, 65536), then the scale
+                const float sx1 = ((const float *)sxp)[2 * h + 1];
+                // the digits meet (weights 1, 256, 65536; the first two in
+                // int32: a column sums 16 products of at most 128·128, so
+                // |C0| + 256·|C1| < 2^27), then the scales
                 const float Ds[4] = {Dsb.x * sx, Dsb.y * sx, Dsb.z * sx, Dsb.w * sx};
+                const float Es[4] = {Dsb.x * sx1, Dsb.y * sx1, Dsb.z * sx1, Dsb.w * sx1};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float v = (float)C[0][e] + 256.0f * (float)C[1][e] + 65536.0f * (float)C[2][e];
-                    acc[e] += Ds[e] * v;
+                    const float v = (float)(C[0][e] + C[1][e] * 256) + 65536.0f * (float)C[2][e];
+                    const float w = (float)(E[0][e] + E[1][e] * 256) + 65536.0f * (float)E[2][e];
+                    acc[e] += Ds[e] * v + Es[e] * w;
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -335,14 +359,15 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     const v4i *bp = bbase + t * kBT + 2 * h;
-                    v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
-                    C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bp[1], C, 0, 0, 0);
-                    // token t's scale of sub-block 2·gcol + h
-                    const float sx = ((const float *)&stl[(bl * NT + t) * 8 + 2 * gcol])[2 * h];
-                    acc[t][0] += (Dsb.x * sx) * (float)C[0];
-                    acc[t][1] += (Dsb.y * sx) * (float)C[1];
-                    acc[t][2] += (Dsb.z * sx) * (float)C[2];
-                    acc[t][3] += (Dsb.w * sx) * (float)C[3];
+                    const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const v4i E = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bp[1], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    // token t's scales of sub-block 2·gcol + h (its two groups of 16)
+                    const float *sxt = (const float *)&stl[(bl * NT + t) * 8 + 2 * gcol];
+                    const float sx = sxt[2 * h], sx1 = sxt[2 * h + 1];
+                    acc[t][0] += (Dsb.x * sx) * (float)C[0] + (Dsb.x * sx1) * (float)E[0];
+                    acc[t][1] += (Dsb.y * sx) * (float)C[1] + (Dsb.y * sx1) * (float)E[1];
+                    acc[t][2] += (Dsb.z * sx) * (float)C[2] + (Dsb.z * sx1) * (float)E[2];
+                    acc[t][3] += (Dsb.w * sx) * (float)C[3] + (Dsb.w * sx1) * (float)E[3];
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -368,6 +393,29 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
     const unsigned n_w = i1 - i0 > (unsigned)wave ? (i1 - i0 - (unsigned)wave + kW - 1) / kW : 0u;
     Regs<kK> A, B;
     Item ia{}, ib{};
+    // the finishing pass's first tile for this wave (a run holds fewer than
+    // kW tiles, as a rule): its old outputs (x of x += W·in) and the emitted
+    // planes' norm weights, loaded with the planes rather than in the run's
+    // tail; lane (token pair ts, row) as in the finishing pass
+    const int hf = lane >> 5, ts = (lane >> 4) & 1, row = lane & 15;
+    const unsigned Tfirst = i0 / ip, Tlast = i1 > i0 ? (i1 - 1) / ip : Tfirst - 1;
+    const unsigned Tw = Tfirst + (unsigned)wave;
+    float pre0 = 0.0f, pre1 = 0.0f, pre_nw = 1.0f;
+    // the RMS scales (given): wave t < NT sums token t's Σx² per group, the
+    // first kRssLoads · 64 groups loaded with the planes, the rest (if any)
+    // after; in group order, so that every workgroup scales by the same bits
+    // (the loads are issued below)
+    constexpr int kRssLoads = 6;
+    const unsigned ngr = cols / 16u;
+    const GMEM float *rs0 = (const GMEM float *)sload(a.rss[0]);
+    const bool rms = rs0 != nullptr;
+    const GMEM float *rsw = rs0;
+#pragma unroll
+    for (int q = 1; q < NT; q++) {
+        const GMEM float *rq = (const GMEM float *)sload(a.rss[q]);
+        rsw = wave == q ? rq : rsw;
+    }
+    float rsv[kRssLoads];
     {
         // a run of global memory a wave: token t's digit p (PB·16 chunks at
         // xq[t] + p·cols + pb·256) for run 4t + p, its statistics (PB·8 chunks
@@ -402,6 +450,27 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
         // reloads the run's first, which every run has)
         ia = item_of(i0 + (n_w > 0 ? (unsigned)wave : 0u));
         load(A, ia);
+        // (behind the planes and the first weights: the first tile's old
+        // outputs and norm weights, and the RMS partial sums)
+        if (Tw <= Tlast && i1 > i0) {
+            const unsigned j = (unsigned)(Tw >= t01) + (unsigned)(Tw >= t02) + (unsigned)(Tw >= t03);
+            const unsigned rj = sel(j, sreg(a.rows[0]), sreg(a.rows[1]), sreg(a.rows[2]), sreg(a.rows[3]));
+            const unsigned grow = (Tw - sel(j, 0u, t01, t02, t03)) * 16 + (unsigned)row;
+            const unsigned gr = grow < rj ? grow : 0u;
+            const float *oj = sel(j, sreg(a.out[0]), sreg(a.out[1]), sreg(a.out[2]), sreg(a.out[3]));
+            if ((a.add_mask >> j) & 1u) {
+                pre0 = oj[(size_t)ts * rj + gr];
+                if (ts + 2 < NT) pre1 = oj[(size_t)(ts + 2) * rj + gr];
+            }
+            if (a.emit_norm) pre_nw = a.emit_norm[gr];
+        }
+        if (rms && wave < NT) {
+#pragma unroll
+            for (int u = 0; u < kRssLoads; u++) {
+                const unsigned gi = (unsigned)lane + 64u * (unsigned)u;
+                rsv[u] = rsw[gi < ngr ? gi : 0u];
+            }
+        }
         if (staging) {
 #pragma unroll
             for (int u = 0; u < kSL; u++) {
@@ -415,6 +484,19 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
             }
         }
         if (threadIdx.x < (unsigned)(kK * NT * kBT)) lv[kZero + threadIdx.x] = v4i{0, 0, 0, 0};
+    }
+    if (rms && wave < NT) {
+        float t = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kRssLoads; u++)
+            if ((unsigned)lane + 64u * (unsigned)u < ngr) t += rsv[u];
+        for (unsigned gi = (unsigned)lane + 64u * kRssLoads; gi < ngr; gi += 64u) t += rsw[gi];
+        t = group_sum<64>(t);
+        const float sc = 1.0f / sqrtf(t / (float)cols + a.eps);
+        if (lane == 0) {
+            tsc[wave] = sc;
+            if (g == 0 && a.rms_out) a.rms_out[wave] = sc;
+        }
     }
     __syncthreads();
 
@@ -433,14 +515,14 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
 
     // ---- each tile of the run: its items' sums in order, by one wave
     // lane (half hf, token pair ts, row): tokens ts and ts + 2
-    const int hf = lane >> 5, ts = (lane >> 4) & 1, row = lane & 15;
-    const unsigned Tfirst = i0 / ip, Tlast = i1 > i0 ? (i1 - 1) / ip : Tfirst - 1;
-    for (unsigned T = Tfirst + (unsigned)wave; T <= Tlast && i1 > i0; T += kW) {
-        const unsigned lo = max(i0, T * ip), hi = min(i1, (T + 1) * ip);
+    for (unsigned T = Tw; T <= Tlast && i1 > i0; T += kW) {
+        // the lane's half's items of the tile in this run, in order (a few
+        // LDS reads in flight at once)
+        const unsigned lo = max(max(i0, T * ip), T * ip + (unsigned)hf * ih);
+        const unsigned hi = min(min(i1, (T + 1) * ip), T * ip + ((unsigned)hf + 1) * ih);
         float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll 4
         for (unsigned i = lo; i < hi; i++) {
-            const int half = (int)((i - T * ip) / ih);
-            if (half != hf) continue;
             const float *sl = slots + (size_t)(i - i0) * NT * 16;
             v0 += sl[ts * 16 + row];
             if (ts + 2 < NT) v1 += sl[(ts + 2) * 16 + row];
@@ -499,8 +581,15 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
         // own value first, then lane + 32's)
         const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v0), false, false);
         const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v1), __float_as_uint(v1), false, false);
-        const float x0 = __uint_as_float(s0[0]), y0 = __uint_as_float(s0[1]);
-        const float x1 = __uint_as_float(s1[0]), y1 = __uint_as_float(s1[1]);
+        float x0 = __uint_as_float(s0[0]), y0 = __uint_as_float(s0[1]);
+        float x1 = __uint_as_float(s1[0]), y1 = __uint_as_float(s1[1]);
+        if (rms) {
+            const float f0 = tsc[ts], f1 = tsc[ts + 2 < NT ? ts + 2 : ts];
+            x0 *= f0;
+            y0 *= f0;
+            x1 *= f1;
+            y1 *= f1;
+        }
         const unsigned j = (unsigned)(T >= t01) + (unsigned)(T >= t02) + (unsigned)(T >= t03);
         const unsigned rj = sel(j, sreg(a.rows[0]), sreg(a.rows[1]), sreg(a.rows[2]), sreg(a.rows[3]));
         const unsigned grow = (T - sel(j, 0u, t01, t02, t03)) * 16 + (unsigned)row;
@@ -512,11 +601,32 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
             r0 = x0 * sigmoidf_(x0) * y0;  // silu(gate) · up (gpu/cpu.rs:238-242)
             r1 = x1 * sigmoidf_(x1) * y1;
         }
+        const bool first = T == Tw;  // (its old outputs and weights loaded up front)
         float *o0 = oj + (size_t)ts * rj + grow;
-        *o0 = adds ? *o0 + r0 : r0;
+        const float e0 = adds ? (first ? pre0 : *o0) + r0 : r0;
+        *o0 = e0;
+        float e1 = 0.0f;
         if (ts + 2 < NT) {
             float *o1 = oj + (size_t)(ts + 2) * rj + grow;
-            *o1 = adds ? *o1 + r1 : r1;
+            e1 = adds ? (first ? pre1 : *o1) + r1 : r1;
+            *o1 = e1;
+        }
+        if (a.emit) {
+            // lanes 16ts..16ts+15 (one group of 16, the tile's rows): tokens
+            // ts and ts + 2
+            const float nw = first ? pre_nw : a.emit_norm ? a.emit_norm[grow] : 1.0f;
+            auto emit_one = [&](unsigned tok, float f) {
+                const planes::View v = planes::view(a.emit + tok * planes::kAreaBytes, rj);
+                const float xv = f * nw;
+                if (a.emit_norm) {
+                    const float sq = group_sum<16>(f * f);
+                    if (row == 0) v.ss[grow / 16] = sq;
+                }
+                if (a.emit_xw) a.emit_xw[(size_t)tok * rj + grow] = xv;
+                planes::write16(v, grow, xv);
+            };
+            emit_one((unsigned)ts, e0);
+            if (ts + 2 < NT) emit_one((unsigned)ts + 2, e1);
         }
     }
 }
@@ -524,7 +634,8 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
 }  // namespace
 
 hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds, int count,
-                         int swiglu, size_t nt, const int8_t *const *xq, const float *const *xstat) {
+                         int swiglu, size_t nt, const int8_t *const *xq, const float *const *xstat,
+                         const StreamExtra *se) {
     if (nt < 2 || nt > (size_t)kTok || count < 1 || count > kJobs || (swiglu && count != 2)) return hipErrorInvalidValue;
     const unsigned NT = (unsigned)nt, J = swiglu ? 2u : 1u, njobs = swiglu ? 1u : (unsigned)count;
     const unsigned K = (unsigned)k_of((int)nt);
@@ -596,7 +707,22 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
         a.xq[t] = xq[t];
         a.xstat[t] = xstat[t];
     }
-    const size_t lds = ((size_t)plane_cap * NT * (kBT + 8) + (size_t)K * NT * kBT + (size_t)kW * kHdrChunks) * 16 +
+    if (se && se->rms) {
+        // (each token's planes are the start of its plane area)
+        for (unsigned t = 0; t < NT; t++) a.rss[t] = (const float *)(xq[t] + planes::kSsOff);
+        a.eps = se->eps;
+        a.rms_out = se->rms_out;
+    }
+    if (se && se->emit_area >= 0) {
+        const size_t rows = ws[0]->rows;
+        if ((njobs != 1 && !swiglu) || rows % 256 || rows > planes::kMaxCols || se->emit_area < 0 ||
+            (size_t)se->emit_area + NT > (size_t)kBatchArea2 + kTok)
+            return hipErrorInvalidValue;
+        a.emit = planes_area(dev, se->emit_area, rows).q;
+        a.emit_norm = se->emit_norm;
+        a.emit_xw = se->emit_xw;
+    }
+    const size_t lds = ((size_t)plane_cap * NT * (kBT + 8) + (size_t)K * NT * kBT + (size_t)kW * kHdrChunks + 1) * 16 +
                        (size_t)items_cap * NT * 16 * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     // raised once a process for each kernel (a function-local static is

@@ -96,6 +96,8 @@ struct dwim_model {
     dwim_buf *up = nullptr, *gate_ffn = nullptr, *logits = nullptr, *rope = nullptr, *drafted = nullptr;
     // the one-token DeltaNet step's Σo² per head quarter ([v_heads][4])
     dwim_buf *head_ss = nullptr;
+    // a 2..4-token batch's RMS scales of its handed-over layer input ([4])
+    dwim_buf *row_scales = nullptr;
     // device-fed greedy decoding: the picks, and where the step running
     // reads its token and writes its pick (null outside decode_greedy)
     uint32_t *picks = nullptr;
@@ -324,6 +326,76 @@ struct dwim_model {
         return 0;
     }
 
+    // 2..4 tokens through a fused layer hand every product's planes to the
+    // next as one token does, in the two sets of batch areas: the layer input
+    // (planes of x·attn_norm with Σx² per group) arrives in the second set
+    // when the previous layer's down product wrote it (batch_in), else is
+    // made in the first; the mixer's output is made in the first set; the
+    // residual product x += o·att hands x·mlp_norm on in the second; the
+    // SwiGLU pair its result in the first; the down product the next
+    // layer's input in the second (and, before a DeltaNet layer, x·attn_norm
+    // in f32 to xh for its gate rows, which scale by the batch's row scales).
+    int batch_in = -1;
+    bool batch_hand(const Layer &l, size_t n) const {
+        return n >= 2 && n <= 4 && fusable(l) && c.state_dim == 128 &&
+               (l.attention || (l.ab->fmt == DWIM_BF16 && l.ab->rows <= 96));
+    }
+    // products of the layer input (handed over in `in_set`, or made here from
+    // x with the norm, the normalized rows to xn_out when given)
+    int batch_input(const dwim_weight *const *ws, dwim_buf *const *outs, int count, const dwim_buf *norm_w, size_t n,
+                    int in_set, dwim_buf *xn_out) {
+        float *o[4];
+        for (int i = 0; i < count; i++) o[i] = outs[i]->data;
+        StreamExtra se;
+        se.in_area = in_set;
+        se.rms = in_set >= 0;
+        se.eps = c.eps;
+        se.rms_out = in_set >= 0 ? row_scales->data : nullptr;
+        DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, ws, o, nullptr, count, 0, in_set >= 0 ? nullptr : x->data, n,
+                                           norm_w->data, c.eps, xn_out ? xn_out->data : nullptr, nullptr, &se));
+        return 0;
+    }
+    // x += w · in (in's planes made here: of in, or the DeltaNet output gate
+    // with gate_z), handing x·mlp_norm on in the second set
+    int batch_residual(const dwim_weight *w, const dwim_buf *in, size_t n, const dwim_buf *norm_w,
+                       const dwim_buf *gate_z, const dwim_buf *emit_norm) {
+        float *o = x->data;
+        const int add = 1;
+        StreamExtra se;
+        se.emit_area = kBatchArea2;
+        se.emit_norm = emit_norm->data;
+        DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, &w, &o, &add, 1, 0, in->data, n, norm_w ? norm_w->data : nullptr,
+                                           c.eps, nullptr, gate_z ? gate_z->data : nullptr, &se));
+        return 0;
+    }
+    // the SwiGLU pair and the down product over handed-over planes
+    int batch_ffn(const Layer &l, size_t n, const Layer *next) {
+        {
+            const dwim_weight *ws[2] = {l.gate, l.up};
+            float *o[2] = {up->data, nullptr};
+            StreamExtra se;
+            se.in_area = kBatchArea2;
+            se.rms = 1;
+            se.eps = c.eps;
+            se.emit_area = kBatchArea;
+            DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, ws, o, nullptr, 2, 1, nullptr, n, nullptr, c.eps, nullptr, nullptr,
+                                               &se));
+        }
+        float *o = x->data;
+        const int add = 1;
+        StreamExtra se;
+        se.in_area = kBatchArea;
+        if (next && batch_hand(*next, n)) {
+            se.emit_area = kBatchArea2;
+            se.emit_norm = next->attn_norm->data;
+            se.emit_xw = next->attention ? nullptr : xh->data;
+        }
+        DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, &l.down, &o, &add, 1, 0, nullptr, n, nullptr, c.eps, nullptr, nullptr,
+                                           &se));
+        batch_in = se.emit_area;
+        return 0;
+    }
+
     // The one-token layer on the handover path (Pass::layer, qwen35/mod.rs:
     // 541-655, in the same order); `next` is the following layer's input
     // norm, to hand its input over, or null.
@@ -386,11 +458,14 @@ struct dwim_model {
 
     // Pass::layer (qwen35/mod.rs:541-655).  Verifying, the linear layers
     // save their inputs and run a copy of their recurrent state (:606-632).
-    int layer(const Layer &l, size_t n, size_t pos, bool verify = false, const dwim_buf *next = nullptr) {
+    int layer(const Layer &l, size_t n, size_t pos, bool verify = false, const Layer *next = nullptr) {
         const float eps = c.eps;
         const bool fused = fusable(l), one = fused && n == 1;
-        if (one && !verify) return layer_one(l, pos, next);
+        if (one && !verify) return layer_one(l, pos, next ? next->attn_norm : nullptr);
         handed = false;
+        const bool bh = batch_hand(l, n);
+        const int in_set = bh ? batch_in : -1;
+        batch_in = -1;
         TRY(dwim_resize(dev, xh, n * c.hidden));
         if (!fused) TRY(normalize(xh, x, l.attn_norm, n));
         if (l.attention) {
@@ -403,12 +478,18 @@ struct dwim_model {
             if (fused) {
                 const dwim_weight *ws[4] = {l.q, l.qgate, l.k, l.v};
                 dwim_buf *outs[4] = {q, gate, k, v};
-                TRY(projections(ws, outs, 4, l.attn_norm, n, nullptr));
+                if (bh)
+                    TRY(batch_input(ws, outs, 4, l.attn_norm, n, in_set, nullptr));
+                else
+                    TRY(projections(ws, outs, 4, l.attn_norm, n, nullptr));
                 DWIM_HIP(launch_qk_prep(dev->stream, q->data, k->data, v->data, l.q_norm->data, l.k_norm->data,
                                         rope->data, n, pos, c.heads, c.kv_heads, c.head_dim, c.rot_dim, eps, kc, vc));
                 DWIM_HIP(launch_attention_gated(dev, att->data, q->data, kc, vc, n, pos, c.heads, c.head_dim,
                                                 c.kv_heads, gate->data, -1));
-                TRY(dwim_matmul_add(dev, x, l.o, att, xb));
+                if (bh)
+                    TRY(batch_residual(l.o, att, n, nullptr, nullptr, l.mlp_norm));
+                else
+                    TRY(dwim_matmul_add(dev, x, l.o, att, xb));
             } else {
                 TRY(dwim_matmul(dev, q, l.q, xh));
                 TRY(dwim_matmul(dev, gate, l.qgate, xh));
@@ -449,6 +530,12 @@ struct dwim_model {
                     TRY(projections(ws, outs, 2, l.attn_norm, n, nullptr));
                     TRY(dwim_resize(dev, ab_in, n * 2 * c.v_heads));
                     DWIM_HIP(gemm_run_bf16(dev, l.ab, ab_in->data, n, 0));
+                } else if (bh) {
+                    // (handed over: xh holds x·attn_norm, the gate rows scale
+                    // by the row scales the qkv product writes)
+                    TRY(batch_input(ws, outs, 2, l.attn_norm, n, in_set, xh));
+                    DWIM_HIP(launch_rows_bf16(dev, l.ab, ab_in->data, xh->data, n,
+                                              in_set >= 0 ? row_scales->data : nullptr));
                 } else {
                     TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
                     TRY(dwim_matmul(dev, ab_in, l.ab, xh));
@@ -482,6 +569,8 @@ struct dwim_model {
                     // the gated norm made in the out product's split
                     DWIM_HIP(gemm_prepare_gated(dev, z->data, att->data, l.norm->data, eps, n, v_dim(), c.state_dim));
                     DWIM_HIP(gemm_run(dev, l.out, x->data, n, kGemmAdd));
+                } else if (bh) {
+                    TRY(batch_residual(l.out, att, n, l.norm, z, l.mlp_norm));
                 } else if (l.out->fmt == DWIM_Q4_K && c.state_dim == 128) {
                     // the gated norm made with the out product's planes
                     const int add = 1;
@@ -515,6 +604,7 @@ struct dwim_model {
                                     up->data));
             return 0;
         }
+        if (bh) return batch_ffn(l, n, next);
         if (fused) {
             DWIM_HIP(launch_swiglu_q4k(dev, l.gate, l.up, up->data, x->data, n, l.mlp_norm->data, eps));
         } else {
@@ -549,6 +639,7 @@ struct dwim_model {
         TRY(dwim_matmul(dev, xb, draft.hidden_proj, xh));
         TRY(dwim_add(dev, x, xb));
         handed = false;
+        batch_in = -1;
         TRY(layer(draft.layer, rows, pos));
         return normalize(xh, x, draft.norm, rows);
     }
@@ -582,8 +673,9 @@ struct dwim_model {
             TRY(dwim_embed(dev, x, embd, tokens, n));
         }
         handed = false;
+        batch_in = -1;
         for (size_t i = 0; i < layers.size(); i++)
-            TRY(layer(layers[i], n, pos, verify, i + 1 < layers.size() ? layers[i + 1].attn_norm : nullptr));
+            TRY(layer(layers[i], n, pos, verify, i + 1 < layers.size() ? &layers[i + 1] : nullptr));
         if (!verify) seq.parity = !seq.parity;
         const size_t h = c.hidden;
         if (!has_draft) {
@@ -1079,7 +1171,7 @@ extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg
         if (m->buf(m->most * m->widths[i], b[i])) return 1;
     if (m->buf(m->most * c.intermediate, &m->up) || m->buf(m->most * c.intermediate, &m->gate_ffn) ||
         m->buf((c.drafter ? kMaxDrafts + 1 : 1) * c.vocab, &m->logits) || m->buf(c.hidden, &m->drafted) ||
-        m->buf(4 * c.v_heads, &m->head_ss))
+        m->buf(4 * c.v_heads, &m->head_ss) || m->buf(4, &m->row_scales))
         return 1;
     std::vector<float> table;
     rope_table(table, max_len, c.rot_dim, c.rope_theta);

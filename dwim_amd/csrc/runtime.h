@@ -171,16 +171,44 @@ hipError_t launch_mv_q4k_mfma(dwim_dev *dev, const dwim_weight *const *ws, float
 // (RMS-normalized by `norm` when given, the normalized rows to xn_out when
 // that is given) in the batch areas, then outs[j] ([n][rows_j]) += or = W_j·x
 // by adds[j], or a SwiGLU pair into outs[0] as launch_mv_q4k_mfma.
-// 2..4 tokens whose planes (pair mode) are at xq[t], xstat[t]: outs[j]
-// ([nt][rows_j]) += or = W_j·x, or a SwiGLU pair into outs[0], every weight
-// read once (k_mv_q4k_stream.hip)
+// Plane areas: 0 and 1 for one token's products (each reads one and writes
+// the other); kBatchArea + t for token t of a 2..4-token launch, and a
+// second such set at kBatchArea2, so that a batch product that reads one set
+// hands its results' planes on in the other.
+constexpr int kBatchArea = 2;
+constexpr int kBatchArea2 = kBatchArea + 4;
+// Optional parts of a 2..4-token product (one launch), as MvExtra's for one
+// token: in_area >= 0, the tokens' planes are already in areas in_area + t
+// (written by the product before, per 16 or per 32 activations) and nothing
+// is made from x; rms, those planes are x·w with Σx² per group, every
+// token's results scaled by 1/sqrt(Σx²/cols + eps) (and the scales to
+// rms_out[t] when given); emit_area >= 0 (one matrix or a SwiGLU pair, rows
+// whole 256-blocks), token t's planes of outs[0] (after the add or the
+// SwiGLU) go to area emit_area + t, of outs[0]·emit_norm with Σ outs[0]² per
+// group when emit_norm is given (and outs[0]·emit_norm in f32 to emit_xw,
+// [nt][rows], when that is given).
+struct StreamExtra {
+    int in_area = -1;
+    int rms = 0;
+    float eps = 0.0f;
+    float *rms_out = nullptr;
+    int emit_area = -1;
+    const float *emit_norm = nullptr;
+    float *emit_xw = nullptr;
+};
+// 2..4 tokens whose planes (per 16 or per 32 activations) are at xq[t],
+// xstat[t]: outs[j] ([nt][rows_j]) += or = W_j·x, or a SwiGLU pair into
+// outs[0], every weight read once (k_mv_q4k_stream.hip); se's rms and emit
+// parts apply (its in_area is the caller's)
 hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds, int count,
-                         int swiglu, size_t nt, const int8_t *const *xq, const float *const *xstat);
+                         int swiglu, size_t nt, const int8_t *const *xq, const float *const *xstat,
+                         const StreamExtra *se = nullptr);
 // (gate_z given: the input is the DeltaNet output gate silu(gate_z)·
 // rmsnorm(x)·norm over heads of 128, made with the planes; xn_out unused)
+// (se given: n <= 4, one launch with se's parts)
 hipError_t launch_mv_q4k_mfma_tokens(dwim_dev *dev, const dwim_weight *const *ws, float *const *outs, const int *adds,
                                      int count, int swiglu, const float *x, size_t n, const float *norm, float eps,
-                                     float *xn_out, const float *gate_z = nullptr);
+                                     float *xn_out, const float *gate_z = nullptr, const StreamExtra *se = nullptr);
 // The planes of nt <= 4 rows of x ([nt][cols]) in the batch areas, one launch;
 // views[t] is token t's (pair: per-32 scales)
 hipError_t launch_planes_batch(dwim_dev *dev, const float *x, size_t cols, size_t nt, int pair, planes::View *views);
@@ -192,6 +220,10 @@ hipError_t launch_mv_q6k_mfma(dwim_dev *dev, const dwim_weight *w, float *out, i
 hipError_t launch_mv_q6k_tokens(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
+// out ([n][rows]) = W·x for a bf16 weight of few rows and n < 16 tokens, each
+// token's results times row_scale[t] when that is given
+hipError_t launch_rows_bf16(dwim_dev *dev, const dwim_weight *wt, float *out, const float *x, size_t n,
+                           const float *row_scale);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                             const dwim_cache *v, size_t n, size_t pos, size_t n_heads,
                             size_t head_dim, size_t n_kv_heads);
