@@ -679,7 +679,11 @@ __global__ void __launch_bounds__(kCThreads) k_attn_combine(float *__restrict__ 
         o.w *= sigmoidf_(gv.w);
     }
     *(float4 *)(out + i) = o;
-    if (pv.q) planes::write4x4(pv, i / 4, o);  // a group of 16 is 4 lanes
+    if (pv.q) {
+        // token t's planes in the t-th area from pv's (a group of 16 is 4 lanes)
+        const planes::View pt = t ? planes::view(pv.q + t * planes::kAreaBytes, pv.cols) : pv;
+        planes::write4x4(pt, (h * D + e0) / 4, o);
+    }
 }
 
 // ---------------------------------------------------------------- prefill
@@ -1072,7 +1076,9 @@ hipError_t launch_attention_gated(dwim_dev *dev, float *out, const float *q, con
     if (!attention_shape_ok(n_heads, head_dim, n_kv_heads)) return hipErrorInvalidValue;
     planes::View pv{};
     if (area >= 0) {
-        if (n != 1 || head_dim % 32 || n_heads * head_dim > planes::kMaxCols || (n_heads * head_dim) % 256)
+        // one token's planes, or 2..4 tokens' in a set of batch areas
+        const bool areas_ok = n == 1 || (n <= 4 && (area == kBatchArea || area == kBatchArea2));
+        if (!areas_ok || head_dim % 32 || n_heads * head_dim > planes::kMaxCols || (n_heads * head_dim) % 256)
             return hipErrorInvalidValue;
         pv = planes_area(dev, area, n_heads * head_dim);
         dev->prepared = 0;

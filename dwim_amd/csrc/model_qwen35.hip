@@ -355,17 +355,20 @@ struct dwim_model {
                                            norm_w->data, c.eps, xn_out ? xn_out->data : nullptr, nullptr, &se));
         return 0;
     }
-    // x += w · in (in's planes made here: of in, or the DeltaNet output gate
-    // with gate_z), handing x·mlp_norm on in the second set
+    // x += w · in, handing x·mlp_norm on in the second set: in's planes made
+    // here (of in, or the DeltaNet output gate with gate_z), or (in null)
+    // already in the first set, written by the attention merge
     int batch_residual(const dwim_weight *w, const dwim_buf *in, size_t n, const dwim_buf *norm_w,
                        const dwim_buf *gate_z, const dwim_buf *emit_norm) {
         float *o = x->data;
         const int add = 1;
         StreamExtra se;
+        se.in_area = in ? -1 : kBatchArea;
         se.emit_area = kBatchArea2;
         se.emit_norm = emit_norm->data;
-        DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, &w, &o, &add, 1, 0, in->data, n, norm_w ? norm_w->data : nullptr,
-                                           c.eps, nullptr, gate_z ? gate_z->data : nullptr, &se));
+        DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, &w, &o, &add, 1, 0, in ? in->data : nullptr, n,
+                                           norm_w ? norm_w->data : nullptr, c.eps, nullptr,
+                                           gate_z ? gate_z->data : nullptr, &se));
         return 0;
     }
     // the SwiGLU pair and the down product over handed-over planes
@@ -485,9 +488,9 @@ struct dwim_model {
                 DWIM_HIP(launch_qk_prep(dev->stream, q->data, k->data, v->data, l.q_norm->data, l.k_norm->data,
                                         rope->data, n, pos, c.heads, c.kv_heads, c.head_dim, c.rot_dim, eps, kc, vc));
                 DWIM_HIP(launch_attention_gated(dev, att->data, q->data, kc, vc, n, pos, c.heads, c.head_dim,
-                                                c.kv_heads, gate->data, -1));
+                                                c.kv_heads, gate->data, bh ? kBatchArea : -1));
                 if (bh)
-                    TRY(batch_residual(l.o, att, n, nullptr, nullptr, l.mlp_norm));
+                    TRY(batch_residual(l.o, nullptr, n, nullptr, nullptr, l.mlp_norm));
                 else
                     TRY(dwim_matmul_add(dev, x, l.o, att, xb));
             } else {
