@@ -349,17 +349,19 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
         const float o = sum16(o0 + o1) * scale;
         if (p == 0 && out) out[((size_t)t * n_v_heads + h) * kD + c0 + c] = o;
         if (t + 1 < n && t < kMaxSteps && steps.state[t]) {
-            // the state after token t, for a rewind that keeps t + 1 tokens,
-            // straight from the registers (no barrier: the token loop goes on
-            // while the stores drain)
-            float *St = steps.state[t] + (size_t)h * kD * kD + c0 + c;
+            // the state after token t, for a rewind that keeps t + 1 tokens
+            // (through LDS, a row's 16 columns in one run, as at the end)
+            float *St = steps.state[t] + (size_t)h * kD * kD;
+            __syncthreads();  // (the previous step's copy is done with the tile)
 #pragma unroll
-            for (int i = 0; i < kKeys; i++) St[(size_t)(p * kKeys + i) * kD] = s[i];
+            for (int i = 0; i < kKeys; i++) tile[p * kKeys + i][c] = s[i];
+            __syncthreads();
+            for (int e = tid; e < kD * kCols; e += kThreads) St[(e / kCols) * kD + c0 + e % kCols] = tile[e / kCols][e % kCols];
         }
     }
 
-    // ---- the state slice out, through LDS (every read of the tile was
-    // before the barrier ahead of the token loop)
+    // ---- the state slice out, through LDS
+    __syncthreads();  // (a step's copy may still read the tile)
 #pragma unroll
     for (int i = 0; i < kKeys; i++) tile[p * kKeys + i][c] = s[i];
     __syncthreads();
