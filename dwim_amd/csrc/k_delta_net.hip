@@ -17,6 +17,7 @@
 // slice is read from HBM once and written once per call, through LDS so that
 // both are coalesced.
 #include "device_util.h"
+#include "planes.h"
 #include "runtime.h"
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -184,12 +185,13 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
                                                          const float *__restrict__ gates,
                                                          const float *__restrict__ decay, float *state,
                                                          const float *state_in, int n, int n_k_heads, int n_v_heads,
-                                                         float eps, GdnSteps steps) {
+                                                         float eps, GdnSteps steps, GdnGate gg) {
     __shared__ float kqs[2][kSmallT][kD];          // normalized k, q of each token
     __shared__ float tile[kD][kCols + 1];          // the state slice's staging
     __shared__ float vs[kSmallT][kCols];
     __shared__ float2 gb[kSmallT];
     __shared__ float red[kSmallT][kThreads / 64];
+    __shared__ float o_s[4][kCols];  // (with gg.planes: the first 4 tokens' o)
     const int h = blockIdx.y, c0 = blockIdx.x * kCols, tid = threadIdx.x;
     const int ratio = n_v_heads / n_k_heads, kh = h / ratio;
     const int c = tid / kParts, p = tid % kParts;
@@ -229,6 +231,12 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
 #pragma unroll
         for (int t = 0; t < kSmallT; t++) vw[3 + t] = t < n ? qkv[(size_t)t * ch + vc] : 0.0f;
         vwt = ((const float4 *)conv_w)[vc];
+    }
+    // (with gg.planes: wave 0, lane 16t + c, takes token t's column c at the end)
+    float zv = 0.0f, nwv = 0.0f;
+    if (gg.planes && tid < 64 && (tid >> 4) < n) {
+        zv = gg.z[(size_t)(tid >> 4) * n_v_heads * kD + (size_t)h * kD + c0 + (tid & 15)];
+        nwv = gg.norm_w[c0 + (tid & 15)];
     }
     float g_alpha = 0.0f, g_beta = 0.0f;
     if (tid < n) {
@@ -348,6 +356,7 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
         }
         const float o = sum16(o0 + o1) * scale;
         if (p == 0 && out) out[((size_t)t * n_v_heads + h) * kD + c0 + c] = o;
+        if (p == 0 && gg.planes && t < 4) o_s[t][c] = o;
         if (t + 1 < n && t < kMaxSteps && steps.state[t]) {
             // the state after token t, for a rewind that keeps t + 1 tokens
             // (through LDS, a row's 16 columns in one run, as at the end)
@@ -361,7 +370,18 @@ __global__ void __launch_bounds__(kThreads) k_gdn_tokens(float *__restrict__ out
     }
 
     // ---- the state slice out, through LDS
-    __syncthreads();  // (a step's copy may still read the tile)
+    __syncthreads();  // (a step's copy may still read the tile; o_s is written)
+    if (gg.planes && tid < 64 && (tid >> 4) < n) {
+        // token t's gated output of the block's 16 columns as one planes group
+        // (whole groups of 16 lanes), unnormalized, and their Σo²
+        const int t = tid >> 4, cc = tid & 15;
+        const float ov = o_s[t][cc];
+        const float ss = group_sum<16>(ov * ov);
+        if (cc == 0) gg.head_ss[((size_t)t * n_v_heads + h) * (kD / kCols) + blockIdx.x] = ss;
+        const float r = zv * sigmoidf_(zv) * (ov * nwv);
+        planes::write16(planes::view(gg.planes + (size_t)t * planes::kAreaBytes, (size_t)n_v_heads * kD),
+                        (size_t)h * kD + c0 + cc, r);
+    }
 #pragma unroll
     for (int i = 0; i < kKeys; i++) tile[p * kKeys + i][c] = s[i];
     __syncthreads();
@@ -742,13 +762,17 @@ hipError_t delta_net_reserve(dwim_dev *dev, size_t n, size_t n_v_heads) {
 hipError_t launch_gdn_tokens(dwim_dev *dev, float *out, const float *qkv, const float *conv_state,
                              float *conv_state_out, const float *conv_w, const float *gates, const float *decay,
                              float *state, const float *state_in, size_t n, size_t n_k_heads, size_t n_v_heads,
-                             size_t head_dim, float eps, const GdnSteps *steps) {
+                             size_t head_dim, float eps, const GdnSteps *steps, const GdnGate *gate) {
     if (head_dim != kD || n < 1 || n > (size_t)kSmallT || n_k_heads == 0 || n_v_heads % n_k_heads)
+        return hipErrorInvalidValue;
+    if (gate && (n > 4 || !gate->z || !gate->norm_w || !gate->planes || !gate->head_ss ||
+                 n_v_heads * kD > planes::kMaxCols || (n_v_heads * kD) % 256))
         return hipErrorInvalidValue;
     dim3 grid(kD / kCols, (unsigned)n_v_heads);
     k_gdn_tokens<<<grid, kThreads, 0, dev->stream>>>(out, qkv, conv_state, conv_state_out, conv_w, gates, decay, state,
                                                      state_in ? state_in : state, (int)n, (int)n_k_heads,
-                                                     (int)n_v_heads, eps, steps ? *steps : GdnSteps{});
+                                                     (int)n_v_heads, eps, steps ? *steps : GdnSteps{},
+                                                     gate ? *gate : GdnGate{});
     return hipGetLastError();
 }
 

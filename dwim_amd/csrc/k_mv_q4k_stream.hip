@@ -93,6 +93,12 @@ struct StreamArgs {
     const float *rss[kTok];
     float eps;
     float *rms_out;
+    // given: the planes hold heads of 128 columns unnormalized, the groups of
+    // token t's head k scaled by 1/sqrt(Σ hss[t][k][0..7] / 128 + heps)
+    // (hss: [NT][heads][8] partial sums of squares)
+    const float *hss;
+    float heps;
+    unsigned heads;
     // given (one matrix or a SwiGLU pair, rows whole 256-blocks): token t's
     // planes of the results, after the add or the SwiGLU, into the plane area
     // at emit + t·kAreaBytes; of results·emit_norm with Σ results² per group
@@ -173,17 +179,19 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
 
     // LDS: planes [block][token][51 chunks], statistics [block][token][8],
     // the zero region, per wave the decoded scales, the tokens' RMS scales
-    // (one chunk), the items' sums
+    // (one chunk), the tokens' head norms ([NT][heads] floats), the items' sums
     const unsigned kStat = a.plane_cap * NT * kBT;
     const unsigned kZero = kStat + a.plane_cap * NT * 8;
     const unsigned kHdr = kZero + kK * NT * kBT;
     const unsigned kTsc = kHdr + kW * kHdrChunks;
-    const unsigned kSlots = kTsc + 1;
+    const unsigned kTf = kTsc + 1;
+    const unsigned kSlots = kTf + (NT * a.heads + 3) / 4;
     v4i *lv = (v4i *)lds;
     const float4 *stl = (const float4 *)(lds + kStat);
     float *hdr = (float *)(lds + kHdr + wave * kHdrChunks);
     float *slots = (float *)(lds + kSlots);  // [item - i0][NT][16]
     float *tsc = (float *)(lds + kTsc);
+    float *tf = (float *)(lds + kTf);
 
     auto item_of = [=](unsigned i) {
         Item it;
@@ -416,6 +424,10 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
         rsw = wave == q ? rq : rsw;
     }
     float rsv[kRssLoads];
+    // the head norms (given): thread (token, head) of the first NT·heads
+    const bool hnorm = a.hss != nullptr;
+    const unsigned nth = NT * a.heads;
+    float4 hs0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), hs1 = hs0;
     {
         // a run of global memory a wave: token t's digit p (PB·16 chunks at
         // xq[t] + p·cols + pb·256) for run 4t + p, its statistics (PB·8 chunks
@@ -471,6 +483,10 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
                 rsv[u] = rsw[gi < ngr ? gi : 0u];
             }
         }
+        if (hnorm && threadIdx.x < nth) {
+            hs0 = ((const float4 *)a.hss)[2 * threadIdx.x];
+            hs1 = ((const float4 *)a.hss)[2 * threadIdx.x + 1];
+        }
         if (staging) {
 #pragma unroll
             for (int u = 0; u < kSL; u++) {
@@ -485,6 +501,9 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
         }
         if (threadIdx.x < (unsigned)(kK * NT * kBT)) lv[kZero + threadIdx.x] = v4i{0, 0, 0, 0};
     }
+    if (hnorm && threadIdx.x < nth)
+        tf[threadIdx.x] = 1.0f / sqrtf((((hs0.x + hs0.y) + (hs0.z + hs0.w)) + ((hs1.x + hs1.y) + (hs1.z + hs1.w))) / 128.0f +
+                                       a.heps);
     if (rms && wave < NT) {
         float t = 0.0f;
 #pragma unroll
@@ -499,6 +518,23 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
         }
     }
     __syncthreads();
+    if (hnorm) {
+        // each statistics chunk (the scales or the sums of a 64-column run)
+        // times its token's head norm
+        for (unsigned e = threadIdx.x; e < PB * NT * 8u; e += kW * 64u) {
+            const unsigned blk = e / (NT * 8u), t = (e / 8u) % NT, k = e % 8u;
+            const unsigned head = ((pb + blk) * 4u + k / 2u) / 2u;
+            const float f = tf[t * a.heads + head];
+            float4 *ch = (float4 *)(lds + kStat) + e;
+            float4 v = *ch;
+            v.x *= f;
+            v.y *= f;
+            v.z *= f;
+            v.w *= f;
+            *ch = v;
+        }
+        __syncthreads();
+    }
 
     // ---- the wave's items, the next one's weights in flight
     // (the loads are unconditional, past the last item a reload of it, so
@@ -713,6 +749,13 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
         a.eps = se->eps;
         a.rms_out = se->rms_out;
     }
+    if (se && se->head_ss) {
+        if (ws[0]->cols % 128) return hipErrorInvalidValue;
+        a.hss = se->head_ss;
+        a.heps = se->head_eps;
+        a.heads = (unsigned)(ws[0]->cols / 128);
+        if (NT * a.heads > (unsigned)(kW * 64)) return hipErrorInvalidValue;
+    }
     if (se && se->emit_area >= 0) {
         const size_t rows = ws[0]->rows;
         if ((njobs != 1 && !swiglu) || rows % 256 || rows > planes::kMaxCols || se->emit_area < 0 ||
@@ -722,7 +765,8 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
         a.emit_norm = se->emit_norm;
         a.emit_xw = se->emit_xw;
     }
-    const size_t lds = ((size_t)plane_cap * NT * (kBT + 8) + (size_t)K * NT * kBT + (size_t)kW * kHdrChunks + 1) * 16 +
+    const size_t lds = ((size_t)plane_cap * NT * (kBT + 8) + (size_t)K * NT * kBT + (size_t)kW * kHdrChunks + 1 +
+                        (NT * a.heads + 3) / 4) * 16 +
                        (size_t)items_cap * NT * 16 * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     // raised once a process for each kernel (a function-local static is

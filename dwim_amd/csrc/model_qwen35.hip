@@ -96,8 +96,9 @@ struct dwim_model {
     dwim_buf *up = nullptr, *gate_ffn = nullptr, *logits = nullptr, *rope = nullptr, *drafted = nullptr;
     // the one-token DeltaNet step's Σo² per head quarter ([v_heads][4])
     dwim_buf *head_ss = nullptr;
-    // a 2..4-token batch's RMS scales of its handed-over layer input ([4])
-    dwim_buf *row_scales = nullptr;
+    // a 2..4-token batch's RMS scales of its handed-over layer input ([4]),
+    // and its DeltaNet output gate's Σo² per 16 columns ([4][v_heads][8])
+    dwim_buf *row_scales = nullptr, *batch_hss = nullptr;
     // device-fed greedy decoding: the picks, and where the step running
     // reads its token and writes its pick (null outside decode_greedy)
     uint32_t *picks = nullptr;
@@ -357,13 +358,16 @@ struct dwim_model {
     }
     // x += w · in, handing x·mlp_norm on in the second set: in's planes made
     // here (of in, or the DeltaNet output gate with gate_z), or (in null)
-    // already in the first set, written by the attention merge
+    // already in the first set, written by the attention merge or (with
+    // head_ss) by the DeltaNet step, heads unnormalized
     int batch_residual(const dwim_weight *w, const dwim_buf *in, size_t n, const dwim_buf *norm_w,
-                       const dwim_buf *gate_z, const dwim_buf *emit_norm) {
+                       const dwim_buf *gate_z, const dwim_buf *emit_norm, const dwim_buf *hss = nullptr) {
         float *o = x->data;
         const int add = 1;
         StreamExtra se;
         se.in_area = in ? -1 : kBatchArea;
+        se.head_ss = hss ? hss->data : nullptr;
+        se.head_eps = c.eps;
         se.emit_area = kBatchArea2;
         se.emit_norm = emit_norm->data;
         DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, &w, &o, &add, 1, 0, in ? in->data : nullptr, n,
@@ -553,10 +557,18 @@ struct dwim_model {
                             st.state[t] = ssm_step[t][l.slot]->data;
                             st.conv[t] = conv_step[t][l.slot]->data;
                         }
+                    // (handing over: its output gate's planes, heads unnormalized)
+                    GdnGate gg;
+                    if (bh) {
+                        gg.z = z->data;
+                        gg.norm_w = l.norm->data;
+                        gg.planes = planes_area(dev, kBatchArea, v_dim()).q;
+                        gg.head_ss = batch_hss->data;
+                    }
                     DWIM_HIP(launch_gdn_tokens(dev, att->data, qkv_in->data, state->data, state_out->data,
                                                l.conv->data, ab_in->data, l.decay->data, ssm->data,
                                                verify ? seq.ssm_state[l.slot]->data : nullptr, n, c.k_heads,
-                                               c.v_heads, c.state_dim, eps, &st));
+                                               c.v_heads, c.state_dim, eps, &st, bh ? &gg : nullptr));
                 } else {
                     TRY(dwim_conv_l2norm(dev, q, k, v, state_out, qkv_in, state, l.conv, c.state_dim, eps));
                     if (verify) {
@@ -573,7 +585,7 @@ struct dwim_model {
                     DWIM_HIP(gemm_prepare_gated(dev, z->data, att->data, l.norm->data, eps, n, v_dim(), c.state_dim));
                     DWIM_HIP(gemm_run(dev, l.out, x->data, n, kGemmAdd));
                 } else if (bh) {
-                    TRY(batch_residual(l.out, att, n, l.norm, z, l.mlp_norm));
+                    TRY(batch_residual(l.out, nullptr, n, nullptr, nullptr, l.mlp_norm, batch_hss));
                 } else if (l.out->fmt == DWIM_Q4_K && c.state_dim == 128) {
                     // the gated norm made with the out product's planes
                     const int add = 1;
@@ -1174,7 +1186,8 @@ extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg
         if (m->buf(m->most * m->widths[i], b[i])) return 1;
     if (m->buf(m->most * c.intermediate, &m->up) || m->buf(m->most * c.intermediate, &m->gate_ffn) ||
         m->buf((c.drafter ? kMaxDrafts + 1 : 1) * c.vocab, &m->logits) || m->buf(c.hidden, &m->drafted) ||
-        m->buf(4 * c.v_heads, &m->head_ss) || m->buf(4, &m->row_scales))
+        m->buf(4 * c.v_heads, &m->head_ss) || m->buf(4, &m->row_scales) ||
+        m->buf(4 * c.v_heads * 8, &m->batch_hss))
         return 1;
     std::vector<float> table;
     rope_table(table, max_len, c.rot_dim, c.rope_theta);

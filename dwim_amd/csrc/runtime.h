@@ -192,6 +192,11 @@ struct StreamExtra {
     int rms = 0;
     float eps = 0.0f;
     float *rms_out = nullptr;
+    // given: the planes hold heads of 128 columns unnormalized (a DeltaNet
+    // output gate), each scaled here by 1/sqrt(Σ head_ss[t][head][0..7] /
+    // 128 + head_eps)
+    const float *head_ss = nullptr;
+    float head_eps = 0.0f;
     int emit_area = -1;
     const float *emit_norm = nullptr;
     float *emit_xw = nullptr;
@@ -255,10 +260,21 @@ struct GdnSteps {
     float *state[kMaxSteps];
     float *conv[kMaxSteps];
 };
+// And given (n <= 4): the mixer's output gate silu(z)·o·norm_w of each
+// token (z [n][nv·D]), unnormalized, as token t's planes in the plane area
+// at planes + t·kAreaBytes, and each 16 columns' Σo² to head_ss
+// [n][nv][D / 16]: the consuming product applies each head's RMS norm.
+struct GdnGate {
+    const float *z = nullptr;
+    const float *norm_w = nullptr;
+    int8_t *planes = nullptr;
+    float *head_ss = nullptr;
+};
 hipError_t launch_gdn_tokens(dwim_dev *dev, float *out, const float *qkv, const float *conv_state,
                              float *conv_state_out, const float *conv_w, const float *gates, const float *decay,
                              float *state, const float *state_in, size_t n, size_t n_k_heads, size_t n_v_heads,
-                             size_t head_dim, float eps, const GdnSteps *steps = nullptr);
+                             size_t head_dim, float eps, const GdnSteps *steps = nullptr,
+                             const GdnGate *gate = nullptr);
 hipError_t launch_delta_net(dwim_dev *dev, float *out, const float *q, const float *k,
                             const float *v, const float *gates, const float *decay, float *state,
                             size_t n, size_t n_k_heads, size_t n_v_heads, size_t head_dim, const Rms *rms = nullptr,
