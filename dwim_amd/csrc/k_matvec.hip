@@ -328,7 +328,7 @@ constexpr int kRowTok = 4;
 
 __global__ void __launch_bounds__(256) k_rows_bf16(const uint16_t *__restrict__ w, const float *__restrict__ x,
                                                    float *__restrict__ out, size_t rows, size_t cols, size_t n,
-                                                   int add, const float *row_scale = nullptr) {
+                                                   int add) {
     __shared__ float part[kRowTok][4];
     const size_t row = blockIdx.x, t0 = (size_t)blockIdx.y * kRowTok;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -359,8 +359,7 @@ __global__ void __launch_bounds__(256) k_rows_bf16(const uint16_t *__restrict__ 
     }
     __syncthreads();
     if (tid < nt) {
-        float v = (part[tid][0] + part[tid][1]) + (part[tid][2] + part[tid][3]);
-        if (row_scale) v *= row_scale[t0 + tid];
+        const float v = (part[tid][0] + part[tid][1]) + (part[tid][2] + part[tid][3]);
         float *o = out + (t0 + tid) * rows + row;
         *o = add ? *o + v : v;
     }
@@ -396,14 +395,6 @@ hipError_t launch_matvec(dwim_dev *dev, const dwim_weight *wt, float *out, const
         }
         return launch_fmt<DWIM_BF16>(s, w, x, out, n, add);
     }
-}
-
-hipError_t launch_rows_bf16(dwim_dev *dev, const dwim_weight *wt, float *out, const float *x, size_t n,
-                           const float *row_scale) {
-    if (wt->fmt != DWIM_BF16 || n < 1 || n >= 16 || wt->rows > kSkRows || wt->cols % 8) return hipErrorInvalidValue;
-    k_rows_bf16<<<dim3((unsigned)wt->rows, (unsigned)((n + kRowTok - 1) / kRowTok)), 256, 0, dev->stream>>>(
-        (const uint16_t *)wt->q, x, out, wt->rows, wt->cols, n, 0, row_scale);
-    return hipGetLastError();
 }
 
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out, float *scratch,

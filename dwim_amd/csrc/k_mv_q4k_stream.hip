@@ -88,17 +88,23 @@ struct StreamArgs {
     float *partials;             // [tile][part][cmax][NT][32]
     unsigned *counters;          // [tile], zero between launches
     // given: the planes are x·w with Σx² per group (rss[t], [cols/16]), and
-    // token t's results scale by 1/sqrt(Σ rss[t] / cols + eps) (workgroup 0
-    // writes the scales to rms_out[t] when that is given)
+    // token t's results scale by 1/sqrt(Σ rss[t] / cols + eps)
     const float *rss[kTok];
     float eps;
-    float *rms_out;
     // given: the planes hold heads of 128 columns unnormalized, the groups of
     // token t's head k scaled by 1/sqrt(Σ hss[t][k][0..7] / 128 + heps)
     // (hss: [NT][heads][8] partial sums of squares)
     const float *hss;
     float heps;
     unsigned heads;
+    // given: bf_out[t][r] = bf_w[r] · bf_x[t] (a small bf16 matrix [bf_rows]
+    // [bf_cols] against f32 rows, times token t's RMS scale when the planes
+    // are RMS-scaled): (row, token) pairs g + grid·k, g + grid·(k + 4), ... by
+    // wave kW − 4 + k of workgroup g, after its tiles
+    const uint16_t *bf_w;
+    const float *bf_x;
+    float *bf_out;
+    unsigned bf_rows, bf_cols;
     // given (one matrix or a SwiGLU pair, rows whole 256-blocks): token t's
     // planes of the results, after the add or the SwiGLU, into the plane area
     // at emit + t·kAreaBytes; of results·emit_norm with Σ results² per group
@@ -512,10 +518,7 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
         for (unsigned gi = (unsigned)lane + 64u * kRssLoads; gi < ngr; gi += 64u) t += rsw[gi];
         t = group_sum<64>(t);
         const float sc = 1.0f / sqrtf(t / (float)cols + a.eps);
-        if (lane == 0) {
-            tsc[wave] = sc;
-            if (g == 0 && a.rms_out) a.rms_out[wave] = sc;
-        }
+        if (lane == 0) tsc[wave] = sc;
     }
     __syncthreads();
     if (hnorm) {
@@ -665,6 +668,39 @@ __global__ void __launch_bounds__(1024) k_mv_stream(const StreamArgs a) {
             if (ts + 2 < NT) emit_one((unsigned)ts + 2, e1);
         }
     }
+    // ---- the small bf16 matrix's (row, token) pairs, a wave each: 8 columns
+    // a lane a load, the loads of 5 such steps issued together
+    if (a.bf_w && wave >= kW - 4) {
+        for (unsigned q = g + gridDim.x * (unsigned)(wave - (kW - 4)); q < a.bf_rows * (unsigned)NT; q += 4u * gridDim.x) {
+            const unsigned r = q / (unsigned)NT, t = q % (unsigned)NT;
+            const uint4 *wr = (const uint4 *)(a.bf_w + (size_t)r * a.bf_cols);
+            const float4 *xr = (const float4 *)(a.bf_x + (size_t)t * a.bf_cols);
+            const unsigned n8 = a.bf_cols / 8;
+            float acc = 0.0f;
+            for (unsigned c0 = (unsigned)lane; c0 < n8; c0 += 5 * 64) {
+                uint4 wv[5];
+                float4 x0[5], x1[5];
+#pragma unroll
+                for (int u = 0; u < 5; u++) {
+                    const unsigned cu = c0 + 64u * u < n8 ? c0 + 64u * u : c0;
+                    wv[u] = wr[cu];
+                    x0[u] = xr[2 * cu];
+                    x1[u] = xr[2 * cu + 1];
+                }
+#pragma unroll
+                for (int u = 0; u < 5; u++) {
+                    if (c0 + 64u * u >= n8) continue;
+                    const uint32_t pw[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+                    const float xs[8] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w, x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc += __uint_as_float(pw[i] << 16) * xs[2 * i] + __uint_as_float(pw[i] & 0xffff0000u) * xs[2 * i + 1];
+                }
+            }
+            acc = group_sum<64>(acc);
+            if (lane == 0) a.bf_out[(size_t)t * a.bf_rows + r] = acc * (rms ? tsc[t] : 1.0f);
+        }
+    }
 }
 
 }  // namespace
@@ -747,7 +783,6 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
         // (each token's planes are the start of its plane area)
         for (unsigned t = 0; t < NT; t++) a.rss[t] = (const float *)(xq[t] + planes::kSsOff);
         a.eps = se->eps;
-        a.rms_out = se->rms_out;
     }
     if (se && se->head_ss) {
         if (ws[0]->cols % 128) return hipErrorInvalidValue;
@@ -755,6 +790,15 @@ hipError_t run_mv_stream(dwim_dev *dev, const dwim_weight *const *ws, float *con
         a.heps = se->head_eps;
         a.heads = (unsigned)(ws[0]->cols / 128);
         if (NT * a.heads > (unsigned)(kW * 64)) return hipErrorInvalidValue;
+    }
+    if (se && se->bf16) {
+        const dwim_weight *b = se->bf16;
+        if (b->fmt != DWIM_BF16 || b->cols % 8 || !se->bf16_x || !se->bf16_out) return hipErrorInvalidValue;
+        a.bf_w = (const uint16_t *)b->q;
+        a.bf_x = se->bf16_x;
+        a.bf_out = se->bf16_out;
+        a.bf_rows = (unsigned)b->rows;
+        a.bf_cols = (unsigned)b->cols;
     }
     if (se && se->emit_area >= 0) {
         const size_t rows = ws[0]->rows;

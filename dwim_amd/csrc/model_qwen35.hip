@@ -96,9 +96,9 @@ struct dwim_model {
     dwim_buf *up = nullptr, *gate_ffn = nullptr, *logits = nullptr, *rope = nullptr, *drafted = nullptr;
     // the one-token DeltaNet step's Σo² per head quarter ([v_heads][4])
     dwim_buf *head_ss = nullptr;
-    // a 2..4-token batch's RMS scales of its handed-over layer input ([4]),
-    // and its DeltaNet output gate's Σo² per 16 columns ([4][v_heads][8])
-    dwim_buf *row_scales = nullptr, *batch_hss = nullptr;
+    // a 2..4-token batch's DeltaNet output gate's Σo² per 16 columns
+    // ([4][v_heads][8])
+    dwim_buf *batch_hss = nullptr;
     // device-fed greedy decoding: the picks, and where the step running
     // reads its token and writes its pick (null outside decode_greedy)
     uint32_t *picks = nullptr;
@@ -343,15 +343,21 @@ struct dwim_model {
     }
     // products of the layer input (handed over in `in_set`, or made here from
     // x with the norm, the normalized rows to xn_out when given)
+    // (bf16 given: the same launch writes bf16_out = bf16 · xh, RMS-scaled
+    // like the products, the DeltaNet gate rows)
     int batch_input(const dwim_weight *const *ws, dwim_buf *const *outs, int count, const dwim_buf *norm_w, size_t n,
-                    int in_set, dwim_buf *xn_out) {
+                    int in_set, dwim_buf *xn_out, const dwim_weight *bf16 = nullptr, dwim_buf *bf16_out = nullptr) {
         float *o[4];
         for (int i = 0; i < count; i++) o[i] = outs[i]->data;
         StreamExtra se;
         se.in_area = in_set;
         se.rms = in_set >= 0;
         se.eps = c.eps;
-        se.rms_out = in_set >= 0 ? row_scales->data : nullptr;
+        if (bf16) {
+            se.bf16 = bf16;
+            se.bf16_x = xh->data;
+            se.bf16_out = bf16_out->data;
+        }
         DWIM_HIP(launch_mv_q4k_mfma_tokens(dev, ws, o, nullptr, count, 0, in_set >= 0 ? nullptr : x->data, n,
                                            norm_w->data, c.eps, xn_out ? xn_out->data : nullptr, nullptr, &se));
         return 0;
@@ -538,11 +544,10 @@ struct dwim_model {
                     TRY(dwim_resize(dev, ab_in, n * 2 * c.v_heads));
                     DWIM_HIP(gemm_run_bf16(dev, l.ab, ab_in->data, n, 0));
                 } else if (bh) {
-                    // (handed over: xh holds x·attn_norm, the gate rows scale
-                    // by the row scales the qkv product writes)
-                    TRY(batch_input(ws, outs, 2, l.attn_norm, n, in_set, xh));
-                    DWIM_HIP(launch_rows_bf16(dev, l.ab, ab_in->data, xh->data, n,
-                                              in_set >= 0 ? row_scales->data : nullptr));
+                    // (the gate rows in the same launch, from xh: x·attn_norm
+                    // handed over, RMS-scaled like the products, or the
+                    // normalized rows the launch makes)
+                    TRY(batch_input(ws, outs, 2, l.attn_norm, n, in_set, xh, l.ab, ab_in));
                 } else {
                     TRY(projections(ws, outs, 2, l.attn_norm, n, xh));
                     TRY(dwim_matmul(dev, ab_in, l.ab, xh));
@@ -1186,8 +1191,7 @@ extern "C" int dwim_model_synthetic(dwim_dev *dev, const dwim_qwen35_config *cfg
         if (m->buf(m->most * m->widths[i], b[i])) return 1;
     if (m->buf(m->most * c.intermediate, &m->up) || m->buf(m->most * c.intermediate, &m->gate_ffn) ||
         m->buf((c.drafter ? kMaxDrafts + 1 : 1) * c.vocab, &m->logits) || m->buf(c.hidden, &m->drafted) ||
-        m->buf(4 * c.v_heads, &m->head_ss) || m->buf(4, &m->row_scales) ||
-        m->buf(4 * c.v_heads * 8, &m->batch_hss))
+        m->buf(4 * c.v_heads, &m->head_ss) || m->buf(4 * c.v_heads * 8, &m->batch_hss))
         return 1;
     std::vector<float> table;
     rope_table(table, max_len, c.rot_dim, c.rope_theta);

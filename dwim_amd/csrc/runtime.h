@@ -181,8 +181,8 @@ constexpr int kBatchArea2 = kBatchArea + 4;
 // token: in_area >= 0, the tokens' planes are already in areas in_area + t
 // (written by the product before, per 16 or per 32 activations) and nothing
 // is made from x; rms, those planes are x·w with Σx² per group, every
-// token's results scaled by 1/sqrt(Σx²/cols + eps) (and the scales to
-// rms_out[t] when given); emit_area >= 0 (one matrix or a SwiGLU pair, rows
+// token's results scaled by 1/sqrt(Σx²/cols + eps); emit_area >= 0 (one
+// matrix or a SwiGLU pair, rows
 // whole 256-blocks), token t's planes of outs[0] (after the add or the
 // SwiGLU) go to area emit_area + t, of outs[0]·emit_norm with Σ outs[0]² per
 // group when emit_norm is given (and outs[0]·emit_norm in f32 to emit_xw,
@@ -191,12 +191,17 @@ struct StreamExtra {
     int in_area = -1;
     int rms = 0;
     float eps = 0.0f;
-    float *rms_out = nullptr;
     // given: the planes hold heads of 128 columns unnormalized (a DeltaNet
     // output gate), each scaled here by 1/sqrt(Σ head_ss[t][head][0..7] /
     // 128 + head_eps)
     const float *head_ss = nullptr;
     float head_eps = 0.0f;
+    // given: the same launch also writes bf16_out ([nt][rows]) = bf16 ·
+    // bf16_x ([nt][cols], f32), each token's results RMS-scaled with the
+    // products' (a small bf16 matrix)
+    const dwim_weight *bf16 = nullptr;
+    const float *bf16_x = nullptr;
+    float *bf16_out = nullptr;
     int emit_area = -1;
     const float *emit_norm = nullptr;
     float *emit_xw = nullptr;
@@ -225,10 +230,6 @@ hipError_t launch_mv_q6k_mfma(dwim_dev *dev, const dwim_weight *w, float *out, i
 hipError_t launch_mv_q6k_tokens(dwim_dev *dev, const dwim_weight *w, float *out, const float *x, size_t n);
 hipError_t launch_swiglu(dwim_dev *dev, const dwim_weight *gate, const dwim_weight *up, float *out,
                          float *scratch, const float *x, size_t n);
-// out ([n][rows]) = W·x for a bf16 weight of few rows and n < 16 tokens, each
-// token's results times row_scale[t] when that is given
-hipError_t launch_rows_bf16(dwim_dev *dev, const dwim_weight *wt, float *out, const float *x, size_t n,
-                           const float *row_scale);
 hipError_t launch_attention(dwim_dev *dev, float *out, const float *q, const dwim_cache *k,
                             const dwim_cache *v, size_t n, size_t pos, size_t n_heads,
                             size_t head_dim, size_t n_kv_heads);
