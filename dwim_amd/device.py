@@ -84,6 +84,12 @@ SIGNATURES = {
     "dwim_delta_net_unit_keys": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz]),
     "dwim_conv_l2norm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, ctypes.c_float]),
     "dwim_argmax": (_int, [_vp, _vp, _sz, _u32p]),
+    "dwim_sampler_open": (_int, [_vp, ctypes.c_float, _sz, ctypes.c_float, ctypes.c_float, ctypes.c_uint64,
+                                 ctypes.POINTER(_vp)]),
+    "dwim_sampler_free": (None, [_vp]),
+    "dwim_sampler_rng": (_int, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
+    "dwim_sample": (_int, [_vp, _vp, _sz, _sz, _u32p]),
+    "dwim_sample_verify": (_int, [_vp, _vp, _sz, _sz, ctypes.c_uint32, _u32p, ctypes.POINTER(ctypes.c_int)]),
     "dwim_prepare": (_int, [_vp, _vp]),
     "dwim_matmul_prepared": (_int, [_vp, _vp, _vp]),
     "dwim_swiglu_prepared": (_int, [_vp, _vp, _vp, _vp]),
@@ -262,6 +268,43 @@ class Cache:
     def __del__(self):
         if getattr(self, "h", None) and _lib is not None:
             _lib.dwim_free_cache(self.h)
+            self.h = None
+
+
+class Sampler:
+    """inference/sampler.rs's Sampler on the device (dwim_sampler_*): the
+    same settings, the same generator, picks from a row of device logits."""
+
+    def __init__(self, dev: "Hip", temperature: float, top_k: int, top_p: float, min_p: float, seed: int):
+        self.dev = dev
+        h = _vp()
+        _check(lib().dwim_sampler_open(dev.h, temperature, top_k, top_p, min_p, seed, ctypes.byref(h)))
+        self.h = h.value
+
+    @property
+    def rng(self) -> int:
+        """the generator's state"""
+        s = ctypes.c_uint64()
+        _check(lib().dwim_sampler_rng(self.h, ctypes.byref(s)))
+        return int(s.value)
+
+    def sample(self, logits: Buffer, row: int = 0, vocab: int | None = None) -> int:
+        """Sampler::sample of row `row` of logits ([rows][vocab])"""
+        vocab = len(logits) if vocab is None else vocab
+        t = ctypes.c_uint32()
+        _check(lib().dwim_sample(self.h, logits.h, row, vocab, ctypes.byref(t)))
+        return int(t.value)
+
+    def verify(self, logits: Buffer, draft: int, row: int = 0, vocab: int | None = None):
+        """Sampler::verify: (token, accepted)"""
+        vocab = len(logits) if vocab is None else vocab
+        t, a = ctypes.c_uint32(), ctypes.c_int()
+        _check(lib().dwim_sample_verify(self.h, logits.h, row, vocab, draft, ctypes.byref(t), ctypes.byref(a)))
+        return int(t.value), bool(a.value)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.dwim_sampler_free(self.h)
             self.h = None
 
 
@@ -452,6 +495,10 @@ class Hip:
         out = np.empty(rows, np.uint32)
         _check(self.L.dwim_argmax(self.h, logits.h, rows, _ptr(out, _u32p)))
         return out
+
+    def sampler(self, temperature: float, top_k: int, top_p: float, min_p: float, seed: int) -> Sampler:
+        """Sampler::new on this device"""
+        return Sampler(self, temperature, top_k, top_p, min_p, seed)
 
 
 def _hip_del(self):

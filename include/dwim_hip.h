@@ -201,6 +201,32 @@ int dwim_conv_l2norm(dwim_dev *dev, dwim_buf *q, dwim_buf *k, dwim_buf *v, dwim_
  * `rows` indices to `out` (host memory) and waits. */
 int dwim_argmax(dwim_dev *dev, const dwim_buf *logits, size_t rows, uint32_t *out);
 
+/* The token sampler on the device (inference/sampler.rs:7-146, which
+ * inference/local.rs:305-312 calls as `pick`): from the top_k most likely
+ * tokens of a row of logits, the smallest set reaching top_p, none less than
+ * min_p times as likely as the most likely, at `temperature` (0: the most
+ * likely, certain), drawn with the sampler's xorshift64* generator seeded
+ * with max(seed, 1), as Sampler::new makes it.  The generator's state stays
+ * on the device; each call reads back only its token.  A sampler holds a
+ * reference on its device.  dwim_sampler_open fails for a negative
+ * temperature, top_p <= 0 or min_p > 1 (settings that keep no token, with
+ * which the reference's sampler would fail at its first pick). */
+typedef struct dwim_sampler dwim_sampler;
+int dwim_sampler_open(dwim_dev *dev, float temperature, size_t top_k, float top_p, float min_p, uint64_t seed,
+                      dwim_sampler **out);
+void dwim_sampler_free(dwim_sampler *s);
+/* The generator's state (waits for the device). */
+int dwim_sampler_rng(dwim_sampler *s, uint64_t *rng);
+/* Sampler::sample (sampler.rs:40-51) of row `row` of `logits` ([rows][vocab]):
+ * the token to *token; waits. */
+int dwim_sample(dwim_sampler *s, const dwim_buf *logits, size_t row, size_t vocab, uint32_t *token);
+/* Sampler::verify (sampler.rs:53-81) of `draft` against row `row`: the draft
+ * kept with the probability dwim_sample would pick it, else another kept token
+ * in proportion to the rest; the token to *token, *accepted 1 when it is the
+ * draft; waits. */
+int dwim_sample_verify(dwim_sampler *s, const dwim_buf *logits, size_t row, size_t vocab, uint32_t draft,
+                       uint32_t *token, int *accepted);
+
 /* One activation vector for several Q4_K matrices: dwim_prepare converts the
  * `cols` activations of x (one token) into the device's int8 planes, which
  * dwim_matmul_prepared then multiplies by a Q4_K weight of that many columns,

@@ -95,6 +95,13 @@ def _declare(L):
         "or_conv": (None, [_f32p, _sz, _f32p, _sz, _f32p, _sz, _f32p, _f32p, _sz, _f32p, _f32p]),
         "or_delta_net": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz]),
         "or_argmax": (ctypes.c_uint32, [_f32p, _sz]),
+        "or_xorshift_next": (ctypes.c_float, [_u64p]),
+        "or_sampler_init": (None, [ctypes.c_void_p, ctypes.c_float, _sz, ctypes.c_float, ctypes.c_float,
+                                   ctypes.c_uint64]),
+        "or_sampler_candidates": (_sz, [ctypes.c_void_p, _f32p, _sz, ctypes.POINTER(ctypes.c_uint32), _f32p, _f32p]),
+        "or_sample": (ctypes.c_uint32, [ctypes.c_void_p, _f32p, _sz]),
+        "or_sampler_verify": (ctypes.c_uint32, [ctypes.c_void_p, _f32p, _sz, ctypes.c_uint32,
+                                                ctypes.POINTER(ctypes.c_int)]),
         "or_rope_table": (None, [_f32p, _sz, _sz, ctypes.c_float]),
         "or_threads": (ctypes.c_int, []),
     }
@@ -461,6 +468,54 @@ def delta_net(q, k, v, gates, decay, state, n_k_heads, n_v_heads, head_dim):
 def argmax(logits) -> int:
     x = f32(logits)
     return int(lib().or_argmax(_p(x, _f32p), x.size))
+
+
+# ---- inference/sampler.rs ----
+class _SamplerState(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", _sz), ("top_p", ctypes.c_float),
+                ("min_p", ctypes.c_float), ("rng", ctypes.c_uint64)]
+
+
+def xorshift_next(state: int):
+    """Rng::next (sampler.rs:136-146): (the value in [0, 1), the next state)."""
+    s = ctypes.c_uint64(state)
+    v = lib().or_xorshift_next(ctypes.byref(s))
+    return float(v), int(s.value)
+
+
+class Sampler:
+    """Sampler (sampler.rs:7-133): sample and verify advance the generator
+    as the reference's do."""
+
+    def __init__(self, temperature, top_k, top_p, min_p, seed):
+        self._s = _SamplerState()
+        lib().or_sampler_init(ctypes.byref(self._s), temperature, top_k, top_p, min_p, seed)
+
+    @property
+    def rng(self) -> int:
+        return int(self._s.rng)
+
+    def candidates(self, logits):
+        """(tokens, probabilities, total) of Sampler::candidates"""
+        x = f32(logits)
+        tok = np.empty(max(x.size, 1), np.uint32)
+        pr = np.empty(max(x.size, 1), np.float32)
+        tot = ctypes.c_float()
+        n = lib().or_sampler_candidates(ctypes.byref(self._s), _p(x, _f32p), x.size,
+                                        tok.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), _p(pr, _f32p),
+                                        ctypes.byref(tot))
+        return tok[:n].copy(), pr[:n].copy(), float(tot.value)
+
+    def sample(self, logits) -> int:
+        x = f32(logits)
+        return int(lib().or_sample(ctypes.byref(self._s), _p(x, _f32p), x.size))
+
+    def verify(self, logits, draft):
+        """(token, accepted) of Sampler::verify"""
+        x = f32(logits)
+        acc = ctypes.c_int()
+        t = lib().or_sampler_verify(ctypes.byref(self._s), _p(x, _f32p), x.size, int(draft), ctypes.byref(acc))
+        return int(t), bool(acc.value)
 
 
 def rope_table(max_len, rot_dim, theta):

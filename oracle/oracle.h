@@ -98,6 +98,20 @@ void or_delta_net(float *out, const float *q, const float *k, const float *v,
                   const float *gates, const float *decay, float *state, size_t n,
                   size_t n_k_heads, size_t n_v_heads, size_t head_dim);
 uint32_t or_argmax(const float *logits, size_t len);
+
+/* The token sampler (sampler.c; dwim inference/sampler.rs) */
+typedef struct {
+    float temperature;
+    size_t top_k;
+    float top_p, min_p;
+    uint64_t rng;
+} or_sampler;
+float or_xorshift_next(uint64_t *state);
+void or_sampler_init(or_sampler *s, float temperature, size_t top_k, float top_p, float min_p, uint64_t seed);
+size_t or_sampler_candidates(const or_sampler *s, const float *logits, size_t len, uint32_t *tokens, float *probs,
+                             float *total);
+uint32_t or_sample(or_sampler *s, const float *logits, size_t len);
+uint32_t or_sampler_verify(or_sampler *s, const float *logits, size_t len, uint32_t draft, int *accepted);
 void or_rope_table(float *table, size_t max_len, size_t rot_dim, float theta);
 
 int or_threads(void);
