@@ -1258,6 +1258,11 @@ extern "C" int dwim_model_verify(dwim_model *m, const uint32_t *tokens, size_t n
 
 extern "C" int dwim_model_rewind(dwim_model *m, size_t keep) { return m->rewind(keep); }
 
+extern "C" int dwim_model_logits(dwim_model *m, const dwim_buf **out) {
+    *out = m->logits;
+    return 0;
+}
+
 extern "C" int dwim_model_mark(dwim_model *m) { return m->mark(); }
 
 extern "C" int dwim_model_rewind_to_mark(dwim_model *m) { return m->rewind_to_mark(); }

@@ -246,6 +246,13 @@ class Buffer:
             self.h = None
 
 
+class BorrowedBuffer(Buffer):
+    """a buffer another object owns (freed with it, never here)"""
+
+    def __del__(self):
+        self.h = None
+
+
 class Weight:
     def __init__(self, dev: "Hip", handle: int, fmt: int, rows: int, cols: int):
         self.dev, self.h, self.fmt, self.rows, self.cols = dev, handle, fmt, rows, cols

@@ -85,13 +85,15 @@ def _declare(L):
     L.dwim_model_save.argtypes = [vp, sz, ctypes.c_void_p, sz, ctypes.POINTER(sz)]
     L.dwim_model_restore.restype = ctypes.c_int
     L.dwim_model_restore.argtypes = [vp, ctypes.c_char_p, sz, ctypes.POINTER(sz)]
+    L.dwim_model_logits.restype = ctypes.c_int
+    L.dwim_model_logits.argtypes = [vp, ctypes.POINTER(vp)]
     _sigs_done = True
 
 
 MODEL_SIGNATURES = ["dwim_model_synthetic", "dwim_model_free", "dwim_model_batch", "dwim_model_forward",
                     "dwim_model_forward_greedy", "dwim_model_decode_greedy", "dwim_model_reset", "dwim_model_draft", "dwim_model_verify",
                     "dwim_model_rewind", "dwim_model_mark", "dwim_model_rewind_to_mark", "dwim_model_add_sequence",
-                    "dwim_model_select_sequence", "dwim_model_save", "dwim_model_restore"]
+                    "dwim_model_select_sequence", "dwim_model_save", "dwim_model_restore", "dwim_model_logits"]
 
 
 class Model:
@@ -156,6 +158,13 @@ class Model:
 
     def rewind(self, keep: int):
         D._check(self.L.dwim_model_rewind(self.h, keep))
+
+    def logits_buffer(self) -> "D.Buffer":
+        """the model's logits on the device, as its last forward or verify left
+        them (a view: the buffer stays the model's)"""
+        h = ctypes.c_void_p()
+        D._check(self.L.dwim_model_logits(self.h, ctypes.byref(h)))
+        return D.BorrowedBuffer(self.dev, h.value)
 
     def mark(self) -> bool:
         D._check(self.L.dwim_model_mark(self.h))

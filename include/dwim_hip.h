@@ -308,6 +308,13 @@ int dwim_model_verify(dwim_model *m, const uint32_t *tokens, size_t n, size_t po
 /* LanguageModel::rewind (qwen35/mod.rs:1099-1169): commits the first `keep`
  * (1..=n) tokens of the batch being verified. */
 int dwim_model_rewind(dwim_model *m, size_t keep);
+/* The model's logits on the device, as its last dwim_model_forward (the row
+ * after the last token, also when its `logits` was NULL) or
+ * dwim_model_verify (a row after every token) left them: the rows a
+ * dwim_sampler picks from (inference/local.rs:305-312) without reading them
+ * back.  The buffer stays the model's (not to be freed) and holds them until
+ * the model's next call. */
+int dwim_model_logits(dwim_model *m, const dwim_buf **out);
 /* LanguageModel::mark / rewind_to_mark (qwen35/mod.rs:1176-1228): copies the
  * running sequence's linear-layer states aside on the device, and back; the
  * one mark belongs to the sequence that made it (error from another). */

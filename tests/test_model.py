@@ -391,3 +391,67 @@ def test_device_fed_decode_is_greedy_decode(shape):
         dev.decode_greedy(cfg.vocab + 10**6, 30, 1)  # past the table
     host.close()
     dev.close()
+
+
+def _sampled(m, prompt, decode, k, ref_settings, gpu):
+    """Local::step / Local::pick (inference/local.rs:299-368) with the
+    device sampler picking from the model's device logits: after the prompt
+    a pick from the last row; then, token by token, drafts verified as one
+    batch, each row's draft checked (Sampler::verify) until one is replaced,
+    the batch rewound to the tokens kept.  Every pick and acceptance is also
+    made by the oracle's sampler on the same logits read back, and must agree."""
+    dev_s = gpu.sampler(*ref_settings)
+    ref_s = O.Sampler(*ref_settings)
+    vocab = m.cfg.vocab
+    m.forward(prompt, 0, want_logits=False)
+    buf = m.logits_buffer()
+    row = gpu.read(buf)[:vocab]
+    token = dev_s.sample(buf, 0, vocab)
+    assert token == ref_s.sample(row)
+    out, pos, accepted = [], len(prompt), 0
+    while len(out) < decode:
+        out.append(token)
+        drafts = m.draft(token, pos, k)
+        if not drafts:
+            m.forward([token], pos, want_logits=False)
+            buf = m.logits_buffer()
+            token, want = dev_s.sample(buf, 0, vocab), ref_s.sample(gpu.read(buf)[:vocab])
+            assert token == want
+            pos += 1
+            continue
+        batch = [token] + drafts
+        m.verify(batch, pos, want_logits=False)
+        buf = m.logits_buffer()
+        rows = gpu.read(buf)[:len(batch) * vocab].reshape(len(batch), vocab)
+        keep = 1
+        for i in range(len(batch)):
+            if i < len(drafts):
+                got = dev_s.verify(buf, drafts[i], i, vocab)
+                assert got == ref_s.verify(rows[i], drafts[i])
+                token, ok = got
+                if not ok:
+                    break
+                out.append(token)
+                accepted += 1
+                keep += 1
+            else:
+                token = dev_s.sample(buf, i, vocab)
+                assert token == ref_s.sample(rows[i])
+        m.rewind(keep)
+        pos += keep
+    assert dev_s.rng == ref_s.rng
+    return out[:decode], accepted
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("settings", [(1.0, 20, 0.95, 0.05, 17), (0.3, 5, 1.0, 0.0, 3), (0.0, 20, 0.95, 0.05, 1)])
+def test_speculative_sampling_with_the_device_sampler(settings):
+    cfg = _tiny()
+    gpu = D.Hip(0)
+    prompt = [5, 9, 33, 1, 60, 12, 7, 2]
+    out, accepted = _sampled(M.Model(gpu, cfg, SEED + 2, max_len=96), prompt, 30, 3, settings, gpu)
+    print(f"sampled: {accepted} drafts accepted")
+    assert len(out) == 30
+    if settings[0] == 0.0:
+        # at temperature zero sampling is greedy decoding
+        assert out == _greedy(M.Model(gpu, cfg, SEED + 2, max_len=96), prompt, 30)
