@@ -474,8 +474,9 @@ __global__ void __launch_bounds__(kMThreads, 2) k_attn_mfma(float *__restrict__ 
         if (next) load_keys(pn, count(pn));
         __syncthreads();
         // ---- softmax numerators with a running max and sum: wave w takes
-        // rows w, w + 4, ..., a lane per position
-        for (int r = wave; r < NR; r += kMThreads / 64) {
+        // rows w, w + 4, ..., a lane per position (the padding rows past R
+        // are never written out, and their products stay in their own rows)
+        for (int r = wave; r < R; r += kMThreads / 64) {
             const float x = p_s[r * kPStride + lane];
             const float mo = m_s[r];
             const float mn = fmaxf(mo, group_max<64>(x));
@@ -963,7 +964,8 @@ hipError_t attention_reserve(dwim_dev *dev, size_t floats) {
 
 namespace {
 
-constexpr size_t kMBlocks = 512;  // blocks the matrix-core pass aims for
+// the matrix-core pass's blocks resident at once on a CU (its launch bounds)
+constexpr size_t kMPerCU = 2;
 // one token over at most this many positions: the one-chunk VALU pass, a
 // single round of blocks (4k positions: 14.1 against 14.2 us with the merge;
 // 32k: 47.8 against 31.2)
@@ -1012,11 +1014,15 @@ hipError_t attention_run(dwim_dev *dev, float *partials, float *out, const float
     }
     const size_t len = pos + n;
     if (head_dim == (size_t)kFD && (n > 1 || len > kValuLen)) {
-        // the matrix-core pass: a run of 64-position steps a block, as many
-        // as leave about two blocks a CU
+        // the matrix-core pass: a run of 64-position steps a block, as few as
+        // keep every block resident at once (two a CU): a second round of a
+        // few blocks costs a whole block's time (32k + 1 positions: 412 blocks
+        // of 5 steps, not 516 of 4; in the model 43.3 against 47.5 us a
+        // 4-token pass, 9.4 against 10.9 us its merge)
         const int G = (int)(n_heads / n_kv_heads), T = n > 1 ? kTok : 1;
         const size_t groups = (n + T - 1) / T, base = (len + kMStep - 1) / kMStep * n_kv_heads * groups;
-        const size_t ch = kMStep * std::max<size_t>(1, base / kMBlocks), chunks = (len + ch - 1) / ch;
+        const size_t slots = kMPerCU * (size_t)dev->cus;
+        const size_t ch = kMStep * std::max<size_t>(1, (base + slots - 1) / slots), chunks = (len + ch - 1) / ch;
         Shape sh{n, pos, n_heads, head_dim, n_kv_heads, ch, chunks};
         dim3 g1((unsigned)chunks, (unsigned)n_kv_heads, (unsigned)groups);
         hipError_t e = T * G <= 16 ? (k->f16 ? mfma_pass<1, true>(dev, g1, partials, q, k, v, sh, G, T)
