@@ -181,8 +181,8 @@ __global__ void __launch_bounds__(512) k_mv_q6k_mfma(const Q6Args a) {
 // A column's three int32 sums combine in f32 (C0 + 256·C1 + 65536·C2), are
 // scaled by the token's activation scale of the column's group and by the
 // row's d·sc, and the four k-groups of a token meet by row rotations.  The
-// loads are the one-token kernel's: every one issued before any compute, the
-// planes and statistics of the wave's blocks for every token first.
+// weight loads are the one-token kernel's, every one issued before any
+// compute, after the copies of the planes (below).
 constexpr int kMaxTok6 = 4;
 
 struct Q6TArgs {
@@ -191,28 +191,32 @@ struct Q6TArgs {
     const uint16_t *d;
     float *out;              // [NT][rows]
     unsigned rows, nb, S;
+    unsigned tw;                    // tiles a workgroup
     const int8_t *xq[kMaxTok6];     // each token's planes [3][cols] (groups of 16)
     const float4 *xstat[kMaxTok6];  // [cols/64][2]
 };
 
-// Per wave LDS, in 16-byte chunks: the planes [block][digit][group][token]
-// (so that the 16 B lanes of an MFMA read 16 distinct chunks), the statistics
-// [block][token][8] (chunks 2k, 2k + 1: scales and sums of groups 4k..4k+3),
-// a zero chunk and the decoded d·sc ([group][row] floats, rows of 20), whose
-// area also takes the spare loads' stores before it is written.
+// A workgroup takes tw tiles (2 when S ≤ 4) of S waves each; wave w takes
+// range w % S of the blocks of tile w / S, and the tw waves of a range share
+// its planes, copied straight from global memory into LDS (global_load_lds,
+// no registers).  That halves the LDS and drops the staging registers of a
+// wave, so that twice as many waves stream weights at once (2 workgroups of
+// 8 waves a CU at the 27B head's 20 blocks a row, against 8 waves of 4).
+//
+// LDS, in 16-byte chunks: per range, its planes [block][digit][group][token]
+// (so that the 16 B lanes of an MFMA read 16 distinct chunks), then its
+// statistics [block][token][8] (chunks 2k, 2k + 1: scales and sums of groups
+// 4k..4k+3); per wave, the decoded d·sc ([group][row] floats), then a zero
+// chunk.
 template <int NT>
 struct Lds6T {
     static constexpr int kPlaneChunks = kK * 48 * NT;
-    static constexpr int kPlaneLoads = (kPlaneChunks + 63) / 64;
     static constexpr int kStatChunks = kK * 8 * NT;
-    static constexpr int kStatLoads = (kStatChunks + 63) / 64;
-    static constexpr int kStat = kPlaneChunks;
-    static constexpr int kZero = kStat + kStatChunks;
-    static constexpr int kHdr = kZero + 1;
-    static constexpr int kHdrStride = 20;
-    static constexpr int kChunks = kHdr + 16 * kHdrStride / 4;
-    static_assert(16 * kHdrStride / 4 >= 64, "the spare loads land in the header area");
-    static_assert(16 * kHdrStride >= 2 * NT * 16, "the sums of a wave fit its header area");
+    static constexpr int kRange = kPlaneChunks + kStatChunks;
+    static constexpr int kHdrFloats = 16 * 16;
+    static constexpr int kWave = kHdrFloats / 4 + 1;
+    static_assert(kHdrFloats >= 2 * NT * 16, "the sums of a wave fit its header area");
+    static constexpr size_t bytes(unsigned S, unsigned tw) { return ((size_t)S * kRange + (size_t)tw * S * kWave) * 16; }
 };
 
 // the group of 16 a k-group x of an MFMA takes in run u (the lanes' layout above)
@@ -221,38 +225,43 @@ DEV int q6_group(int x, int u) { return 8 * (x >> 1) + (x & 1) + 2 * u; }
 template <int NT>
 __global__ void __launch_bounds__(512) k_mv_q6k_tokens(const Q6TArgs a) {
     using L = Lds6T<NT>;
-    typedef unsigned v4u6 __attribute__((ext_vector_type(4)));
     extern __shared__ uint4 lds_all[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kq = lane >> 4, c = lane & 15;
-    const unsigned S = a.S, nb = a.nb, tile = blockIdx.x;
-    const unsigned b0 = wave * nb / S, b1 = (wave + 1) * nb / S;
+    const unsigned S = a.S, nb = a.nb, tw = a.tw;
+    const unsigned rg = (unsigned)wave % S, sub = (unsigned)wave / S, tile = blockIdx.x * tw + sub;
+    const unsigned b0 = rg * nb / S, b1 = (rg + 1) * nb / S;
     const int nblk = (int)(b1 - b0);
-    uint4 *my = lds_all + wave * L::kChunks;
-    float *hdr = (float *)(my + L::kHdr);
+    uint4 *range = lds_all + rg * L::kRange;
+    uint4 *mine = lds_all + S * L::kRange + wave * L::kWave;
+    float *hdr = (float *)mine;
+    const uint4 *zero = mine + L::kHdrFloats / 4;
     const unsigned cols = nb * 256;
 
-    // planes and statistics of the wave's blocks, every token; loads past
-    // them reload chunk 0 (no branch around a load)
-    v4u6 xc[L::kPlaneLoads], xs[L::kStatLoads];
-#pragma unroll
-    for (int u = 0; u < L::kPlaneLoads; u++) {
-        const int ci0 = lane + 64 * u, ci = ci0 < nblk * 48 * NT ? ci0 : 0;
-        const int g = ci % 16, p = (ci / 16) % 3, t = (ci / 48) % NT, i = ci / (48 * NT);
-        const int8_t *src = t == 0 ? a.xq[0] : t == 1 ? a.xq[1] : t == 2 ? a.xq[2] : a.xq[3];
-        xc[u] = *(const v4u6 *)(src + p * cols + (b0 + i) * 256u + 16u * g);
-    }
-#pragma unroll
-    for (int u = 0; u < L::kStatLoads; u++) {
-        const int ci0 = lane + 64 * u, ci = ci0 < nblk * 8 * NT ? ci0 : 0;
-        const int j = ci % 8, t = (ci / 8) % NT, i = ci / (8 * NT);
-        const float4 *src = t == 0 ? a.xstat[0] : t == 1 ? a.xstat[1] : t == 2 ? a.xstat[2] : a.xstat[3];
-        xs[u] = *(const v4u6 *)&src[(b0 + i) * 8u + j];
+    // the range's planes and statistics, its copies split over the tw waves
+    // that share them (lane l of copy u writes chunk 64u + l)
+    {
+        const int np = nblk * 48 * NT, ns = nblk * 8 * NT;
+        for (int u = (int)sub; 64 * u < np; u += (int)tw) {
+            const int d = 64 * u + lane;
+            if (d < np) {
+                const int t = d % NT, g = (d / NT) % 16, p = (d / (NT * 16)) % 3, i = d / (NT * 48);
+                const int8_t *src = t == 0 ? a.xq[0] : t == 1 ? a.xq[1] : t == 2 ? a.xq[2] : a.xq[3];
+                lds_copy16((const uint8_t *)(src + p * cols + (b0 + i) * 256u + 16u * g), (uint8_t *)(range + 64 * u));
+            }
+        }
+        for (int u = (int)sub; 64 * u < ns; u += (int)tw) {
+            const int d = 64 * u + lane;
+            if (d < ns) {
+                const int j = d % 8, t = (d / 8) % NT, i = d / (8 * NT);
+                const float4 *src = t == 0 ? a.xstat[0] : t == 1 ? a.xstat[1] : t == 2 ? a.xstat[2] : a.xstat[3];
+                lds_copy16((const uint8_t *)&src[(b0 + i) * 8u + j], (uint8_t *)(range + L::kPlaneChunks + 64 * u));
+            }
+        }
     }
     const unsigned row = tile * 16 + (unsigned)c, row_c = row < a.rows ? row : a.rows - 1;
     const unsigned n = (unsigned)kq >> 1, lb = 16u * ((unsigned)kq & 1u);
     const int k4 = lane & 3, R4 = lane >> 2;
     const unsigned hrow = tile * 16 + (unsigned)R4, hrow_c = hrow < a.rows ? hrow : a.rows - 1;
-    asm volatile("");
     uint4 ql[kK][2], qh[kK];
     uint32_t scw[kK];
     uint16_t dw[kK];
@@ -267,28 +276,17 @@ __global__ void __launch_bounds__(512) k_mv_q6k_tokens(const Q6TArgs a) {
         scw[i] = *(const uint32_t *)(a.sc + hblk * 16 + 4 * k4);
         dw[i] = a.d[hblk];
     }
-    // every load's chunk is stored, the spare ones into the header area
-#pragma unroll
-    for (int u = 0; u < L::kPlaneLoads; u++) {
-        const int ci0 = lane + 64 * u;
-        const int g = ci0 % 16, p = (ci0 / 16) % 3, t = (ci0 / 48) % NT, i = ci0 / (48 * NT);
-        const int dst = ci0 < nblk * 48 * NT ? ((i * 3 + p) * 16 + g) * NT + t : L::kHdr + lane;
-        ((v4u6 *)my)[dst] = xc[u];
-    }
-#pragma unroll
-    for (int u = 0; u < L::kStatLoads; u++) {
-        const int ci0 = lane + 64 * u;
-        ((v4u6 *)my)[ci0 < nblk * 8 * NT ? L::kStat + ci0 : L::kHdr + lane] = xs[u];
-    }
-    if (lane == 0) my[L::kZero] = make_uint4(0, 0, 0, 0);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (lane == 0) mine[L::kHdrFloats / 4] = make_uint4(0, 0, 0, 0);
+    // the copies land in LDS when the wave's loads are done; then every
+    // wave's are
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
 
     // B lane (kq, c): token c % 4 of k-group kq when c / 4 == kq; output
     // lane (kq, c): rows 4kq.., column group gq = c / 4, token tc = c % 4
     const int tb = c & 3, gq = c >> 2;
     const bool active = gq == kq && tb < NT;
-    const float *stf = (const float *)(my + L::kStat);
+    const float *stf = (const float *)(range + L::kPlaneChunks);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, macc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) macc[t] = 0.0f;
@@ -306,10 +304,10 @@ __global__ void __launch_bounds__(512) k_mv_q6k_tokens(const Q6TArgs a) {
                 const float4 xm = *(const float4 *)&stf[((i * NT + t) * 8 + 2 * k4 + 1) * 4];
                 macc[t] -= 32.0f * ((s0 * xm.x + s1 * xm.y) + (s2 * xm.z + s3 * xm.w));
             }
-            hdr[(4 * k4) * L::kHdrStride + R4] = s0;
-            hdr[(4 * k4 + 1) * L::kHdrStride + R4] = s1;
-            hdr[(4 * k4 + 2) * L::kHdrStride + R4] = s2;
-            hdr[(4 * k4 + 3) * L::kHdrStride + R4] = s3;
+            hdr[(4 * k4) * 16 + R4] = s0;
+            hdr[(4 * k4 + 1) * 16 + R4] = s1;
+            hdr[(4 * k4 + 2) * 16 + R4] = s2;
+            hdr[(4 * k4 + 3) * 16 + R4] = s3;
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -326,13 +324,13 @@ __global__ void __launch_bounds__(512) k_mv_q6k_tokens(const Q6TArgs a) {
             v4i6 C[3];
 #pragma unroll
             for (int p = 0; p < 3; p++) {
-                const uint4 xq = my[active ? ((i * 3 + p) * 16 + gb) * NT + tb : L::kZero];
+                const uint4 xq = *(active ? range + ((i * 3 + p) * 16 + gb) * NT + tb : zero);
                 const v4i6 bv = {(int)xq.x, (int)xq.y, (int)xq.z, (int)xq.w};
                 C[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, v4i6{0, 0, 0, 0}, 0, 0, 0);
             }
             // the column's activation scale (zero for the columns past NT)
             const float sx = tb < NT ? stf[((i * NT + tb) * 8 + 2 * (go >> 2)) * 4 + (go & 3)] : 0.0f;
-            const float4 D = *(const float4 *)&hdr[go * L::kHdrStride + 4 * kq];
+            const float4 D = *(const float4 *)&hdr[go * 16 + 4 * kq];
             const float Dv[4] = {D.x, D.y, D.z, D.w};
 #pragma unroll
             for (int e = 0; e < 4; e++)
@@ -359,11 +357,11 @@ __global__ void __launch_bounds__(512) k_mv_q6k_tokens(const Q6TArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; t++) red[(NT + t) * 16 + R4] = macc[t];
     __syncthreads();
-    if (wave != 0 || lane >= 16 * NT) return;
+    if (rg != 0 || lane >= 16 * NT) return;
     const int t = lane >> 4, rl = lane & 15;
     float v = 0.0f;
     for (unsigned w = 0; w < S; w++) {
-        const float *rw = (const float *)(lds_all + w * L::kChunks + L::kHdr);
+        const float *rw = (const float *)(lds_all + S * L::kRange + (sub * S + w) * L::kWave);
         v += rw[t * 16 + rl] + rw[(NT + t) * 16 + rl];
     }
     const unsigned r = tile * 16 + (unsigned)rl;
@@ -371,14 +369,17 @@ __global__ void __launch_bounds__(512) k_mv_q6k_tokens(const Q6TArgs a) {
 }
 
 template <int NT>
-hipError_t go_tokens(dwim_dev *dev, const Q6TArgs &a, unsigned tiles) {
-    const size_t lds = (size_t)a.S * Lds6T<NT>::kChunks * 16;
-    // the attribute holds for the process, raised once (a function-local
-    // static is initialized once even when host threads reach it together)
-    static const hipError_t raised = hipFuncSetAttribute(
-        (const void *)k_mv_q6k_tokens<NT>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(8 * Lds6T<NT>::kChunks * 16));
+hipError_t go_tokens(dwim_dev *dev, Q6TArgs a, unsigned tiles) {
+    using L = Lds6T<NT>;
+    a.tw = a.S <= 4 ? 2 : 1;
+    // the attribute holds for the process, raised once to the most a launch
+    // takes (a function-local static is initialized once even when host
+    // threads reach it together)
+    static const hipError_t raised =
+        hipFuncSetAttribute((const void *)k_mv_q6k_tokens<NT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)std::max(L::bytes(8, 1), L::bytes(4, 2)));
     if (raised != hipSuccess) return raised;
-    k_mv_q6k_tokens<NT><<<tiles, a.S * 64, lds, dev->stream>>>(a);
+    k_mv_q6k_tokens<NT><<<(tiles + a.tw - 1) / a.tw, a.tw * a.S * 64, L::bytes(a.S, a.tw), dev->stream>>>(a);
     return hipGetLastError();
 }
 

@@ -159,8 +159,10 @@ def test_q6_k_matmul_matches_cpu(gpu):
 
 def test_q6_k_few_tokens_match_cpu(gpu):
     # a verify batch through the head: runs of up to four tokens sharing the
-    # weight loads (2, 3, 4, then 5 = 3 + 2 and 7 = 4 + 3), 8 waves a tile at 10240
-    shapes = [(4000, 5120, 4), (1000, 10240, 3), (33, 256, 2), (517, 2048, 5), (64, 4608, 7)]
+    # weight loads (2, 3, 4, then 5 = 3 + 2 and 7 = 4 + 3), 8 waves a tile at 10240,
+    # two tiles a workgroup up to 4 waves a tile (an odd tile count: the second
+    # tile of the last workgroup past the rows)
+    shapes = [(4000, 5120, 4), (4008, 5120, 3), (1000, 10240, 3), (33, 256, 2), (517, 2048, 5), (64, 4608, 7)]
     block_matmul_matches_cpu(gpu, _k_quantized(O.Q6_K, 47), shapes)
 
 
